@@ -1,0 +1,243 @@
+#!/usr/bin/env python3
+"""Benchmark of the HeadStartLSTM training hot path on one MI355X.
+
+Workload (the headline): recurrent mode, fp32,
+T=256 B=32 D=256 H=512, a=1e-4, x ~ N(0,1), nn.LSTM init, h0=c0=0,
+loss = out.sum(); one step = forward + backward (all parameter gradients and
+dx), captured whole in one HIP graph and replayed.  Synthetic data, seeded.
+
+Prints ONE JSON line:
+  value       timesteps*batch/s = T*B / step time
+  roofline    the dominant kernel of the step (persistent recurrent kernel),
+              algorithmic fp32 MFMA FLOPs per launch / its mean launch time,
+              timed with HIP events on its launch stream
+  cpu_baseline the CPU restatement of the reference torch backend (oracle/),
+              same workload, timed on this host's cores
+  scan        configs[4] parallel scan (T=4096 B=16 H=1024) forward and
+              backward kernels: algorithmic HBM bytes / launch time
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+
+MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+METRIC = "fwd+bwd ms/step & timesteps·batch/s at T256 B32 D256 H512; scan HBM GB/s"
+T, B, D, H = 256, 32, 256, 512
+ST, SB, SD, SH = 4096, 16, 256, 1024
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_inputs():
+    """configs[2] synthetic inputs (SURVEY 8(d) recipe): seed 0, module on CPU, then x."""
+    from prlstm_amd import HeadStartLSTM
+    torch.manual_seed(0)
+    m = HeadStartLSTM(D, H, a_init=1e-4)
+    x = torch.randn(T, B, D)
+    return m, x
+
+
+def bench_gpu(args):
+    from prlstm_amd import _lib
+    from prlstm_amd.graph import GraphedTrainStep
+    dev = torch.device("cuda", 0)
+    m_cpu, x_cpu = make_inputs()
+    m = m_cpu.to(dev)
+    x = x_cpu.to(dev)
+    step = GraphedTrainStep(m, x)
+    for _ in range(args.warmup):
+        step.step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step.step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - w0) * 1e3 / args.steps
+    ms = e0.elapsed_time(e1) / args.steps
+    path = _lib.last_recurrent_path()
+
+    # per-kernel launch times: the same step run eagerly with the library's event hooks
+    _lib.set_timing(True)
+    for k in ("rec_fwd", "rec_bwd", "input_proj", "step_fwd", "step_bwd"):
+        _lib.timing_collect(k)
+    for _ in range(args.steps):
+        m.zero_grad(set_to_none=True)
+        out, _ = m(x)
+        out.sum().backward()
+    torch.cuda.synchronize()
+    kern = {}
+    for k in ("rec_fwd", "rec_bwd", "input_proj", "step_fwd", "step_bwd"):
+        tot, n = _lib.timing_collect(k)
+        if n:
+            kern[k] = tot / n
+    _lib.set_timing(False)
+    log(f"graph step {ms:.4f} ms (wall {wall_ms:.4f} ms), path {path}, kernels(ms) {kern}")
+    return ms, wall_ms, kern, path
+
+
+def bench_scan(args):
+    from prlstm_amd import _lib, HeadStartLSTM
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    m = HeadStartLSTM(SD, SH, a_init=0.0)
+    x = torch.randn(ST, SB, SD, device=dev)
+    w_ih = m.weight_ih_l0.detach().to(dev)
+    b_ih = m.bias_ih_l0.detach().to(dev)
+    c0 = torch.zeros(SB, SH, device=dev)
+    gates = torch.empty(ST, SB, 4 * SH, device=dev)
+    out = torch.empty(ST, SB, SH, device=dev)
+    c_seq = torch.empty(ST, SB, SH, device=dev)
+    dout = torch.randn(ST, SB, SH, device=dev)
+    dh_n = torch.zeros(SB, SH, device=dev)
+    dc_n = torch.zeros(SB, SH, device=dev)
+    dgates = torch.empty(ST, SB, 4 * SH, device=dev)
+    db_part = torch.empty(SB, 4 * SH, dtype=torch.float64, device=dev)
+    P, s = _lib.ptr, _lib.stream_of(dev)
+    _lib.call("hsl_par_fwd", P(x), P(c0), P(w_ih), P(b_ih), 1e-6, P(gates), P(out), P(c_seq),
+              ST, SB, SD, SH, s)
+    reps = max(3, args.steps // 2)
+    for warm in (True, False):
+        if not warm:
+            _lib.set_timing(True)
+            _lib.timing_collect("scan_fwd")
+            _lib.timing_collect("scan_bwd")
+        for _ in range(1 if warm else reps):
+            _lib.call("hsl_scan_fwd", P(gates), P(c0), 1e-6, P(out), P(c_seq), ST, SB, SH, s)
+            _lib.call("hsl_scan_bwd", P(gates), P(c0), P(c_seq), P(dout), P(dh_n), P(dc_n), 1e-6,
+                      P(dgates), P(db_part), None, ST, SB, SH, s)
+    torch.cuda.synchronize()
+    tf, nf = _lib.timing_collect("scan_fwd")
+    tb, nb = _lib.timing_collect("scan_bwd")
+    _lib.set_timing(False)
+    fwd_ms, bwd_ms = tf / nf, tb / nb
+    n = ST * SB * SH
+    fwd_b, bwd_b = 24 * n, 40 * n
+    res = {
+        "config": {"workload": "parallel scan fwd+bwd kernels, configs[4]", "T": ST, "B": SB, "H": SH},
+        "fwd_ms": round(fwd_ms, 5), "bwd_ms": round(bwd_ms, 5),
+        "fwd_GBps": round(fwd_b / fwd_ms / 1e6, 1), "bwd_GBps": round(bwd_b / bwd_ms / 1e6, 1),
+        "GBps": round((fwd_b + bwd_b) / (fwd_ms + bwd_ms) / 1e6, 1),
+        "roofline": {"bound": "hbm", "achieved": round((fwd_b + bwd_b) / (fwd_ms + bwd_ms) / 1e6, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round((fwd_b + bwd_b) / (fwd_ms + bwd_ms) / 1e6 / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+    }
+    log(f"scan fwd {fwd_ms:.4f} ms ({res['fwd_GBps']} GB/s) bwd {bwd_ms:.4f} ms ({res['bwd_GBps']} GB/s)")
+    return res
+
+
+def bench_cpu(args):
+    """The reference torch backend restated (oracle/), fp32 on this host's cores."""
+    from oracle.hsl_oracle import RefHeadStartLSTM
+    cores = len(os.sched_getaffinity(0))
+    cores = min(cores, args.cpu_threads) if args.cpu_threads else cores
+    torch.set_num_threads(cores)
+    torch.manual_seed(0)
+    m = RefHeadStartLSTM(D, H, a_init=1e-4)
+    x = torch.randn(T, B, D)
+
+    def one():
+        m.zero_grad(set_to_none=True)
+        t0 = time.perf_counter()
+        out, _ = m(x)
+        out.sum().backward()
+        return time.perf_counter() - t0
+
+    first = one()  # warm-up
+    times = []
+    budget = args.cpu_seconds
+    spent = first
+    while (len(times) < 1 or spent + statistics.median(times) <= budget) and len(times) < 15:
+        times.append(one())
+        spent += times[-1]
+    med = statistics.median(times)
+    log(f"cpu baseline: {cores} threads, median {med:.3f} s over {len(times)} steps (warm-up {first:.3f} s)")
+    return {"value": round(T * B / med, 1), "unit": "timesteps·batch/s", "cores": cores,
+            "kind": "port", "ms_per_step": round(med * 1e3, 2),
+            "sample": f"configs[2] fwd+bwd (out.sum() loss), fp32, torch CPU restatement of "
+                      f"_torch.py, median of {len(times)} full steps after 1 warm-up"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0,
+                    help="bound on the CPU baseline sample (seconds of CPU work)")
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-scan", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(each box has one MI355X); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+
+    ms, wall_ms, kern, path = bench_gpu(args)
+    scan = None if args.no_scan else bench_scan(args)
+    cpu = None if args.no_cpu else bench_cpu(args)
+
+    step_flops = 24.0 * T * B * H * (D + H)           # algorithmic fwd+bwd FLOPs
+    rec_flops = 2.0 * T * B * H * 4 * H               # recurrent product of one direction
+    if "rec_fwd" in kern or "rec_bwd" in kern:
+        name = max((k for k in ("rec_fwd", "rec_bwd") if k in kern), key=lambda k: kern[k])
+        kname = {"rec_fwd": "rec_fwd_persistent", "rec_bwd": "rec_bwd_persistent"}[name]
+    else:
+        name = max((k for k in ("step_fwd", "step_bwd") if k in kern), key=lambda k: kern[k])
+        kname = name + " (per-step launches)"
+    kms = kern[name]
+    achieved = rec_flops / (kms * 1e-3) / 1e12
+    value = T * B / (ms * 1e-3)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "timesteps·batch/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "HeadStartLSTM recurrent fwd+bwd (configs[2]), one hipGraph replay per step",
+                   "T": T, "B": B, "D": D, "H": H, "a": 1e-4, "loss": "out.sum()",
+                   "recurrent_path": {1: "per-step", 2: "persistent"}.get(path, path)},
+        "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(achieved, 3),
+                     "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel_ms": round(kms, 5), "flops_per_launch": rec_flops},
+        "step_tflops": round(step_flops / (ms * 1e-3) / 1e12, 3),
+        "kernels_ms": {k: round(v, 5) for k, v in kern.items()},
+        "wall_ms_per_step": round(wall_ms, 5),
+        "scan": scan,
+        "cpu_baseline": cpu,
+    }
+    if cpu:
+        line["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,167 @@
+/*
+ * hsl.h -- C ABI of the HeadStartLSTM training hot path on MI355X (gfx950).
+ *
+ * HeadStartLSTM is a one-layer LSTM with sigmoid g-gate and a learnable
+ * per-gate scale a[4] on the recurrent term:
+ *   z_t = x_t W_ih^T + b_ih + a (.) (h_{t-1} W_hh^T + b_hh)      gate order [i,f,g,o]
+ *   i,f,g,o = sigmoid(z_t);  c_t = f c_{t-1} + i g;  h_t = o tanh(c_t)
+ * Parallel mode drops the a-term and solves c_t = f c_{t-1} + i g as a scan.
+ *
+ * Conventions for every entry point:
+ *  - all tensor pointers are device memory, fp32, contiguous row-major, caller
+ *    allocated; shapes are given by T (time), B (batch), D (input), H (hidden);
+ *  - the last argument is the HIP stream (hipStream_t passed as void*; NULL is
+ *    the null stream); work is only enqueued, nothing is synchronised, and no
+ *    device memory is allocated, so every call can be captured in a hipGraph;
+ *  - the return value is HSL_OK (0) or an HSL_ERR_* code; hsl_last_error()
+ *    then returns a message (per host thread);
+ *  - scratch memory is passed in as (ws, ws_bytes); the needed size is given by
+ *    the matching *_ws_bytes() query.  Calls that share one workspace on
+ *    different streams at the same time race.
+ *
+ * Each entry point names the reference code it replaces
+ * (m-j-tilley/prLSTM, src/headstartlstm/...).
+ */
+#ifndef HSL_H
+#define HSL_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HSL_ABI_VERSION 1
+
+enum hsl_status {
+  HSL_OK = 0,
+  HSL_ERR_ARG = 1,          /* bad shape / null pointer / workspace too small */
+  HSL_ERR_UNSUPPORTED = 2,  /* shape outside what the kernels handle          */
+  HSL_ERR_HIP = 3,          /* a HIP runtime call failed                       */
+  HSL_ERR_DEVICE = 4        /* a kernel reported an error (see hsl_poll_error) */
+};
+
+/* Library identity and error text.  (No reference counterpart.) */
+int hsl_abi_version(void);
+const char* hsl_last_error(void);
+
+/* Recurrent-path selection: 0 = automatic (persistent kernels where the shape
+ * fits on chip, else one launch per time step), 1 = always per-step,
+ * 2 = persistent only (HSL_ERR_UNSUPPORTED if it does not fit).  Returns the
+ * previous value.  Process-wide. */
+int hsl_set_recurrent_path(int mode);
+/* Bound, in microseconds, on any wait a persistent kernel does for another
+ * workgroup (default 2,000,000).  On expiry the kernel stops and raises the
+ * device error flag instead of waiting forever.  Returns the previous value. */
+long long hsl_set_spin_timeout_us(long long us);
+/* Which path the last hsl_rec_fwd / hsl_rec_bwd on this host thread used:
+ * 1 = per-step, 2 = persistent. */
+int hsl_last_recurrent_path(void);
+/* Measurement hook (no reference counterpart): with timing on, the library
+ * records a pair of HIP events on the launch stream around each launch of the
+ * persistent recurrent kernels (kind 1 forward, 2 backward), the scan kernels
+ * (3 forward, 4 backward), the input projection (5) and the per-step loops
+ * (6 forward, 7 backward).  hsl_timing_collect waits for and sums the recorded
+ * pairs of one kind (milliseconds) and forgets them.  Not for graph capture. */
+int hsl_set_timing(int on);
+int hsl_timing_collect(int kind, double* total_ms, int* count);
+/* Copy the device error flag kept at the start of a recurrent workspace into
+ * *flag (synchronises `stream`); nonzero means a persistent wait timed out. */
+int hsl_poll_error(const void* ws, int* flag, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Recurrent mode: replaces HeadStartLSTMTorchFn (_torch.py:86-170).
+ * ------------------------------------------------------------------------- */
+
+/* Workspace for hsl_rec_fwd: input-gate buffer [T,B,4H], exchange buffers. */
+size_t hsl_rec_fwd_ws_bytes(int T, int B, int D, int H);
+
+/* Forward: _torch.py:86-131 (a-prescale :91-94, input GEMM :96, time loop
+ * :111-120).  Writes
+ *   h_save [T+1,B,H]   h_save[0] = h0, h_save[t+1] = h_t  (output = h_save[1:])
+ *   c_save [T+1,B,H]   c_save[0] = c0, c_save[t+1] = c_t
+ *   gact   [T,B,4H]    sigmoid gate activations [i|f|g|o]
+ *   tanh_c [T,B,H]     tanh(c_t)
+ * gact and tanh_c are what hsl_rec_bwd reads back. */
+int hsl_rec_fwd(const float* x, const float* h0, const float* c0,
+                const float* w_ih, const float* w_hh, const float* b_ih,
+                const float* b_hh, const float* a,
+                float* h_save, float* c_save, float* gact, float* tanh_c,
+                void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream);
+
+/* Workspace for hsl_rec_bwd: dgates [T,B,4H], exchange buffers, GEMM
+ * split-K partials, fp64 reduction buffers. */
+size_t hsl_rec_bwd_ws_bytes(int T, int B, int D, int H);
+
+/* Backward: _torch.py:133-170 (reverse loop :143-150, batched GEMMs :153-162,
+ * a-unscale :165-168).  dout [T,B,H], dh_n/dc_n [B,H].  Writes dx [T,B,D] (skipped
+ * when dx is NULL),
+ * dw_ih [4H,D], dw_hh [4H,H], db_ih [4H], db_hh [4H], da [4].  dh0/dc0 [B,H]
+ * receive the gradients w.r.t. h0/c0 when non-NULL (the reference torch
+ * backend returns None for them, _torch.py:170; its Metal backend returns
+ * them, _metal.py:154-174). */
+int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n,
+                const float* x, const float* h_save, const float* c_save,
+                const float* gact, const float* tanh_c,
+                const float* w_ih, const float* w_hh, const float* b_hh, const float* a,
+                float* dx, float* dw_ih, float* dw_hh, float* db_ih, float* db_hh,
+                float* da, float* dh0, float* dc0,
+                void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Parallel (scan) mode: replaces headstartlstm_parallel (_parallel.py:38-74)
+ * and the autograd backward torch derives for it.
+ * ------------------------------------------------------------------------- */
+
+/* Forward: gates = x W_ih^T + b_ih ([T,B,4H], kept for the backward), then the
+ * scan c_t = max(f_t,eps) c_{t-1} + max(i_t g_t, eps), c_{-1} = max(c0,eps)
+ * (the recurrence _parallel.py:21-35 evaluates in the log domain), and
+ * out_t = o_t tanh(c_t).  Writes gates, out [T,B,H], c_seq [T,B,H].
+ * h_n = out[T-1], c_n = c_seq[T-1] (_parallel.py:74). */
+int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float* b_ih,
+                float eps, float* gates, float* out, float* c_seq,
+                int T, int B, int D, int H, void* stream);
+
+size_t hsl_par_bwd_ws_bytes(int T, int B, int D, int H);
+
+/* Backward of hsl_par_fwd w.r.t. x, W_ih, b_ih and c0 (W_hh, b_hh, a and h0
+ * are unused in parallel mode, so they get no gradient, _parallel.py:41-43).
+ * dout [T,B,H], dh_n/dc_n [B,H] are the gradients of out, h_n, c_n.
+ * dx and dc0 may be NULL (then they are not computed). */
+int hsl_par_bwd(const float* dout, const float* dh_n, const float* dc_n,
+                const float* x, const float* c0, const float* gates, const float* c_seq,
+                const float* w_ih, float eps,
+                float* dx, float* dw_ih, float* db_ih, float* dc0,
+                void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream);
+
+/* The scan kernels on their own (used by hsl_par_fwd / hsl_par_bwd).
+ * hsl_scan_fwd: gates [T,B,4H] pre-activations -> out, c_seq [T,B,H].
+ * hsl_scan_bwd: -> dgates [T,B,4H] (pre-activation gradients) and, when
+ * db_part is non-NULL, per-batch column sums of dgates as doubles [B,4H];
+ * dc0 may be NULL. */
+int hsl_scan_fwd(const float* gates, const float* c0, float eps,
+                 float* out, float* c_seq, int T, int B, int H, void* stream);
+int hsl_scan_bwd(const float* gates, const float* c0, const float* c_seq,
+                 const float* dout, const float* dh_n, const float* dc_n, float eps,
+                 float* dgates, double* db_part, float* dc0,
+                 int T, int B, int H, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * fp32 MFMA GEMM used by both modes (torch.nn.functional.linear at
+ * _torch.py:96 / _parallel.py:56 and the `@` products at _torch.py:157-162).
+ *   C[M,N] = op(A)[M,K] . op(B)[K,N] (+ bias[N] when bias != NULL)
+ *   trans_a = 0: A is [M,lda] row-major; 1: A is [K,lda] and op(A) = A^T
+ *   trans_b = 0: B is [K,ldb] row-major; 1: B is [N,ldb] and op(B) = B^T
+ * Split-K (for K much larger than M*N) goes through ws; with ws_bytes = 0 the
+ * product is computed without splitting.
+ * ------------------------------------------------------------------------- */
+size_t hsl_gemm_ws_bytes(int M, int N, int K);
+int hsl_gemm_f32(const float* A, const float* Bm, const float* bias, float* C,
+                 int M, int N, int K, int lda, int ldb, int ldc,
+                 int trans_a, int trans_b, void* ws, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HSL_H */

@@ -1,0 +1,136 @@
+// Library-wide state of libhsl: error text, per-device facts, options.
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <vector>
+
+#include "hsl_internal.h"
+
+namespace hsl {
+
+namespace {
+thread_local char g_err[512] = "";
+thread_local int g_last_path = 0;
+std::atomic<int> g_path_mode{0};
+std::atomic<long long> g_spin_us{2000000};
+std::mutex g_dev_mu;
+DeviceInfo g_devs[64];
+}  // namespace
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(HSL_ERR_HIP, "%s failed: %s", what, hipGetErrorString(e));
+}
+
+int device_info(DeviceInfo* out) {
+  int dev = 0;
+  HSL_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return fail(HSL_ERR_UNSUPPORTED, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  DeviceInfo& d = g_devs[dev];
+  if (d.device != dev) {
+    int cus = 0;
+    HSL_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    d.num_cus = cus;
+    d.num_xcds = 8;  // MI355X: 8 XCDs; workgroup i is dispatched to XCD i % 8
+    d.device = dev;
+  }
+  *out = d;
+  return HSL_OK;
+}
+
+// ---- optional per-kernel timing (hsl_set_timing) ---------------------------------
+namespace {
+struct TimingRec {
+  hipEvent_t start, stop;
+  int kind;
+};
+std::mutex g_tmu;
+std::vector<TimingRec> g_trecs;
+std::atomic<int> g_timing{0};
+}  // namespace
+
+int timing_begin(int kind, hipStream_t s) {
+  if (!g_timing.load()) return -1;
+  TimingRec r{nullptr, nullptr, kind};
+  if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) return -1;
+  if (hipEventRecord(r.start, s) != hipSuccess) return -1;
+  std::lock_guard<std::mutex> lk(g_tmu);
+  g_trecs.push_back(r);
+  return (int)g_trecs.size() - 1;
+}
+
+void timing_end(int slot, hipStream_t s) {
+  if (slot < 0) return;
+  std::lock_guard<std::mutex> lk(g_tmu);
+  if (slot < (int)g_trecs.size()) (void)hipEventRecord(g_trecs[slot].stop, s);
+}
+
+int recurrent_path_mode() { return g_path_mode.load(); }
+long long spin_timeout_ticks() { return g_spin_us.load() * 100; }  // 100 MHz clock
+void note_recurrent_path(int path) { g_last_path = path; }
+
+}  // namespace hsl
+
+extern "C" {
+
+int hsl_abi_version(void) { return HSL_ABI_VERSION; }
+
+const char* hsl_last_error(void) { return hsl::g_err; }
+
+int hsl_set_recurrent_path(int mode) {
+  if (mode < 0 || mode > 2) mode = 0;
+  return hsl::g_path_mode.exchange(mode);
+}
+
+long long hsl_set_spin_timeout_us(long long us) {
+  if (us < 1) us = 1;
+  return hsl::g_spin_us.exchange(us);
+}
+
+int hsl_last_recurrent_path(void) { return hsl::g_last_path; }
+
+int hsl_set_timing(int on) { return hsl::g_timing.exchange(on ? 1 : 0); }
+
+int hsl_timing_collect(int kind, double* total_ms, int* count) {
+  if (!total_ms || !count) return hsl::fail(HSL_ERR_ARG, "hsl_timing_collect: null pointer");
+  std::lock_guard<std::mutex> lk(hsl::g_tmu);
+  double sum = 0.0;
+  int n = 0;
+  std::vector<hsl::TimingRec> keep;
+  for (auto& r : hsl::g_trecs) {
+    if (r.kind != kind) {
+      keep.push_back(r);
+      continue;
+    }
+    float ms = 0.f;
+    HSL_HIP(hipEventSynchronize(r.stop));
+    HSL_HIP(hipEventElapsedTime(&ms, r.start, r.stop));
+    sum += ms;
+    ++n;
+    (void)hipEventDestroy(r.start);
+    (void)hipEventDestroy(r.stop);
+  }
+  hsl::g_trecs.swap(keep);
+  *total_ms = sum;
+  *count = n;
+  return HSL_OK;
+}
+
+int hsl_poll_error(const void* ws, int* flag, void* stream) {
+  if (!ws || !flag) return hsl::fail(HSL_ERR_ARG, "hsl_poll_error: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  HSL_HIP(hipMemcpyAsync(flag, ws, sizeof(int), hipMemcpyDeviceToHost, s));
+  HSL_HIP(hipStreamSynchronize(s));
+  return HSL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,116 @@
+// Internal helpers shared by the HeadStartLSTM HIP kernels (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/hsl.h"
+
+namespace hsl {
+
+// ---- host-side error reporting ------------------------------------------------
+int fail(int code, const char* fmt, ...);        // records text, returns code
+int hip_fail(hipError_t e, const char* what);    // HSL_ERR_HIP with the HIP text
+#define HSL_HIP(call)                                         \
+  do {                                                        \
+    hipError_t hsl_e_ = (call);                               \
+    if (hsl_e_ != hipSuccess) return ::hsl::hip_fail(hsl_e_, #call); \
+  } while (0)
+#define HSL_CHECK(call)                    \
+  do {                                     \
+    int hsl_rc_ = (call);                  \
+    if (hsl_rc_ != HSL_OK) return hsl_rc_; \
+  } while (0)
+
+// Per-device facts queried once.
+struct DeviceInfo {
+  int device = -1;
+  int num_cus = 0;
+  int num_xcds = 8;
+};
+int device_info(DeviceInfo* out);
+
+// Process-wide options (see hsl_set_recurrent_path / hsl_set_spin_timeout_us).
+int recurrent_path_mode();
+// Timing hooks (active only after hsl_set_timing(1)): events around one launch.
+enum TimingKind { kTimeRecFwd = 1, kTimeRecBwd = 2, kTimeScanFwd = 3, kTimeScanBwd = 4,
+                  kTimeInputProj = 5, kTimeStepFwd = 6, kTimeStepBwd = 7 };
+int timing_begin(int kind, hipStream_t s);
+void timing_end(int slot, hipStream_t s);
+long long spin_timeout_ticks();   // in wall_clock64 ticks (100 MHz)
+void note_recurrent_path(int path);
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Carves a caller-provided workspace into aligned pieces.
+struct Carver {
+  char* base;
+  size_t cap;
+  size_t off = 0;
+  Carver(void* b, size_t c) : base(static_cast<char*>(b)), cap(c) {}
+  template <class T>
+  T* take(size_t count) {
+    off = align_up(off, 256);
+    T* p = reinterpret_cast<T*>(base ? base + off : nullptr);
+    off += count * sizeof(T);
+    return p;
+  }
+  bool fits() const { return off <= cap; }
+};
+
+// ---- GEMM (gemm.hip) ------------------------------------------------------------
+struct GemmDesc {
+  const float* A;
+  const float* B;
+  const float* bias;  // [N] or null
+  float* C;
+  int M, N, K, lda, ldb, ldc;
+  int trans_a, trans_b;
+  int acc64;  // 1: fp64 accumulation across BK-slices (long K reductions)
+};
+size_t gemm_ws_bytes(int M, int N, int K, int acc64);
+// Full product with optional split-K through ws (ws may be null when ws_bytes==0).
+int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s);
+// Split-K partial sums kept as fp32 [used][M][N] in `partials` (room for `splits`
+// planes); *used receives the number of planes written (<= splits).  Used by the
+// fused epilogues of the weight gradients.
+int gemm_partials(const GemmDesc& d, float* partials, int splits, hipStream_t s, int* used);
+int gemm_pick_splits(int M, int N, int K, int acc64);
+
+// ---- shared finalisation (recurrent.hip) ------------------------------------------
+// db = sum_b db_part[b][:] ; db_ih = db ; db_hh = a_g db ; da[g] = sum_{n in g} rowdot[n] + b_hh[n] db[n].
+// Any of rowdot, b_hh, a, db_hh, da may be null (parallel mode only wants db_ih).
+int bias_grads_from_parts(const double* db_part, int B, const double* rowdot, const float* b_hh, const float* a,
+                          float* db_ih, float* db_hh, float* da, int H, hipStream_t s);
+int zero_words(unsigned long long* p, size_t n, hipStream_t s);
+int copy_f32(float* dst, const float* src, size_t n, hipStream_t s);
+
+// ---- device math ----------------------------------------------------------------
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+// exp(x) = 2^(x log2 e) on v_exp_f32; sigmoid and tanh from their definitions with
+// v_rcp_f32 (about 1 ulp each).  Both saturate cleanly: exp overflow gives inf and
+// rcp(inf) = 0, so sigmoid(-inf..) -> 0 and tanh(+-large) -> +-1 without NaN.
+__device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + exp_f(-x)); }
+__device__ __forceinline__ float tanh_f(float x) { return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + exp_f(2.0f * x)); }
+
+// 64-bit {tag:hi32, value:lo32} words used to hand values between workgroups of a
+// persistent kernel.  Stores and loads are relaxed device-scope atomics (each word
+// is read or written whole); a reader accepts a word only when its tag matches the
+// step it waits for, so no separate barrier or fence is needed.
+__device__ __forceinline__ void tag_store(unsigned long long* p, float v, unsigned tag) {
+  unsigned long long w = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(v);
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long tag_load(const unsigned long long* p) {
+  return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned tag_of(unsigned long long w) { return static_cast<unsigned>(w >> 32); }
+__device__ __forceinline__ float val_of(unsigned long long w) { return __uint_as_float(static_cast<unsigned>(w)); }
+
+}  // namespace hsl

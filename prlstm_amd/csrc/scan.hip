@@ -1,0 +1,376 @@
+// Parallel (scan) mode of HeadStartLSTM: forward scan, hand-written backward scan and
+// the parallel-mode entry points.
+//
+// Reference behaviour (src/headstartlstm/_parallel.py:21-74):
+//   gates = x W_ih^T + b_ih;  i,f,g,o = sigmoid(gates);  b = i*g
+//   c_t = exp(a*_t + logcumsumexp([log max(c0,eps), log max(b,eps) - a*])_t),
+//   a*_t = cumsum(log max(f,eps))
+//   out = o * tanh(c);  h_n = out[T-1];  c_n = c[T-1]
+// The log-domain expression is the closed form of the first-order linear recurrence
+//   c_t = f~_t c_{t-1} + b~_t,   f~ = max(f,eps), b~ = max(i g, eps), c_{-1} = max(c0,eps)
+// (all coefficients positive).  Here it is evaluated as a scan of the affine maps
+// c -> f~ c + b~ in the linear domain: f~, b~ lie in [eps, 1), so nothing overflows,
+// a running product that underflows is the exact fp32 limit, and every term is
+// positive, so composing maps never cancels.  The backward is the mirror reverse
+// scan G_t = e_t + f~_{t+1} G_{t+1} of the total gradient G_t = dL/dc_t; the clamps
+// pass gradient where their input is >= eps (torch's clamp_min rule).
+//
+// Layout: gates [T,B,4H] (the GEMM output, never transposed), out/c [T,B,H].  One
+// workgroup owns 64 consecutive channels (b,j) = one wave-width, so every load and
+// store is a 256-byte row segment, and walks all of T in chunks of NW*L steps: each
+// of the NW waves takes L consecutive steps, composes them into one map, the maps
+// are combined through LDS, and each wave re-runs its steps from its carry-in.  The
+// next chunk's loads are issued before the current chunk is processed.
+#include "hsl_internal.h"
+
+namespace hsl {
+namespace {
+
+constexpr int kFwdWaves = 16, kFwdSteps = 8;
+constexpr int kBwdWaves = 8, kBwdSteps = 8;
+
+template <int NW, int L>
+__global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restrict__ gates, const float* __restrict__ c0,
+                                                          float eps, float* __restrict__ out, float* __restrict__ cseq,
+                                                          int T, int B, int H) {
+  __shared__ float sA[NW][64], sV[NW][64], sC[64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int C = B * H;
+  const int ch = blockIdx.x * 64 + lane;
+  const bool ok = ch < C;
+  const int b = ok ? ch / H : 0, j = ok ? ch % H : 0;
+  const size_t gstride = (size_t)B * 4 * H;  // per time step
+  const float* gbase = gates + (size_t)b * 4 * H + j;
+  const size_t ostride = (size_t)B * H;
+  if (w == 0) sC[lane] = ok ? fmaxf(c0[ch], eps) : 0.f;
+
+  constexpr int CH = NW * L;
+  const int nchunks = (T + CH - 1) / CH;
+  float cur[4][L], nxt[4][L];
+  auto load = [&](int chunk, float (&r)[4][L]) {
+#pragma unroll
+    for (int s = 0; s < L; ++s) {
+      const int t = chunk * CH + w * L + s;
+      const bool v = ok && t < T;
+      const float* p = gbase + (size_t)t * gstride;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) r[g][s] = v ? p[g * H] : 0.f;
+    }
+  };
+  if (nchunks > 0) load(0, cur);
+  for (int k = 0; k < nchunks; ++k) {
+    if (k + 1 < nchunks) load(k + 1, nxt);
+    float fv[L], bv[L], ov[L];
+    float A = 1.f, V = 0.f;
+#pragma unroll
+    for (int s = 0; s < L; ++s) {
+      const int t = k * CH + w * L + s;
+      const float ig = sigmoid_f(cur[0][s]), fg = sigmoid_f(cur[1][s]);
+      const float gg = sigmoid_f(cur[2][s]), og = sigmoid_f(cur[3][s]);
+      fv[s] = fmaxf(fg, eps);
+      bv[s] = fmaxf(ig * gg, eps);
+      ov[s] = og;
+      if (t < T) {
+        A = fv[s] * A;
+        V = fv[s] * V + bv[s];
+      }
+    }
+    sA[w][lane] = A;
+    sV[w][lane] = V;
+    __syncthreads();
+    float c = sC[lane];
+    for (int u = 0; u < w; ++u) c = sA[u][lane] * c + sV[u][lane];
+#pragma unroll
+    for (int s = 0; s < L; ++s) {
+      const int t = k * CH + w * L + s;
+      if (t < T) {
+        c = fv[s] * c + bv[s];
+        if (ok) {
+          out[(size_t)t * ostride + ch] = ov[s] * tanh_f(c);
+          cseq[(size_t)t * ostride + ch] = c;
+        }
+      }
+    }
+    __syncthreads();
+    if (w == NW - 1) sC[lane] = c;
+#pragma unroll
+    for (int s = 0; s < L; ++s)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) cur[g][s] = nxt[g][s];
+  }
+}
+
+// Reverse scan.  For wave steps [ws, we] and G_in = G_{we+1}:
+//   G_t = e_t + f~_{t+1} G_{t+1},  e_t = dout'_t o_t (1 - tanh^2 c_t) (+ dc_n at T-1),
+//   dout'_t = dout_t (+ dh_n at T-1),  f~_T = 0.
+// Then df~_t = G_t c_{t-1}, db~_t = G_t and the sigmoid/clamp chain gives dgates.
+template <int NW, int L>
+__global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
+    const float* __restrict__ gates, const float* __restrict__ c0, const float* __restrict__ cseq,
+    const float* __restrict__ dout, const float* __restrict__ dh_n, const float* __restrict__ dc_n, float eps,
+    float* __restrict__ dgates, double* __restrict__ db_part, float* __restrict__ dc0, int T, int B, int H) {
+  __shared__ float sA[NW][64], sV[NW][64], sG[64];
+  __shared__ double sdb[NW][4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int C = B * H;
+  const int ch = blockIdx.x * 64 + lane;
+  const bool ok = ch < C;
+  const int b = ok ? ch / H : 0, j = ok ? ch % H : 0;
+  const size_t gstride = (size_t)B * 4 * H;
+  const float* gbase = gates + (size_t)b * 4 * H + j;
+  float* dgbase = dgates + (size_t)b * 4 * H + j;
+  const size_t ostride = (size_t)B * H;
+  const float c0c = ok ? fmaxf(c0[ch], eps) : 0.f;
+  const bool c0_pass = ok && c0[ch] >= eps;
+  const float dhn = ok ? dh_n[ch] : 0.f, dcn = ok ? dc_n[ch] : 0.f;
+  if (w == 0) sG[lane] = 0.f;
+
+  constexpr int CH = NW * L;
+  const int nchunks = (T + CH - 1) / CH;
+  // per step: zi zf zg zo c dout; plus zf at we+1 and c at ws-1
+  float cur[6][L], nxt[6][L];
+  float cur_fn, nxt_fn, cur_cp, nxt_cp;
+  auto load = [&](int chunk, float (&r)[6][L], float& fnext, float& cprev) {
+    const int ws = chunk * CH + w * L;
+#pragma unroll
+    for (int s = 0; s < L; ++s) {
+      const int t = ws + s;
+      const bool v = ok && t < T;
+      const float* p = gbase + (size_t)t * gstride;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) r[g][s] = v ? p[g * H] : 0.f;
+      r[4][s] = v ? cseq[(size_t)t * ostride + ch] : 0.f;
+      r[5][s] = v ? dout[(size_t)t * ostride + ch] : 0.f;
+    }
+    const int tn = ws + L;
+    fnext = (ok && tn < T) ? gbase[(size_t)tn * gstride + H] : 0.f;
+    cprev = ws == 0 ? c0c : ((ok && ws - 1 < T) ? cseq[(size_t)(ws - 1) * ostride + ch] : 0.f);
+  };
+  if (nchunks > 0) load(nchunks - 1, cur, cur_fn, cur_cp);
+  double dbacc[4] = {0.0, 0.0, 0.0, 0.0};
+  float g_first = 0.f, f_first = 0.f;  // G and f~ at this wave's first step (for dc0)
+  for (int k = nchunks - 1; k >= 0; --k) {
+    if (k > 0) load(k - 1, nxt, nxt_fn, nxt_cp);
+    const int ws = k * CH + w * L;
+    // f~_{t+1} for each step (0 beyond T), e_t
+    float fn[L], ev[L];
+#pragma unroll
+    for (int s = 0; s < L; ++s) {
+      const int t = ws + s;
+      const float znext = (s + 1 < L) ? cur[1][s + 1] : cur_fn;
+      fn[s] = (t + 1 < T) ? fmaxf(sigmoid_f(znext), eps) : 0.f;
+      const float og = sigmoid_f(cur[3][s]);
+      const float tc = tanh_f(cur[4][s]);
+      float d = cur[5][s];
+      if (t == T - 1) d = d + dhn;
+      float e = d * og * (1.0f - tc * tc);
+      if (t == T - 1) e = e + dcn;
+      ev[s] = (t < T) ? e : 0.f;
+    }
+    float A = 1.f, V = 0.f;
+#pragma unroll
+    for (int s = L - 1; s >= 0; --s) {
+      if (ws + s < T) {
+        V = ev[s] + fn[s] * V;
+        A = fn[s] * A;
+      }
+    }
+    sA[w][lane] = A;
+    sV[w][lane] = V;
+    __syncthreads();
+    float G = sG[lane];
+    for (int u = NW - 1; u > w; --u) G = sA[u][lane] * G + sV[u][lane];
+#pragma unroll
+    for (int s = L - 1; s >= 0; --s) {
+      const int t = ws + s;
+      if (t < T) {
+        G = ev[s] + fn[s] * G;
+        const float ig = sigmoid_f(cur[0][s]), fg = sigmoid_f(cur[1][s]);
+        const float gg = sigmoid_f(cur[2][s]), og = sigmoid_f(cur[3][s]);
+        const float tc = tanh_f(cur[4][s]);
+        const float cprev = s > 0 ? cur[4][s - 1] : cur_cp;
+        float d = cur[5][s];
+        if (t == T - 1) d = d + dhn;
+        const float bb = ig * gg;
+        const float dbb = bb >= eps ? G : 0.f;
+        const float dfp = fg >= eps ? (G * cprev) * fg * (1.0f - fg) : 0.f;
+        const float dip = (dbb * gg) * ig * (1.0f - ig);
+        const float dgp = (dbb * ig) * gg * (1.0f - gg);
+        const float dop = (d * tc) * og * (1.0f - og);
+        if (ok) {
+          float* q = dgbase + (size_t)t * gstride;
+          q[0] = dip;
+          q[H] = dfp;
+          q[2 * H] = dgp;
+          q[3 * H] = dop;
+        }
+        dbacc[0] += (double)dip;
+        dbacc[1] += (double)dfp;
+        dbacc[2] += (double)dgp;
+        dbacc[3] += (double)dop;
+        if (s == 0) {
+          g_first = G;
+          f_first = fmaxf(fg, eps);
+        }
+      }
+    }
+    __syncthreads();
+    if (w == 0) sG[lane] = G;
+#pragma unroll
+    for (int s = 0; s < L; ++s)
+#pragma unroll
+      for (int r = 0; r < 6; ++r) cur[r][s] = nxt[r][s];
+    cur_fn = nxt_fn;
+    cur_cp = nxt_cp;
+  }
+  // dc0 = G_0 f~_0 where the clamp of c0 passes gradient
+  if (w == 0 && ok && dc0) dc0[ch] = (c0_pass && T > 0) ? g_first * f_first : 0.f;
+  if (db_part) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) sdb[w][g][lane] = dbacc[g];
+    __syncthreads();
+    if (w == 0 && ok) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        double s = 0.0;
+        for (int u = 0; u < NW; ++u) s += sdb[u][g][lane];
+        db_part[(size_t)b * 4 * H + g * H + j] = s;
+      }
+    }
+  }
+}
+
+int check_scan_dims(int T, int B, int H) {
+  if (T < 0 || B < 0 || H < 0) return fail(HSL_ERR_ARG, "negative dimension (T=%d B=%d H=%d)", T, B, H);
+  if ((long long)B * H >= (1ll << 31) || (long long)T * B * 4 * H > (1ll << 40))
+    return fail(HSL_ERR_UNSUPPORTED, "problem too large");
+  return HSL_OK;
+}
+
+int scan_fwd(const float* gates, const float* c0, float eps, float* out, float* cseq, int T, int B, int H,
+             hipStream_t s) {
+  const int C = B * H;
+  if (C == 0 || T == 0) return HSL_OK;
+  const int slot = timing_begin(kTimeScanFwd, s);
+  hipLaunchKernelGGL((scan_fwd_kernel<kFwdWaves, kFwdSteps>), dim3((C + 63) / 64), dim3(kFwdWaves * 64), 0, s, gates,
+                     c0, eps, out, cseq, T, B, H);
+  HSL_HIP(hipGetLastError());
+  timing_end(slot, s);
+  return HSL_OK;
+}
+
+int scan_bwd(const float* gates, const float* c0, const float* cseq, const float* dout, const float* dh_n,
+             const float* dc_n, float eps, float* dgates, double* db_part, float* dc0, int T, int B, int H,
+             hipStream_t s) {
+  const int C = B * H;
+  if (C == 0) return HSL_OK;
+  if (T == 0) {  // no steps: dc0 = dc_n through the clamp is not reached; all zero
+    if (dc0) HSL_CHECK(copy_f32(dc0, nullptr, (size_t)C, s));
+    if (db_part) HSL_CHECK(zero_words(reinterpret_cast<unsigned long long*>(db_part), (size_t)4 * C, s));
+    return HSL_OK;
+  }
+  const int slot = timing_begin(kTimeScanBwd, s);
+  hipLaunchKernelGGL((scan_bwd_kernel<kBwdWaves, kBwdSteps>), dim3((C + 63) / 64), dim3(kBwdWaves * 64), 0, s, gates,
+                     c0, cseq, dout, dh_n, dc_n, eps, dgates, db_part, dc0, T, B, H);
+  HSL_HIP(hipGetLastError());
+  timing_end(slot, s);
+  return HSL_OK;
+}
+
+struct ParWs {
+  float* dgates;    // [T*B*4H]
+  double* db_part;  // [B*4H]
+  float* gemm;
+  size_t gemm_bytes;
+};
+
+size_t carve_par(void* ws, size_t cap, int T, int B, int D, int H, ParWs* o) {
+  Carver c(ws, cap);
+  o->dgates = c.take<float>((size_t)T * B * 4 * H);
+  o->db_part = c.take<double>((size_t)B * 4 * H);
+  size_t g = gemm_ws_bytes(4 * H, D, T * B, 1);
+  const size_t g6 = gemm_ws_bytes(T * B, D, 4 * H, 1);
+  if (g6 > g) g = g6;
+  o->gemm_bytes = g;
+  o->gemm = c.take<float>(g / sizeof(float) + 1);
+  return c.off;
+}
+
+}  // namespace
+}  // namespace hsl
+
+using namespace hsl;
+
+extern "C" {
+
+int hsl_scan_fwd(const float* gates, const float* c0, float eps, float* out, float* c_seq, int T, int B, int H,
+                 void* stream) {
+  HSL_CHECK(check_scan_dims(T, B, H));
+  if (T > 0 && B > 0 && H > 0 && (!gates || !c0 || !out || !c_seq)) return fail(HSL_ERR_ARG, "hsl_scan_fwd: null pointer");
+  return scan_fwd(gates, c0, eps, out, c_seq, T, B, H, static_cast<hipStream_t>(stream));
+}
+
+int hsl_scan_bwd(const float* gates, const float* c0, const float* c_seq, const float* dout, const float* dh_n,
+                 const float* dc_n, float eps, float* dgates, double* db_part, float* dc0, int T, int B, int H,
+                 void* stream) {
+  HSL_CHECK(check_scan_dims(T, B, H));
+  if (B > 0 && H > 0 && T > 0 && (!gates || !c0 || !c_seq || !dout || !dh_n || !dc_n || !dgates))
+    return fail(HSL_ERR_ARG, "hsl_scan_bwd: null pointer");
+  return scan_bwd(gates, c0, c_seq, dout, dh_n, dc_n, eps, dgates, db_part, dc0, T, B, H,
+                  static_cast<hipStream_t>(stream));
+}
+
+int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float* b_ih, float eps, float* gates,
+                float* out, float* c_seq, int T, int B, int D, int H, void* stream) {
+  HSL_CHECK(check_scan_dims(T, B, H));
+  if (D < 0) return fail(HSL_ERR_ARG, "negative D");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (T == 0 || B == 0 || H == 0) return HSL_OK;
+  if (!x || !c0 || !w_ih || !b_ih || !gates || !out || !c_seq) return fail(HSL_ERR_ARG, "hsl_par_fwd: null pointer");
+  GemmDesc g1{x, w_ih, b_ih, gates, T * B, 4 * H, D, D, D, 4 * H, 0, 1};
+  const int slot = timing_begin(kTimeInputProj, s);
+  HSL_CHECK(gemm_run(g1, nullptr, 0, s));
+  timing_end(slot, s);
+  return scan_fwd(gates, c0, eps, out, c_seq, T, B, H, s);
+}
+
+size_t hsl_par_bwd_ws_bytes(int T, int B, int D, int H) {
+  if (T < 0 || B < 0 || D < 0 || H < 0) return 0;
+  ParWs w;
+  return carve_par(nullptr, 0, T, B, D, H, &w);
+}
+
+int hsl_par_bwd(const float* dout, const float* dh_n, const float* dc_n, const float* x, const float* c0,
+                const float* gates, const float* c_seq, const float* w_ih, float eps, float* dx, float* dw_ih,
+                float* db_ih, float* dc0, void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream) {
+  HSL_CHECK(check_scan_dims(T, B, H));
+  if (D < 0) return fail(HSL_ERR_ARG, "negative D");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (H == 0) return HSL_OK;
+  if (!dw_ih || !db_ih || !w_ih) return fail(HSL_ERR_ARG, "hsl_par_bwd: null pointer");
+  ParWs w;
+  const size_t need = carve_par(ws, ws_bytes, T, B, D, H, &w);
+  if (!ws || ws_bytes < need) return fail(HSL_ERR_ARG, "hsl_par_bwd: workspace %zu bytes, need %zu", ws_bytes, need);
+  if (T == 0 || B == 0) {
+    HSL_CHECK(copy_f32(dw_ih, nullptr, (size_t)4 * H * D, s));
+    HSL_CHECK(copy_f32(db_ih, nullptr, (size_t)4 * H, s));
+    if (dc0) HSL_CHECK(copy_f32(dc0, nullptr, (size_t)B * H, s));
+    return HSL_OK;
+  }
+  if (!dout || !dh_n || !dc_n || !x || !c0 || !gates || !c_seq)
+    return fail(HSL_ERR_ARG, "hsl_par_bwd: null pointer");
+  HSL_CHECK(scan_bwd(gates, c0, c_seq, dout, dh_n, dc_n, eps, w.dgates, w.db_part, dc0, T, B, H, s));
+  HSL_CHECK(bias_grads_from_parts(w.db_part, B, nullptr, nullptr, nullptr, db_ih, nullptr, nullptr, H, s));
+  const int TB = T * B;
+  if (D > 0) {
+    GemmDesc g5{w.dgates, x, nullptr, dw_ih, 4 * H, D, TB, 4 * H, D, D, 1, 0, 1};
+    HSL_CHECK(gemm_run(g5, w.gemm, w.gemm_bytes, s));
+    if (dx) {
+      GemmDesc g6{w.dgates, w_ih, nullptr, dx, TB, D, 4 * H, 4 * H, D, D, 0, 0, 1};
+      HSL_CHECK(gemm_run(g6, w.gemm, w.gemm_bytes, s));
+    }
+  }
+  return HSL_OK;
+}
+
+}  // extern "C"

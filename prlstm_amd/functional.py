@@ -1,0 +1,179 @@
+"""Autograd functions of the HeadStartLSTM hot path on MI355X.
+
+Both keep the reference backend functional signature
+``fn(x, h0, c0, W_ih, W_hh, b_ih, b_hh, a) -> (output[T,B,H], h_n[B,H], c_n[B,H])``
+(``_torch.py:173``, ``_parallel.py:38``) and run every kernel through libhsl
+(include/hsl.h) on the current HIP stream.  No host synchronisation and no
+allocation outside torch's caching allocator happens, so a whole training step
+can be captured in a graph (see ``prlstm_amd.graph``).
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+EPS = 1e-6  # clamp floor of the parallel scan (_parallel.py:21, :38)
+
+_debug_checks = False
+
+
+def debug_checks(enabled=True):
+    """When enabled, every recurrent call synchronises and raises if a persistent
+    kernel reported a timed-out wait (the device error flag of its workspace)."""
+    global _debug_checks
+    _debug_checks = bool(enabled)
+
+
+def _poll(ws, device):
+    if not _debug_checks:
+        return
+    flag = ctypes.c_int(0)
+    _lib.call("hsl_poll_error", _lib.ptr(ws), ctypes.byref(flag), _lib.stream_of(device))
+    if flag.value:
+        raise RuntimeError(f"a persistent kernel reported device error flag {flag.value} "
+                           "(a wait between workgroups timed out)")
+
+
+def _check(x, h0, c0, w_ih, w_hh, b_ih, b_hh, a):
+    if x.dim() != 3:
+        raise RuntimeError(f"x must be [T, B, D], got shape {tuple(x.shape)}")
+    T, B, D = x.shape
+    H = w_hh.shape[-1]
+    want = {
+        "h0": (h0, (B, H)), "c0": (c0, (B, H)),
+        "weight_ih_l0": (w_ih, (4 * H, D)), "weight_hh_l0": (w_hh, (4 * H, H)),
+        "bias_ih_l0": (b_ih, (4 * H,)), "bias_hh_l0": (b_hh, (4 * H,)), "a": (a, (4,)),
+    }
+    for name, (t, shape) in want.items():
+        if tuple(t.shape) != shape:
+            raise RuntimeError(f"{name} must have shape {shape}, got {tuple(t.shape)}")
+    for name, t in [("x", x)] + [(n, v[0]) for n, v in want.items()]:
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"prlstm_amd runs on ROCm devices only: {name} is on {t.device} "
+                "(move the module and inputs to the GPU)")
+        if t.device != x.device:
+            raise RuntimeError(f"{name} is on {t.device}, x is on {x.device}")
+        if t.dtype != torch.float32:
+            raise RuntimeError(f"prlstm_amd kernels compute in float32; {name} is {t.dtype}")
+    return T, B, D, H
+
+
+def _c(t):
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _grad_or_zeros(g, like):
+    return _c(g) if g is not None else torch.zeros_like(like)
+
+
+class RecurrentFn(torch.autograd.Function):
+    """Exact BPTT (the reference torch backend, ``_torch.py:86-170``).
+
+    Backward returns gradients for x, the four weights/biases and a, plus the
+    gradients w.r.t. h0 and c0 when those require grad (the reference torch
+    backend returns None for them; its Metal backend returns them).
+    """
+
+    @staticmethod
+    def forward(ctx, x, h0, c0, w_ih, w_hh, b_ih, b_hh, a):
+        T, B, D, H = _check(x, h0, c0, w_ih, w_hh, b_ih, b_hh, a)
+        x, h0, c0, w_ih, w_hh, b_ih, b_hh, a = map(_c, (x, h0, c0, w_ih, w_hh, b_ih, b_hh, a))
+        h_save = x.new_empty(T + 1, B, H)
+        c_save = x.new_empty(T + 1, B, H)
+        gact = x.new_empty(T, B, 4 * H)
+        tanh_c = x.new_empty(T, B, H)
+        lib = _lib.load()
+        nbytes = lib.hsl_rec_fwd_ws_bytes(T, B, D, H)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+        P = _lib.ptr
+        _lib.call("hsl_rec_fwd", P(x), P(h0), P(c0), P(w_ih), P(w_hh), P(b_ih), P(b_hh), P(a),
+                  P(h_save), P(c_save), P(gact), P(tanh_c), P(ws), nbytes, T, B, D, H,
+                  _lib.stream_of(x.device))
+        _poll(ws, x.device)
+        ctx.save_for_backward(x, w_ih, w_hh, b_hh, a, h_save, c_save, gact, tanh_c)
+        ctx.dims = (T, B, D, H)
+        return h_save[1:], h_save[T], c_save[T]
+
+    @staticmethod
+    def backward(ctx, dout, dh_n, dc_n):
+        x, w_ih, w_hh, b_hh, a, h_save, c_save, gact, tanh_c = ctx.saved_tensors
+        T, B, D, H = ctx.dims
+        dout = _grad_or_zeros(dout, h_save[1:])
+        dh_n = _grad_or_zeros(dh_n, h_save[T])
+        dc_n = _grad_or_zeros(dc_n, c_save[T])
+        need = ctx.needs_input_grad
+        dx = torch.empty_like(x) if need[0] else None
+        dh0 = x.new_empty(B, H) if need[1] else None
+        dc0 = x.new_empty(B, H) if need[2] else None
+        dw_ih = torch.empty_like(w_ih)
+        dw_hh = torch.empty_like(w_hh)
+        db_ih = x.new_empty(4 * H)
+        db_hh = x.new_empty(4 * H)
+        da = x.new_empty(4)
+        lib = _lib.load()
+        nbytes = lib.hsl_rec_bwd_ws_bytes(T, B, D, H)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+        P = _lib.ptr
+        _lib.call("hsl_rec_bwd", P(dout), P(dh_n), P(dc_n), P(x), P(h_save), P(c_save), P(gact),
+                  P(tanh_c), P(w_ih), P(w_hh), P(b_hh), P(a), P(dx), P(dw_ih), P(dw_hh), P(db_ih),
+                  P(db_hh), P(da), P(dh0), P(dc0), P(ws), nbytes, T, B, D, H,
+                  _lib.stream_of(x.device))
+        _poll(ws, x.device)
+        return dx, dh0, dc0, dw_ih, dw_hh, db_ih, db_hh, da
+
+
+class ParallelFn(torch.autograd.Function):
+    """Parallel (scan) mode (``_parallel.py:38-74``).
+
+    h0, W_hh, b_hh and a are accepted for the common signature but unused, so
+    they receive no gradient (None), as in the reference.
+    """
+
+    @staticmethod
+    def forward(ctx, x, h0, c0, w_ih, w_hh, b_ih, b_hh, a, eps):
+        T, B, D, H = _check(x, h0, c0, w_ih, w_hh, b_ih, b_hh, a)
+        x, c0, w_ih, b_ih = map(_c, (x, c0, w_ih, b_ih))
+        gates = x.new_empty(T, B, 4 * H)
+        out = x.new_empty(T, B, H)
+        c_seq = x.new_empty(T, B, H)
+        P = _lib.ptr
+        _lib.call("hsl_par_fwd", P(x), P(c0), P(w_ih), P(b_ih), float(eps), P(gates), P(out),
+                  P(c_seq), T, B, D, H, _lib.stream_of(x.device))
+        ctx.save_for_backward(x, c0, w_ih, gates, c_seq)
+        ctx.dims = (T, B, D, H)
+        ctx.eps = float(eps)
+        return out, out[T - 1], c_seq[T - 1]
+
+    @staticmethod
+    def backward(ctx, dout, dh_n, dc_n):
+        x, c0, w_ih, gates, c_seq = ctx.saved_tensors
+        T, B, D, H = ctx.dims
+        dout = _grad_or_zeros(dout, c_seq)
+        dh_n = _grad_or_zeros(dh_n, c0)
+        dc_n = _grad_or_zeros(dc_n, c0)
+        need = ctx.needs_input_grad
+        dx = torch.empty_like(x) if need[0] else None
+        dc0 = x.new_empty(B, H) if need[2] else None
+        dw_ih = torch.empty_like(w_ih)
+        db_ih = x.new_empty(4 * H)
+        lib = _lib.load()
+        nbytes = lib.hsl_par_bwd_ws_bytes(T, B, D, H)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+        P = _lib.ptr
+        _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(x), P(c0), P(gates), P(c_seq),
+                  P(w_ih), ctx.eps, P(dx), P(dw_ih), P(db_ih), P(dc0), P(ws), nbytes, T, B, D, H,
+                  _lib.stream_of(x.device))
+        return dx, None, dc0, dw_ih, None, db_ih, None, None, None
+
+
+def headstartlstm_recurrent(x, h0, c0, W_ih, W_hh, b_ih, b_hh, a):
+    """Recurrent-mode functional (drop-in for ``headstartlstm_torch``, ``_torch.py:173``)."""
+    return RecurrentFn.apply(x, h0, c0, W_ih, W_hh, b_ih, b_hh, a)
+
+
+def headstartlstm_parallel(x, h0, c0, W_ih, W_hh, b_ih, b_hh, a, eps=EPS):
+    """Parallel-mode functional (drop-in for ``headstartlstm_parallel``, ``_parallel.py:38``)."""
+    return ParallelFn.apply(x, h0, c0, W_ih, W_hh, b_ih, b_hh, a, eps)

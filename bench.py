@@ -41,6 +41,17 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated against a known-size copy), or None."""
+    for f in sorted((ROOT / "profiles").glob("hbm_traffic_*.md")):
+        for line in f.read_text().splitlines():
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel:
+                return int(float(parts[2]))
+    return None
+
+
 def make_inputs():
     """configs[2] synthetic inputs (SURVEY 8(d) recipe): seed 0, module on CPU, then x."""
     from prlstm_amd import HeadStartLSTM
@@ -122,6 +133,11 @@ def bench_scan(args):
             _lib.call("hsl_scan_bwd", P(gates), P(c0), P(c_seq), P(dout), P(dh_n), P(dc_n), 1e-6,
                       P(dgates), P(db_part), None, ST, SB, SH, s)
     torch.cuda.synchronize()
+    # known-size elementwise kernel (reads and writes 256 MiB each) for calibrating
+    # the FETCH_SIZE / WRITE_SIZE counters of rocprofv3 --pmc runs of this script
+    calib = out.view(-1)[: 64 * 2 ** 20]
+    torch.mul(c_seq.view(-1)[: 64 * 2 ** 20], 1.0, out=calib)
+    torch.cuda.synchronize()
     tf, nf = _lib.timing_collect("scan_fwd")
     tb, nb = _lib.timing_collect("scan_bwd")
     _lib.set_timing(False)
@@ -136,7 +152,9 @@ def bench_scan(args):
         "roofline": {"bound": "hbm", "achieved": round((fwd_b + bwd_b) / (fwd_ms + bwd_ms) / 1e6, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round((fwd_b + bwd_b) / (fwd_ms + bwd_ms) / 1e6 / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": (measured_traffic("scan_fwd_kernel") or 0) + (measured_traffic("scan_bwd_kernel") or 0)
+                     or None,
+                     "algorithmic_bytes": fwd_b + bwd_b},
     }
     log(f"scan fwd {fwd_ms:.4f} ms ({res['fwd_GBps']} GB/s) bwd {bwd_ms:.4f} ms ({res['bwd_GBps']} GB/s)")
     return res
@@ -226,7 +244,8 @@ def main():
                    "recurrent_path": {1: "per-step", 2: "persistent"}.get(path, path)},
         "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(achieved, 3),
                      "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic(kname) if kname.endswith("persistent") else None,
                      "kernel_ms": round(kms, 5), "flops_per_launch": rec_flops},
         "step_tflops": round(step_flops / (ms * 1e-3) / 1e12, 3),
         "kernels_ms": {k: round(v, 5) for k, v in kern.items()},

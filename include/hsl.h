@@ -54,6 +54,11 @@ int hsl_set_recurrent_path(int mode);
  * workgroup (default 2,000,000).  On expiry the kernel stops and raises the
  * device error flag instead of waiting forever.  Returns the previous value. */
 long long hsl_set_spin_timeout_us(long long us);
+/* Hand-off between the workgroups of a persistent kernel: 0 = automatic (stores
+ * that stay in the XCD's L2 when the launch verifies that every workgroup of a
+ * batch group runs on one XCD, device-scope stores otherwise), 1 = always
+ * device-scope stores.  Returns the previous value.  Process-wide. */
+int hsl_set_exchange_scope(int mode);
 /* Which path the last hsl_rec_fwd / hsl_rec_bwd on this host thread used:
  * 1 = per-step, 2 = persistent. */
 int hsl_last_recurrent_path(void);

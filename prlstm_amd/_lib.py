@@ -25,6 +25,7 @@ SIGNATURES = {
     "hsl_set_recurrent_path": (_I, [_I]),
     "hsl_set_spin_timeout_us": (ctypes.c_longlong, [ctypes.c_longlong]),
     "hsl_last_recurrent_path": (_I, []),
+    "hsl_set_exchange_scope": (_I, [_I]),
     "hsl_poll_error": (_I, [_P, _P, _P]),
     "hsl_set_timing": (_I, [_I]),
     "hsl_timing_collect": (_I, [_I, _P, _P]),
@@ -89,6 +90,11 @@ def call(name, *args):
 def set_recurrent_path(mode):
     """0 = automatic, 1 = one launch per time step, 2 = persistent only."""
     return load().hsl_set_recurrent_path(int(mode))
+
+
+def set_exchange_scope(mode):
+    """0 = automatic (XCD-local hand-off when verified), 1 = always device scope."""
+    return load().hsl_set_exchange_scope(int(mode))
 
 
 def set_spin_timeout_us(us):

@@ -13,6 +13,7 @@ namespace {
 thread_local char g_err[512] = "";
 thread_local int g_last_path = 0;
 std::atomic<int> g_path_mode{0};
+std::atomic<int> g_exchange_scope{0};
 std::atomic<long long> g_spin_us{2000000};
 std::mutex g_dev_mu;
 DeviceInfo g_devs[64];
@@ -75,6 +76,7 @@ void timing_end(int slot, hipStream_t s) {
 }
 
 int recurrent_path_mode() { return g_path_mode.load(); }
+int exchange_scope_mode() { return g_exchange_scope.load(); }
 long long spin_timeout_ticks() { return g_spin_us.load() * 100; }  // 100 MHz clock
 void note_recurrent_path(int path) { g_last_path = path; }
 
@@ -97,6 +99,8 @@ long long hsl_set_spin_timeout_us(long long us) {
 }
 
 int hsl_last_recurrent_path(void) { return hsl::g_last_path; }
+
+int hsl_set_exchange_scope(int mode) { return hsl::g_exchange_scope.exchange(mode == 1 ? 1 : 0); }
 
 int hsl_set_timing(int on) { return hsl::g_timing.exchange(on ? 1 : 0); }
 

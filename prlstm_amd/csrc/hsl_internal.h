@@ -34,6 +34,7 @@ int device_info(DeviceInfo* out);
 
 // Process-wide options (see hsl_set_recurrent_path / hsl_set_spin_timeout_us).
 int recurrent_path_mode();
+int exchange_scope_mode();  // 1: persistent kernels always use device-scope stores
 // Timing hooks (active only after hsl_set_timing(1)): events around one launch.
 enum TimingKind { kTimeRecFwd = 1, kTimeRecBwd = 2, kTimeScanFwd = 3, kTimeScanBwd = 4,
                   kTimeInputProj = 5, kTimeStepFwd = 6, kTimeStepBwd = 7 };

@@ -217,6 +217,65 @@ struct EpiCellBwd {
 // ---------------------------------------------------------------------------------
 // persistent path
 // ---------------------------------------------------------------------------------
+// Hand-off between the workgroups of a batch group.  Readers always poll with
+// relaxed device-scope loads (sc1), which are served by the reader's L2.  When every
+// member of the group runs on the same XCD (checked at launch start, see
+// agree_placement), writers use workgroup-scope stores, which land in that shared L2
+// and are seen by the readers' sc1 loads without a trip to HBM (about 2x faster);
+// otherwise writers use device-scope stores (written through to memory), which every
+// XCD sees.  Either way a word is accepted only when its tag names the awaited step.
+__device__ __forceinline__ void tag_put(unsigned long long* p, float v, unsigned tag, bool xcd_local) {
+  const unsigned long long w = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(v);
+  if (xcd_local)
+    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  else
+    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned xcc_id() {
+  unsigned x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return x;
+}
+
+// Within-wave ordering of LDS writes before reads by other lanes of the same wave.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Every workgroup of the group publishes its XCD id (device-scope) and reads all of
+// the group's; returns true when they are all equal.  All members see the same words,
+// so they all choose the same store mode.  Returns false and sets *abort on timeout.
+__device__ bool agree_placement(unsigned long long* hello, int wg, int nw, long long spin, int* abort_flag,
+                                int* err) {
+  __shared__ int differs;
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    differs = 0;
+    tag_put(hello + wg, __uint_as_float(xcc_id()), 1u, false);
+  }
+  __syncthreads();
+  if (tid < nw) {
+    const long long t0 = wall_clock64();
+    unsigned long long w;
+    while (true) {
+      w = tag_load(hello + tid);
+      if (tag_of(w) == 1u) break;
+      if (wall_clock64() - t0 > spin) {
+        *abort_flag = 1;
+        atomicOr(err, 1);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (__float_as_uint(val_of(w)) != xcc_id()) differs = 1;
+  }
+  __syncthreads();
+  return differs == 0;
+}
+
 struct PFwdArgs {
   const float* gih;
   const float* w_hh;
@@ -228,166 +287,163 @@ struct PFwdArgs {
   float* c_save;
   float* gact;
   float* tanh_c;
-  unsigned long long* xbuf;  // [2][NG][4][Hp]
+  unsigned long long* xbuf;   // [2][NG][4][Hp] h words
+  unsigned long long* hello;  // [NG][NWMAX]
   int* err;
-  int T, B, H, Hp, NG, Bg;
+  int T, B, H, Hp, NG, NGX, Bg, NW;
+  int device_scope;  // 1: never use the XCD-local stores
   long long spin;
 };
 
-// Waits until every word p[j] (valid[j]) carries `tag`; returns false on timeout.
-template <int PER>
-__device__ __forceinline__ bool wait_words(const unsigned long long* const (&p)[PER], const bool (&valid)[PER],
-                                           unsigned tag, float (&out)[PER], long long spin) {
-  bool ok[PER];
-  unsigned long long w[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    ok[j] = !valid[j];
-    w[j] = 0ull;
-  }
-  const long long t0 = wall_clock64();
-  while (true) {
-#pragma unroll
-    for (int j = 0; j < PER; ++j)
-      if (!ok[j]) w[j] = tag_load(p[j]);
-    bool all = true;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      ok[j] = ok[j] || tag_of(w[j]) == tag;
-      all = all && ok[j];
-    }
-    if (all) break;
-    if (wall_clock64() - t0 > spin) return false;
-    __builtin_amdgcn_s_sleep(1);
-  }
-#pragma unroll
-  for (int j = 0; j < PER; ++j) out[j] = valid[j] ? val_of(w[j]) : 0.f;
-  return true;
-}
-
+// Forward.  Wave q multiplies the q-th quarter of k (KQ values).  h_{t-1} of a quarter
+// comes from NS = KQ/16 source workgroups (16 units each); the wave issues the loads
+// for all of them, then consumes the sources in order, each as soon as its 64 words
+// (4 batch rows x 16 units, one per lane) carry the awaited tag, so the MFMAs of early
+// sources overlap the wait for late ones.  One workgroup barrier per step joins the
+// four k-quarters; wave q then runs the cell for batch slot q (lanes 0-15 = units).
 template <int KQ>
 __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
-  constexpr int HP = 4 * KQ;         // padded hidden size
-  constexpr int PER = HP / 64;       // exchange words per thread (4*HP / 256)
-  __shared__ float hl[4][HP + 4];    // h_{t-1} of the group's batch rows
-  __shared__ float red[4][4][64];    // [wave][batch][row] partial products
-  __shared__ float act[4][64];       // [batch][row] gate activations
+  constexpr int HP = 4 * KQ;
+  constexpr int NS = KQ / kUnits;
+  __shared__ float hq[4][4][KQ + 4];   // [wave][batch slot][k within the quarter]
+  __shared__ float red[2][4][4][64];   // [step parity][wave][batch slot][gate row]
   __shared__ int abort_flag;
 
   const int T = p.T, B = p.B, H = p.H, NG = p.NG, Bg = p.Bg;
-  const int grp = blockIdx.x % NG, wg = blockIdx.x / NG;
+  const int grp = blockIdx.x % p.NGX, wg = blockIdx.x / p.NGX;
+  if (grp >= NG) return;  // unused XCD slot (groups are padded to a multiple of 8)
   const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
-  const int gate = lane >> 4, uu = lane & 15, u = wg * kUnits + uu;
-  const bool row_ok = u < H;
-  const int n = gate * H + u;  // this lane's gate row (same mapping in every phase)
-
   if (tid == 0) abort_flag = 0;
+  const bool fast = agree_placement(p.hello + (size_t)grp * (HP / kUnits), wg, p.NW, p.spin, &abort_flag, p.err) &&
+                    !p.device_scope;
+  if (abort_flag) return;
 
-  // a-scaled W_hh slice: lane = gate row, registers = this wave's quarter of k.
-  const float ag = p.a[gate];
+  // a-scaled W_hh slice: lane = gate row (gate lane/16, unit lane%16), registers = k quarter
+  const int rgate = lane >> 4, ru = wg * kUnits + (lane & 15);
+  const bool row_ok = ru < H;
+  const int n = rgate * H + ru;
   float wreg[KQ];
+  {
+    const float ag = p.a[rgate];
 #pragma unroll
-  for (int kk = 0; kk < KQ; ++kk) {
-    const int k = q * KQ + kk;
-    wreg[kk] = (row_ok && k < H) ? ag * p.w_hh[(size_t)n * H + k] : 0.f;
+    for (int kk = 0; kk < KQ; ++kk) {
+      const int k = q * KQ + kk;
+      wreg[kk] = (row_ok && k < H) ? ag * p.w_hh[(size_t)n * H + k] : 0.f;
+    }
   }
-  const float bs = row_ok ? ag * p.b_hh[n] : 0.f;
 
-  // phase-D thread -> (batch slot q, row lane); cell thread (tid < 64) -> (batch slot, unit)
-  const int bd = grp * Bg + q;
-  const bool d_ok = row_ok && q < Bg && bd < B;
-  const int ci = tid >> 4, cu = wg * kUnits + (tid & 15), cb = grp * Bg + ci;
-  const bool c_ok = tid < 64 && ci < Bg && cb < B && cu < H;
+  // cell thread: wave q, lane < 16 -> (batch slot q, unit cu)
+  const int cb = grp * Bg + q, cu = wg * kUnits + (lane & 15);
+  const bool c_ok = lane < kUnits && q < Bg && cb < B && cu < H;
+  float bs[4] = {0.f, 0.f, 0.f, 0.f};
   float c_reg = 0.f;
   if (c_ok) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) bs[g] = p.a[g] * p.b_hh[g * H + cu];
     const size_t bu = (size_t)cb * H + cu;
     c_reg = p.c0[bu];
     p.h_save[bu] = p.h0[bu];
     p.c_save[bu] = c_reg;
   }
 
-  // exchange words this thread gathers each step: (batch slot, k)
-  const unsigned long long* wp[PER];
-  bool wv[PER];
-  int wi[PER], wk[PER];
+  // receive words: source j of this wave's quarter, lane -> (batch slot wi, unit wk)
+  const int wi = lane >> 4, wkk = lane & 15, wb = grp * Bg + wi;
+  const unsigned long long* wp[NS];
+  bool wv[NS];
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int idx = tid + 256 * j;
-    wi[j] = idx / HP;
-    wk[j] = idx % HP;
-    const int b = grp * Bg + wi[j];
-    wv[j] = wi[j] < Bg && b < B && wk[j] < H;
-    wp[j] = nullptr;
+  for (int j = 0; j < NS; ++j) {
+    const int k = (q * NS + j) * kUnits + wkk;
+    wv[j] = wi < Bg && wb < B && k < H;
+    wp[j] = p.xbuf + ((size_t)grp * 4 + wi) * HP + k;  // + slot offset per step
   }
-  __syncthreads();
+  const size_t slot_words = (size_t)NG * 4 * HP;
+  const size_t plane = (size_t)B * H;
 
   for (int t = 0; t < T; ++t) {
-    // this step's input-gate value for phase D (independent of h: issue early)
-    const float gi = d_ok ? p.gih[((size_t)t * B + bd) * 4 * H + n] : 0.f;
-
-    // ---- gather h_{t-1} -------------------------------------------------------------
-    if (t == 0) {
+    float gi[4] = {0.f, 0.f, 0.f, 0.f};
+    if (c_ok) {
+      const float* g = p.gih + ((size_t)t * B + cb) * 4 * H + cu;
 #pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        const int b = grp * Bg + wi[j];
-        hl[wi[j]][wk[j]] = wv[j] ? p.h0[(size_t)b * H + wk[j]] : 0.f;
-      }
-    } else {
-      const int slot = (t - 1) & 1;
-#pragma unroll
-      for (int j = 0; j < PER; ++j)
-        wp[j] = p.xbuf + (((size_t)slot * NG + grp) * 4 + wi[j]) * HP + wk[j];
-      float v[PER];
-      if (!wait_words<PER>(wp, wv, (unsigned)t, v, p.spin)) {
-        abort_flag = 1;
-        atomicOr(p.err, 1);
-      }
-#pragma unroll
-      for (int j = 0; j < PER; ++j) hl[wi[j]][wk[j]] = v[j];
+      for (int gt = 0; gt < 4; ++gt) gi[gt] = g[gt * H];
     }
-    __syncthreads();
-    if (abort_flag) return;
 
-    // ---- z-partials: 4 batch rows x 64 gate rows over this wave's k quarter ------------
     f4 acc[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
-    const float* hrow = &hl[lane & 3][q * KQ];
+    const float* hrow = &hq[q][lane & 3][0];
+    if (t == 0) {
 #pragma unroll
-    for (int kk = 0; kk < KQ; kk += 4) {
-      const f4 hv = *reinterpret_cast<const f4*>(hrow + kk);
+      for (int j = 0; j < NS; ++j) {
+        const int k = (q * NS + j) * kUnits + wkk;
+        hq[q][wi][j * kUnits + wkk] = wv[j] ? p.h0[(size_t)wb * H + k] : 0.f;
+      }
+      wave_sync();
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[c] = __builtin_amdgcn_mfma_f32_4x4x1f32(hv[c], wreg[kk + c], acc[c], 4, 0, 0);
+      for (int kk = 0; kk < KQ; kk += 4) {
+        const f4 hv = *reinterpret_cast<const f4*>(hrow + kk);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] = __builtin_amdgcn_mfma_f32_4x4x1f32(hv[c], wreg[kk + c], acc[c], 4, 0, 0);
+      }
+    } else {
+      const size_t off = (size_t)((t - 1) & 1) * slot_words;
+      const unsigned tag = (unsigned)t;
+      unsigned long long w[NS];
+#pragma unroll
+      for (int j = 0; j < NS; ++j) w[j] = wv[j] ? tag_load(wp[j] + off) : 0ull;
+      const long long t0 = wall_clock64();
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        while (true) {
+          const bool okj = !wv[j] || tag_of(w[j]) == tag;
+          if (__all(okj)) break;
+          if (wall_clock64() - t0 > p.spin) {
+            abort_flag = 1;
+            atomicOr(p.err, 1);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+          for (int jj = j; jj < NS; ++jj)
+            if (wv[jj] && tag_of(w[jj]) != tag) w[jj] = tag_load(wp[jj] + off);
+        }
+        hq[q][wi][j * kUnits + wkk] = wv[j] ? val_of(w[j]) : 0.f;
+        wave_sync();
+#pragma unroll
+        for (int kk = j * kUnits; kk < (j + 1) * kUnits; kk += 4) {
+          const f4 hv = *reinterpret_cast<const f4*>(hrow + kk);
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            acc[c] = __builtin_amdgcn_mfma_f32_4x4x1f32(hv[c], wreg[kk + c], acc[c], 4, 0, 0);
+        }
+      }
     }
     const f4 zs = (acc[0] + acc[1]) + (acc[2] + acc[3]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[q][i][lane] = zs[i];
+    for (int i = 0; i < 4; ++i) red[t & 1][q][i][lane] = zs[i];
     __syncthreads();
+    if (abort_flag) return;
 
-    // ---- activations: thread (batch slot q, row lane) ------------------------------
-    {
-      const float mm = (red[0][q][lane] + red[1][q][lane]) + (red[2][q][lane] + red[3][q][lane]);
-      const float z = (gi + mm) + bs;
-      const float s = sigmoid_f(z);
-      act[q][lane] = s;
-      if (d_ok) p.gact[((size_t)t * B + bd) * 4 * H + n] = s;
-    }
-    __syncthreads();
-
-    // ---- cell update + publish h_t --------------------------------------------------
     if (c_ok) {
-      const int cuu = tid & 15;
-      const float ig = act[ci][cuu], fg = act[ci][16 + cuu], gg = act[ci][32 + cuu], og = act[ci][48 + cuu];
-      const float c = fg * c_reg + ig * gg;
+      const int uu = lane & 15;
+      float act[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r = g * kUnits + uu;
+        const float mm = (red[t & 1][0][q][r] + red[t & 1][1][q][r]) + (red[t & 1][2][q][r] + red[t & 1][3][q][r]);
+        act[g] = sigmoid_f((gi[g] + mm) + bs[g]);
+      }
+      const float c = act[1] * c_reg + act[0] * act[2];
       const float tc = tanh_f(c);
-      const float h = og * tc;
+      const float h = act[3] * tc;
       c_reg = c;
-      tag_store(p.xbuf + (((size_t)(t & 1) * NG + grp) * 4 + ci) * HP + cu, h, (unsigned)(t + 1));
+      tag_put(p.xbuf + (size_t)(t & 1) * slot_words + ((size_t)grp * 4 + q) * HP + cu, h, (unsigned)(t + 1), fast);
       const size_t bu = (size_t)cb * H + cu;
-      const size_t plane = (size_t)B * H;
       p.h_save[(size_t)(t + 1) * plane + bu] = h;
       p.c_save[(size_t)(t + 1) * plane + bu] = c;
       p.tanh_c[(size_t)t * plane + bu] = tc;
+      float* ga = p.gact + ((size_t)t * B + cb) * 4 * H + cu;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) ga[g * H] = act[g];
     }
   }
 }
@@ -405,27 +461,37 @@ struct PBwdArgs {
   double* db_part;  // [B][4H]
   float* dh0;
   float* dc0;
-  unsigned long long* pbuf;  // [2][NG][NW][4][Hp]
+  unsigned long long* pbuf;   // [2][NG][NWMAX][4][Hp] partial-dh words
+  unsigned long long* hello;  // [NG][NWMAX]
   int* err;
-  int T, B, H, Hp, NG, Bg, NW;
+  int T, B, H, Hp, NG, NGX, Bg, NW;
+  int device_scope;
   long long spin;
 };
 
+// Backward.  Wave q owns batch slot q for the dh receive and the cell, and the q-th
+// quarter of the columns for the partial product.  A lane of wave q gathers the
+// partials of sources m, m+4, m+8, ... (m = lane/16) for unit lane%16, adds them in
+// that order, and two cross-lane shuffles finish the fixed-order sum, so the
+// receive needs no LDS and no barrier.  One workgroup barrier per step publishes the
+// step's dgates (double-buffered in LDS) to the four column quarters.
 template <int KQ>
 __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
   constexpr int HP = 4 * KQ;
   constexpr int CG = (KQ + 63) / 64;     // 64-column groups per wave
   constexpr int NWMAX = HP / kUnits;     // workgroups per group at most
-  constexpr int PER = NWMAX * 64 / 256;  // exchange words per thread
-  static_assert(PER >= 1, "at least one word per thread");
-  __shared__ float dgl[4][64 + 4];       // this step's dgates of the 64 rows, per batch slot
-  __shared__ float prl[NWMAX][4][kUnits];
+  constexpr int PER = (NWMAX + 3) / 4;   // partials gathered per lane
+  __shared__ float dgl[2][4][64 + 4];    // [step parity][batch slot][gate row]
   __shared__ int abort_flag;
 
   const int T = p.T, B = p.B, H = p.H, NG = p.NG, Bg = p.Bg, NW = p.NW;
-  const int grp = blockIdx.x % NG, wg = blockIdx.x / NG;
+  const int grp = blockIdx.x % p.NGX, wg = blockIdx.x / p.NGX;
+  if (grp >= NG) return;
   const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
   if (tid == 0) abort_flag = 0;
+  const bool fast = agree_placement(p.hello + (size_t)grp * NWMAX, wg, NW, p.spin, &abort_flag, p.err) &&
+                    !p.device_scope;
+  if (abort_flag) return;
 
   // W_s columns owned by this lane: col = q*KQ + cg*64 + lane; registers over the 64 rows.
   float wreg[CG][64];
@@ -443,33 +509,29 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
     }
   }
 
-  // cell thread (tid < 64) -> (batch slot ci, unit cu)
-  const int ci = tid >> 4, cuu = tid & 15, cu = wg * kUnits + cuu, cb = grp * Bg + ci;
-  const bool c_ok = tid < 64 && ci < Bg && cb < B && cu < H;
+  // cell thread: wave q, lane < 16 -> (batch slot q, unit cu)
+  const int uu = lane & 15, cu = wg * kUnits + uu, cb = grp * Bg + q;
+  const bool c_ok = lane < kUnits && q < Bg && cb < B && cu < H;
   float dc = 0.f;
   double dbacc[4] = {0.0, 0.0, 0.0, 0.0};
   if (c_ok) dc = p.dc_n[(size_t)cb * H + cu];
 
-  // exchange words gathered each step: (source workgroup, batch slot, unit)
+  // receive words: source m + 4j, batch slot q, column cu
+  const int m = lane >> 4;
+  const bool r_ok = q < Bg && cb < B && cu < H;
   const unsigned long long* wp[PER];
   bool wv[PER];
-  int ws_[PER], wi[PER], wu[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const int idx = tid + 256 * j;
-    ws_[j] = idx / 64;
-    wi[j] = (idx / kUnits) % 4;
-    wu[j] = idx % kUnits;
-    const int b = grp * Bg + wi[j], u = wg * kUnits + wu[j];
-    wv[j] = ws_[j] < NW && wi[j] < Bg && b < B && u < H;
-    wp[j] = nullptr;
+    const int src = m + 4 * j;
+    wv[j] = r_ok && src < NW;
+    wp[j] = p.pbuf + (((size_t)grp * NWMAX + (src < NWMAX ? src : 0)) * 4 + q) * HP + cu;
   }
-  __syncthreads();
-
+  const size_t slot_words = (size_t)NG * NWMAX * 4 * HP;
   const size_t plane = (size_t)B * H;
+
   for (int s = 0; s <= T; ++s) {
     const int t = T - 1 - s;
-    // prefetch this step's saved values (cell threads)
     float dout_v = 0.f, cp = 0.f, ig = 0.f, fg = 0.f, gg = 0.f, og = 0.f, tc = 0.f;
     if (c_ok && s < T) {
       const size_t bu = (size_t)cb * H + cu;
@@ -483,28 +545,38 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
       og = ga[3 * H];
     }
 
-    // ---- dh for this step: dh_n, or the sum of the partials published last step ------
+    // ---- dh: dh_n, or the fixed-order sum of last step's partials ------------------
     float dh = 0.f;
     if (s == 0) {
       if (c_ok) dh = p.dh_n[(size_t)cb * H + cu];
     } else {
-      const int slot = (s - 1) & 1;
+      const size_t off = (size_t)((s - 1) & 1) * slot_words;
+      const unsigned tag = (unsigned)s;
+      unsigned long long w[PER];
 #pragma unroll
-      for (int j = 0; j < PER; ++j)
-        wp[j] = p.pbuf + ((((size_t)slot * NG + grp) * NWMAX + ws_[j]) * 4 + wi[j]) * HP + wg * kUnits + wu[j];
-      float v[PER];
-      if (!wait_words<PER>(wp, wv, (unsigned)s, v, p.spin)) {
-        abort_flag = 1;
-        atomicOr(p.err, 1);
-      }
+      for (int j = 0; j < PER; ++j) w[j] = wv[j] ? tag_load(wp[j] + off) : 0ull;
+      const long long t0 = wall_clock64();
+      while (true) {
+        bool ok = true;
 #pragma unroll
-      for (int j = 0; j < PER; ++j)
-        if (ws_[j] < NWMAX) prl[ws_[j]][wi[j]][wu[j]] = v[j];
-      __syncthreads();
-      if (abort_flag) return;
-      if (c_ok) {
-        for (int w = 0; w < NW; ++w) dh += prl[w][ci][cuu];
+        for (int j = 0; j < PER; ++j) ok = ok && (!wv[j] || tag_of(w[j]) == tag);
+        if (__all(ok)) break;
+        if (wall_clock64() - t0 > p.spin) {
+          abort_flag = 1;
+          atomicOr(p.err, 1);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+          if (wv[j] && tag_of(w[j]) != tag) w[j] = tag_load(wp[j] + off);
       }
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) part += wv[j] ? val_of(w[j]) : 0.f;
+      part += __shfl_xor(part, 16);
+      part += __shfl_xor(part, 32);
+      dh = part;
     }
     if (s == T) {  // dh is now the gradient w.r.t. h0
       if (c_ok) {
@@ -517,8 +589,8 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
       return;
     }
 
-    // ---- cell backward -----------------------------------------------------------
-    if (tid < 64) {
+    // ---- cell backward (wave q: batch slot q) ----------------------------------------
+    if (lane < kUnits) {
       float d[4] = {0.f, 0.f, 0.f, 0.f};
       if (c_ok) {
         dh = dh + dout_v;
@@ -531,12 +603,13 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
         }
       }
 #pragma unroll
-      for (int gt = 0; gt < 4; ++gt) dgl[ci][gt * 16 + cuu] = d[gt];
+      for (int gt = 0; gt < 4; ++gt) dgl[s & 1][q][gt * kUnits + uu] = d[gt];
     }
     __syncthreads();
+    if (abort_flag) return;
 
-    // ---- partial dh_{t-1}[batch][col] = sum over this workgroup's 64 rows -----------
-    const float* drow = &dgl[lane & 3][0];
+    // ---- partial dh_{t-1}[batch][col] over this workgroup's 64 rows ------------------
+    const float* drow = &dgl[s & 1][lane & 3][0];
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) {
       f4 acc[4];
@@ -550,12 +623,10 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
       }
       const f4 part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
       if (col_ok[cg]) {
+        unsigned long long* dst = p.pbuf + (size_t)(s & 1) * slot_words + ((size_t)grp * NWMAX + wg) * 4 * HP + col[cg];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (i < Bg && grp * Bg + i < B)
-            tag_store(p.pbuf + ((((size_t)(s & 1) * NG + grp) * NWMAX + wg) * 4 + i) * HP + col[cg], part[i],
-                      (unsigned)(s + 1));
-        }
+        for (int i = 0; i < 4; ++i)
+          if (i < Bg && grp * Bg + i < B) tag_put(dst + (size_t)i * HP, part[i], (unsigned)(s + 1), fast);
       }
     }
   }
@@ -566,7 +637,7 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
 // ---------------------------------------------------------------------------------
 struct PersistentPlan {
   bool ok = false;
-  int KQ = 0, Hp = 0, NG = 0, Bg = 0, NW = 0, grid = 0;
+  int KQ = 0, Hp = 0, NG = 0, NGX = 0, Bg = 0, NW = 0, grid = 0;
 };
 
 int pick_kq(int H) {
@@ -598,8 +669,11 @@ int plan_persistent(int B, int H, bool bwd, PersistentPlan* pl) {
   p.Hp = 4 * kq;
   p.NG = (B + 3) / 4;
   p.Bg = (B + p.NG - 1) / p.NG;
+  // group g is served by workgroups blockIdx % NGX == g; NGX is a multiple of the XCD
+  // count so that every group sits on one XCD (workgroup i runs on XCD i % 8)
+  p.NGX = (p.NG + di.num_xcds - 1) / di.num_xcds * di.num_xcds;
   p.NW = (H + kUnits - 1) / kUnits;
-  p.grid = p.NG * p.NW;
+  p.grid = p.NGX * p.NW;
   int occ = 0;
   switch (kq) {
     case 16: HSL_CHECK(bwd ? max_resident(rec_bwd_persistent<16>, &occ) : max_resident(rec_fwd_persistent<16>, &occ)); break;
@@ -638,7 +712,8 @@ int copy_f32_impl(float* dst, const float* src, size_t n, hipStream_t s) {
 struct FwdWs {
   int* err;
   float* gih;                // [T*B*4H]
-  unsigned long long* xbuf;  // [2*NG*4*Hp] (persistent)
+  unsigned long long* xbuf;  // [2*NG*4*Hp] + hello [NG*Hp/16] (persistent)
+  unsigned long long* hello;
   float* w_perm;             // [4H*H]      (per-step)
   float* bs;                 // [4H]        (per-step)
   size_t words;
@@ -650,8 +725,10 @@ size_t carve_fwd(void* ws, size_t cap, int T, int B, int H, FwdWs* o) {
   o->gih = c.take<float>((size_t)T * B * 4 * H);
   const int kq = pick_kq(H);
   const size_t ng = (size_t)(B + 3) / 4;
-  o->words = kq ? 2 * ng * 4 * (size_t)(4 * kq) : 0;
+  const size_t hello = kq ? ng * (size_t)(4 * kq / kUnits) : 0;
+  o->words = kq ? 2 * ng * 4 * (size_t)(4 * kq) + hello : 0;
   o->xbuf = c.take<unsigned long long>(o->words);
+  o->hello = o->xbuf ? o->xbuf + (o->words - hello) : nullptr;
   o->w_perm = c.take<float>((size_t)4 * H * H);
   o->bs = c.take<float>((size_t)4 * H);
   return c.off;
@@ -664,7 +741,8 @@ struct BwdWs {
   double* rowdot;            // [4H]
   float* dc;                 // [B*H]   (per-step)
   float* w_s;                // [4H*H]  (per-step)
-  unsigned long long* pbuf;  // [2*NG*NWMAX*4*Hp] (persistent)
+  unsigned long long* pbuf;  // [2*NG*NWMAX*4*Hp] + hello [NG*NWMAX] (persistent)
+  unsigned long long* hello;
   size_t words;
   float* gemm;               // shared by the weight-gradient GEMMs
   size_t gemm_bytes;
@@ -693,8 +771,10 @@ size_t carve_bwd(void* ws, size_t cap, int T, int B, int D, int H, BwdWs* o) {
   o->w_s = c.take<float>((size_t)4 * H * H);
   const int kq = pick_kq(H);
   const size_t ng = (size_t)(B + 3) / 4;
-  o->words = kq ? 2 * ng * (size_t)(4 * kq / kUnits) * 4 * (size_t)(4 * kq) : 0;
+  const size_t hello = kq ? ng * (size_t)(4 * kq / kUnits) : 0;
+  o->words = kq ? 2 * ng * (size_t)(4 * kq / kUnits) * 4 * (size_t)(4 * kq) + hello : 0;
   o->pbuf = c.take<unsigned long long>(o->words);
+  o->hello = o->pbuf ? o->pbuf + (o->words - hello) : nullptr;
   o->gemm_bytes = gemm_region_bytes(T, B, D, H);
   o->gemm = c.take<float>(o->gemm_bytes / sizeof(float) + 1);
   return c.off;
@@ -774,8 +854,8 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
 
   if (pl.ok) {
     HSL_CHECK(zero_words(w.xbuf, w.words, s));
-    PFwdArgs pa{w.gih, w_hh, b_hh, a, h0, c0, h_save, c_save, gact, tanh_c, w.xbuf, w.err,
-                T, B, H, pl.Hp, pl.NG, pl.Bg, spin_timeout_ticks()};
+    PFwdArgs pa{w.gih, w_hh, b_hh, a, h0, c0, h_save, c_save, gact, tanh_c, w.xbuf, w.hello, w.err,
+                T, B, H, pl.Hp, pl.NG, pl.NGX, pl.Bg, pl.NW, exchange_scope_mode(), spin_timeout_ticks()};
     const int slot = timing_begin(kTimeRecFwd, s);
     switch (pl.KQ) {
       case 16: launch_fwd_persistent<16>(pa, pl.grid, s); break;
@@ -859,8 +939,8 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
 
   if (pl.ok) {
     HSL_CHECK(zero_words(w.pbuf, w.words, s));
-    PBwdArgs pa{dout, dh_n, dc_n, c_save, gact, tanh_c, w_hh, a, w.dgates, w.db_part, dh0, dc0, w.pbuf, w.err,
-                T, B, H, pl.Hp, pl.NG, pl.Bg, pl.NW, spin_timeout_ticks()};
+    PBwdArgs pa{dout, dh_n, dc_n, c_save, gact, tanh_c, w_hh, a, w.dgates, w.db_part, dh0, dc0, w.pbuf, w.hello,
+                w.err, T, B, H, pl.Hp, pl.NG, pl.NGX, pl.Bg, pl.NW, exchange_scope_mode(), spin_timeout_ticks()};
     const int slot = timing_begin(kTimeRecBwd, s);
     switch (pl.KQ) {
       case 16: launch_bwd_persistent<16>(pa, pl.grid, s); break;

@@ -25,6 +25,7 @@ def _debug():
     yield
     functional.debug_checks(False)
     prlstm_amd.set_recurrent_path(0)
+    prlstm_amd.set_exchange_scope(0)
 
 
 def _run_ref(m, x, hx, wts):
@@ -137,6 +138,13 @@ def test_config1(dev, path):
 def test_config2_headline(dev):
     """T256 B32 D256 H512 (persistent path, as benchmarked)."""
     check(256, 32, 256, 512, dev, 2)
+
+
+@pytest.mark.parametrize("shape", [(12, 5, 16, 40), (128, 32, 256, 256)])
+def test_device_scope_exchange(dev, shape):
+    """The persistent kernels' device-scope hand-off (used when a batch group spans XCDs)."""
+    prlstm_amd.set_exchange_scope(1)
+    check(*shape, dev, 2, a=[0.6, 0.2, 0.9, 0.4])
 
 
 def test_config2_nonlinear_a(dev):

@@ -276,6 +276,30 @@ __device__ bool agree_placement(unsigned long long* hello, int wg, int nw, long 
   return differs == 0;
 }
 
+// v_mfma_f32_4x4x1_16b_f32 with the A operand of block `kk` (lanes 4kk..4kk+3)
+// broadcast to all 16 blocks.  kk is a compile-time constant at every call site after
+// unrolling, so the switch folds to one instruction.
+__device__ __forceinline__ f4 mfma4_bcast(float a, float b, f4 c, int kk) {
+  switch (kk) {
+    case 0: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 0, 0);
+    case 1: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 1, 0);
+    case 2: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 2, 0);
+    case 3: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 3, 0);
+    case 4: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 4, 0);
+    case 5: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 5, 0);
+    case 6: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 6, 0);
+    case 7: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 7, 0);
+    case 8: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 8, 0);
+    case 9: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 9, 0);
+    case 10: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 10, 0);
+    case 11: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 11, 0);
+    case 12: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 12, 0);
+    case 13: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 13, 0);
+    case 14: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 14, 0);
+    default: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, 15, 0);
+  }
+}
+
 struct PFwdArgs {
   const float* gih;
   const float* w_hh;
@@ -296,17 +320,18 @@ struct PFwdArgs {
 };
 
 // Forward.  Wave q multiplies the q-th quarter of k (KQ values).  h_{t-1} of a quarter
-// comes from NS = KQ/16 source workgroups (16 units each); the wave issues the loads
-// for all of them, then consumes the sources in order, each as soon as its 64 words
-// (4 batch rows x 16 units, one per lane) carry the awaited tag, so the MFMAs of early
-// sources overlap the wait for late ones.  One workgroup barrier per step joins the
-// four k-quarters; wave q then runs the cell for batch slot q (lanes 0-15 = units).
+// comes from NS = KQ/16 source workgroups (16 units each).  Lane l polls the word of
+// batch slot l%4 and unit l/4 of every source (all loads in flight together, reloading
+// only the words whose tag is still old), then the 16 MFMAs of source j read their A
+// operand straight from the polled registers: with cbsz=4, abid=kk broadcasts lanes
+// 4kk..4kk+3, i.e. h[0..3][unit kk], to all 16 blocks.  One workgroup barrier per
+// step joins the four k-quarters; wave q then runs the cell for batch slot q
+// (lanes 0-15 = units).
 template <int KQ>
 __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
   constexpr int HP = 4 * KQ;
   constexpr int NS = KQ / kUnits;
-  __shared__ float hq[4][4][KQ + 4];   // [wave][batch slot][k within the quarter]
-  __shared__ float red[2][4][4][64];   // [step parity][wave][batch slot][gate row]
+  __shared__ f4 red[2][4][64];         // [step parity][batch slot][gate row] -> 4 wave partials
   __shared__ int abort_flag;
 
   const int T = p.T, B = p.B, H = p.H, NG = p.NG, Bg = p.Bg;
@@ -346,8 +371,8 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
     p.c_save[bu] = c_reg;
   }
 
-  // receive words: source j of this wave's quarter, lane -> (batch slot wi, unit wk)
-  const int wi = lane >> 4, wkk = lane & 15, wb = grp * Bg + wi;
+  // receive words: source j of this wave's quarter, lane -> (batch slot lane%4, unit lane/4)
+  const int wi = lane & 3, wkk = lane >> 2, wb = grp * Bg + wi;
   const unsigned long long* wp[NS];
   bool wv[NS];
 #pragma unroll
@@ -367,22 +392,12 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
       for (int gt = 0; gt < 4; ++gt) gi[gt] = g[gt * H];
     }
 
-    f4 acc[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
-    const float* hrow = &hq[q][lane & 3][0];
+    float hv[NS];
     if (t == 0) {
 #pragma unroll
       for (int j = 0; j < NS; ++j) {
         const int k = (q * NS + j) * kUnits + wkk;
-        hq[q][wi][j * kUnits + wkk] = wv[j] ? p.h0[(size_t)wb * H + k] : 0.f;
-      }
-      wave_sync();
-#pragma unroll
-      for (int kk = 0; kk < KQ; kk += 4) {
-        const f4 hv = *reinterpret_cast<const f4*>(hrow + kk);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] = __builtin_amdgcn_mfma_f32_4x4x1f32(hv[c], wreg[kk + c], acc[c], 4, 0, 0);
+        hv[j] = wv[j] ? p.h0[(size_t)wb * H + k] : 0.f;
       }
     } else {
       const size_t off = (size_t)((t - 1) & 1) * slot_words;
@@ -391,35 +406,34 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
 #pragma unroll
       for (int j = 0; j < NS; ++j) w[j] = wv[j] ? tag_load(wp[j] + off) : 0ull;
       const long long t0 = wall_clock64();
+      while (true) {
+        bool ok = true;
 #pragma unroll
-      for (int j = 0; j < NS; ++j) {
-        while (true) {
-          const bool okj = !wv[j] || tag_of(w[j]) == tag;
-          if (__all(okj)) break;
-          if (wall_clock64() - t0 > p.spin) {
-            abort_flag = 1;
-            atomicOr(p.err, 1);
-            break;
-          }
-          __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-          for (int jj = j; jj < NS; ++jj)
-            if (wv[jj] && tag_of(w[jj]) != tag) w[jj] = tag_load(wp[jj] + off);
+        for (int j = 0; j < NS; ++j) ok = ok && (!wv[j] || tag_of(w[j]) == tag);
+        if (__all(ok)) break;
+        if (wall_clock64() - t0 > p.spin) {
+          abort_flag = 1;
+          atomicOr(p.err, 1);
+          break;
         }
-        hq[q][wi][j * kUnits + wkk] = wv[j] ? val_of(w[j]) : 0.f;
-        wave_sync();
 #pragma unroll
-        for (int kk = j * kUnits; kk < (j + 1) * kUnits; kk += 4) {
-          const f4 hv = *reinterpret_cast<const f4*>(hrow + kk);
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            acc[c] = __builtin_amdgcn_mfma_f32_4x4x1f32(hv[c], wreg[kk + c], acc[c], 4, 0, 0);
-        }
+        for (int j = 0; j < NS; ++j)
+          if (wv[j] && tag_of(w[j]) != tag) w[j] = tag_load(wp[j] + off);
       }
-    }
-    const f4 zs = (acc[0] + acc[1]) + (acc[2] + acc[3]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[t & 1][q][i][lane] = zs[i];
+      for (int j = 0; j < NS; ++j) hv[j] = wv[j] ? val_of(w[j]) : 0.f;
+    }
+    f4 acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
+#pragma unroll
+      for (int kk = 0; kk < kUnits; ++kk)
+        acc[kk & 7] = mfma4_bcast(hv[j], wreg[j * kUnits + kk], acc[kk & 7], kk);
+    const f4 zs = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) reinterpret_cast<float*>(&red[t & 1][i][lane])[q] = zs[i];
     __syncthreads();
     if (abort_flag) return;
 
@@ -428,8 +442,8 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
       float act[4];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int r = g * kUnits + uu;
-        const float mm = (red[t & 1][0][q][r] + red[t & 1][1][q][r]) + (red[t & 1][2][q][r] + red[t & 1][3][q][r]);
+        const f4 pr = red[t & 1][q][g * kUnits + uu];
+        const float mm = (pr[0] + pr[1]) + (pr[2] + pr[3]);
         act[g] = sigmoid_f((gi[g] + mm) + bs[g]);
       }
       const float c = act[1] * c_reg + act[0] * act[2];
@@ -609,19 +623,21 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
     if (abort_flag) return;
 
     // ---- partial dh_{t-1}[batch][col] over this workgroup's 64 rows ------------------
-    const float* drow = &dgl[s & 1][lane & 3][0];
+    // lane l holds dgates of batch slot l%4 for rows 4(l/4)..4(l/4)+3; the MFMA for row
+    // r = 4kk+c broadcasts register c of lanes 4kk..4kk+3 (abid = kk).
+    const f4 dv = *reinterpret_cast<const f4*>(&dgl[s & 1][lane & 3][4 * (lane >> 2)]);
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) {
-      f4 acc[4];
+      f4 acc[8];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < 8; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 64; r += 4) {
-        const f4 dv = *reinterpret_cast<const f4*>(drow + r);
+      for (int kk = 0; kk < 16; ++kk) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] = __builtin_amdgcn_mfma_f32_4x4x1f32(dv[c], wreg[cg][r + c], acc[c], 4, 0, 0);
+        for (int c = 0; c < 4; ++c)
+          acc[(kk & 1) * 4 + c] = mfma4_bcast(dv[c], wreg[cg][4 * kk + c], acc[(kk & 1) * 4 + c], kk);
       }
-      const f4 part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      const f4 part = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
       if (col_ok[cg]) {
         unsigned long long* dst = p.pbuf + (size_t)(s & 1) * slot_words + ((size_t)grp * NWMAX + wg) * 4 * HP + col[cg];
 #pragma unroll

@@ -3,13 +3,15 @@
 // Split-K writes fp32 partial tiles [splits][M][N] and a second kernel adds them in
 // fp64 (plus the bias), so long reductions (K = T*B up to 65536 for the weight
 // gradients) lose less accuracy than one fp32 running sum.
-#include "gemm_core.h"
+#include "gemm2_core.h"
 
 namespace hsl {
 
 using CfgBig = GemmCfg<128, 128, 32, 2, 2, 1>;
 using CfgMid = GemmCfg<64, 64, 32, 2, 2, 1>;
 using CfgSmall = GemmCfg<32, 32, 32, 1, 1, 4>;
+// fp64-accumulating products with both sides >= 64 use the double-buffered core.
+using Cfg2Acc = Gemm2Cfg<64, 64, 32, true>;
 
 namespace {
 
@@ -65,8 +67,28 @@ int dispatch(Tile t, const GemmArgs& g, int ta, int tb, int splits, const Epi& e
   }
 }
 
-int actual_splits(Tile t, int K, int splits) {
+bool use_v2(const GemmDesc& d) { return d.acc64 && d.M >= 64 && d.N >= 64; }
+
+int dispatch_v2(const GemmDesc& d, float* partial, int splits, hipStream_t s, int* used) {
+  const int vec_a = aligned16(d.A) && d.lda % 4 == 0, vec_b = aligned16(d.B) && d.ldb % 4 == 0;
+  if (!d.trans_a && !d.trans_b)
+    return launch_gemm2<Cfg2Acc, false, false>(d.A, d.B, d.bias, d.C, partial, d.M, d.N, d.K, d.lda, d.ldb, d.ldc,
+                                               splits, vec_a, vec_b, s, used);
+  if (!d.trans_a && d.trans_b)
+    return launch_gemm2<Cfg2Acc, false, true>(d.A, d.B, d.bias, d.C, partial, d.M, d.N, d.K, d.lda, d.ldb, d.ldc,
+                                              splits, vec_a, vec_b, s, used);
+  if (d.trans_a && !d.trans_b)
+    return launch_gemm2<Cfg2Acc, true, false>(d.A, d.B, d.bias, d.C, partial, d.M, d.N, d.K, d.lda, d.ldb, d.ldc,
+                                              splits, vec_a, vec_b, s, used);
+  return launch_gemm2<Cfg2Acc, true, true>(d.A, d.B, d.bias, d.C, partial, d.M, d.N, d.K, d.lda, d.ldb, d.ldc,
+                                           splits, vec_a, vec_b, s, used);
+}
+
+// Number of k-slices the chosen kernel really launches for a requested split count.
+int actual_splits(const GemmDesc& d, Tile t, int splits) {
   int kps;
+  const int K = d.K;
+  if (use_v2(d)) return gemm2_split_layout<Cfg2Acc>(K, splits, &kps);
   switch (t) {
     case Tile::Big: return split_layout<CfgBig>(K, splits, &kps);
     case Tile::Mid: return split_layout<CfgMid>(K, splits, &kps);
@@ -118,8 +140,9 @@ size_t gemm_ws_bytes(int M, int N, int K, int acc64) {
 
 int gemm_partials(const GemmDesc& d, float* partials, int splits, hipStream_t s, int* used) {
   HSL_CHECK(check_desc(d));
+  if (use_v2(d)) return dispatch_v2(d, partials, splits, s, used);
   const Tile t = pick_tile(d.M, d.N, d.acc64);
-  *used = actual_splits(t, d.K, splits);
+  *used = actual_splits(d, t, splits);
   EpiPartial epi{partials, d.M, d.N};
   return dispatch(t, make_args(d), d.trans_a, d.trans_b, *used, epi, s, d.acc64);
 }
@@ -129,16 +152,22 @@ int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s) {
   if (d.M == 0 || d.N == 0) return HSL_OK;
   const Tile t = pick_tile(d.M, d.N, d.acc64);
   int splits = gemm_pick_splits(d.M, d.N, d.K, d.acc64);
-  if (splits > 1) splits = actual_splits(t, d.K, splits);
+  if (splits > 1) splits = actual_splits(d, t, splits);
   const size_t need = sizeof(float) * (size_t)splits * d.M * d.N;
   if (splits > 1 && (ws == nullptr || ws_bytes < need)) splits = 1;
-  if (splits == 1) {
+  float* P = static_cast<float*>(ws);
+  if (use_v2(d)) {
+    int used = 1;
+    HSL_CHECK(dispatch_v2(d, splits > 1 ? P : nullptr, splits, s, &used));
+    if (splits == 1) return HSL_OK;
+    splits = used;
+  } else if (splits == 1) {
     EpiStore epi{d.C, d.bias, d.M, d.N, d.ldc};
     return dispatch(t, make_args(d), d.trans_a, d.trans_b, 1, epi, s, d.acc64);
+  } else {
+    EpiPartial epi{P, d.M, d.N};
+    HSL_CHECK(dispatch(t, make_args(d), d.trans_a, d.trans_b, splits, epi, s, d.acc64));
   }
-  float* P = static_cast<float*>(ws);
-  EpiPartial epi{P, d.M, d.N};
-  HSL_CHECK(dispatch(t, make_args(d), d.trans_a, d.trans_b, splits, epi, s, d.acc64));
   const size_t total = (size_t)d.M * d.N;
   int blocks = (int)((total + 255) / 256);
   if (blocks > 4096) blocks = 4096;

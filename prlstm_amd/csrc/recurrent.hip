@@ -36,9 +36,9 @@ constexpr int kPadLdsBytes = 96 * 1024;  // dynamic LDS that keeps one persisten
 // ---------------------------------------------------------------------------------
 // small helper kernels
 // ---------------------------------------------------------------------------------
-__global__ void zero_u64_kernel(unsigned long long* p, size_t n) {
+__global__ void fill_u64_kernel(unsigned long long* p, size_t n, unsigned long long v) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-    p[i] = 0ull;
+    p[i] = v;
 }
 
 __global__ void copy_f32_kernel(float* dst, const float* src, size_t n) {
@@ -217,25 +217,125 @@ struct EpiCellBwd {
 // ---------------------------------------------------------------------------------
 // persistent path
 // ---------------------------------------------------------------------------------
-// Hand-off between the workgroups of a batch group.  Readers always poll with
-// relaxed device-scope loads (sc1), which are served by the reader's L2.  When every
-// member of the group runs on the same XCD (checked at launch start, see
-// agree_placement), writers use workgroup-scope stores, which land in that shared L2
-// and are seen by the readers' sc1 loads without a trip to HBM (about 2x faster);
-// otherwise writers use device-scope stores (written through to memory), which every
-// XCD sees.  Either way a word is accepted only when its tag names the awaited step.
-__device__ __forceinline__ void tag_put(unsigned long long* p, float v, unsigned tag, bool xcd_local) {
-  const unsigned long long w = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(v);
+// Hand-off between the workgroups of a batch group.  Values travel as 4-byte words in
+// rotating slots that start out holding kEmpty, a NaN pattern that no result takes
+// (results are NaN-canonicalised before they are published), so a word is ready as
+// soon as it differs from kEmpty.  A word is set back to kEmpty by the lane that owns
+// it once every reader is known to be done with it, and written again only slots
+// later; see the two kernels for the exact schedule.
+//
+// Readers poll with relaxed device-scope loads (sc1), which are served by the reader's
+// L2.  When every member of the group runs on the same XCD (checked at launch start,
+// see agree_placement), writers use workgroup-scope stores, which land in that shared
+// L2; a store's completion, which every later poll of the writing wave waits for, then
+// means it is visible to the whole group.  Otherwise writers use device-scope stores
+// and each step adds a device-scope release before its publish and an acquire after
+// its receive (write-back and invalidation of the XCD's L2).
+constexpr unsigned kEmpty = 0xFFFFFFFFu;
+
+__device__ __forceinline__ float canon_nan(float v) { return v == v ? v : __uint_as_float(0x7FC00000u); }
+
+__device__ __forceinline__ void word_put(float* p, float v, bool xcd_local) {
+  unsigned* u = reinterpret_cast<unsigned*>(p);
   if (xcd_local)
-    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_store(u, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   else
-    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(u, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A lane's N (1, 2, 4 or 8) words inside a block of 64 lanes: with N == 1 word 0 of
+// lane l is at l; otherwise word j is at 128*(j/2) + 2*l + j%2, so a lane's words pair
+// up into 8-byte loads and stores and the 64 lanes of a pair are contiguous.
+template <int N>
+__device__ __forceinline__ int lane_word(int l, int j) {
+  if constexpr (N == 1)
+    return l;
+  else
+    return 128 * (j >> 1) + 2 * l + (j & 1);
+}
+
+// p = block + lane_word<N>(lane, 0).
+template <int N>
+__device__ __forceinline__ void words_clear(float* p, bool xcd_local) {
+  if constexpr (N == 1) {
+    word_put(p, __uint_as_float(kEmpty), xcd_local);
+  } else {
+    const unsigned long long e = ~0ull;
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      unsigned long long* u = reinterpret_cast<unsigned long long*>(p + 128 * i);
+      if (xcd_local)
+        __hip_atomic_store(u, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      else
+        __hip_atomic_store(u, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// Loads the lane's words whose flag in `need` is set (pairs are loaded together).
+template <int N>
+__device__ __forceinline__ void words_load(const float* p, const bool (&need)[N], unsigned (&v)[N]) {
+  if constexpr (N == 1) {
+    if (need[0])
+      v[0] = __hip_atomic_load(reinterpret_cast<unsigned*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      if (need[2 * i] || need[2 * i + 1]) {
+        const unsigned long long w =
+            __hip_atomic_load(reinterpret_cast<unsigned long long*>(const_cast<float*>(p + 128 * i)),
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v[2 * i] = static_cast<unsigned>(w);
+        v[2 * i + 1] = static_cast<unsigned>(w >> 32);
+      }
+    }
+  }
+}
+
+// Polls the lane's words until every word flagged in `expect` differs from kEmpty.
+// Returns false (after setting the error flags) when the spin limit runs out.
+template <int N>
+__device__ __forceinline__ bool words_wait(const float* p, const bool (&expect)[N], unsigned (&v)[N], long long spin,
+                                           int* abort_flag, int* err) {
+  bool need[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    need[j] = expect[j];
+    v[j] = 0u;
+  }
+  words_load<N>(p, need, v);
+  const long long t0 = wall_clock64();
+  while (true) {
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      need[j] = expect[j] && v[j] == kEmpty;
+      ok = ok && !need[j];
+    }
+    if (__all(ok)) return true;
+    if (wall_clock64() - t0 > spin) {
+      *abort_flag = 1;
+      atomicOr(err, 1);
+      return false;
+    }
+    words_load<N>(p, need, v);
+  }
 }
 
 __device__ __forceinline__ unsigned xcc_id() {
   unsigned x;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
   return x;
+}
+
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also waits for
+// the wave's outstanding global loads and stores; the persistent kernels keep those
+// in flight across the barrier on purpose.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Within-wave ordering of LDS writes before reads by other lanes of the same wave.
@@ -254,7 +354,7 @@ __device__ bool agree_placement(unsigned long long* hello, int wg, int nw, long 
   const int tid = threadIdx.x;
   if (tid == 0) {
     differs = 0;
-    tag_put(hello + wg, __uint_as_float(xcc_id()), 1u, false);
+    tag_store(hello + wg, __uint_as_float(xcc_id()), 1u);
   }
   __syncthreads();
   if (tid < nw) {
@@ -311,7 +411,7 @@ struct PFwdArgs {
   float* c_save;
   float* gact;
   float* tanh_c;
-  unsigned long long* xbuf;   // [2][NG][4][Hp] h words
+  float* xbuf;                // [4 slots][NG][4 quarters][64 lanes x KQ/16 words] h words
   unsigned long long* hello;  // [NG][NWMAX]
   int* err;
   int T, B, H, Hp, NG, NGX, Bg, NW;
@@ -320,17 +420,26 @@ struct PFwdArgs {
 };
 
 // Forward.  Wave q multiplies the q-th quarter of k (KQ values).  h_{t-1} of a quarter
-// comes from NS = KQ/16 source workgroups (16 units each).  Lane l polls the word of
-// batch slot l%4 and unit l/4 of every source (all loads in flight together, reloading
-// only the words whose tag is still old), then the 16 MFMAs of source j read their A
-// operand straight from the polled registers: with cbsz=4, abid=kk broadcasts lanes
-// 4kk..4kk+3, i.e. h[0..3][unit kk], to all 16 blocks.  One workgroup barrier per
-// step joins the four k-quarters; wave q then runs the cell for batch slot q
-// (lanes 0-15 = units).
+// comes from NS = KQ/16 source workgroups (16 units each).  Lane l of wave q needs
+// h[batch slot l%4][unit q*KQ + 16j + l/4] for j < NS; these NS words form the lane's
+// part of a 64-lane block (lane_word), so the receive is NS/2 8-byte loads per lane.  The 16 MFMAs of
+// source j then read their A operand straight from the received registers: with
+// cbsz=4, abid=kk broadcasts lanes 4kk..4kk+3, i.e. h[0..3][unit kk], to all 16
+// blocks.  One workgroup barrier per step joins the four k-quarters; wave q then runs
+// the cell for batch slot q (lanes 0-15 = units).
+//
+// Slots: h_t goes to slot t%4.  After its publish in step t, the owner of a word clears
+// it in slot (t+2)%4 (h_{t-2}).  By then the four waves together have received h_{t-1}
+// from every workgroup of the group, each of which published it after reading h_{t-2}
+// (a single wave has heard only from the sources of its quarter, which is why the
+// clear comes after the barrier).  The clear completes before the owner's next receive
+// does, hence before it publishes h_{t+1}; a reader of h_{t+2} has seen h_{t+1} first,
+// so it sees the clear or h_{t+2}, never h_{t-2}.
 template <int KQ>
 __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
   constexpr int HP = 4 * KQ;
   constexpr int NS = KQ / kUnits;
+  constexpr int GW = 4 * HP;           // words per group and slot
   __shared__ f4 red[2][4][64];         // [step parity][batch slot][gate row] -> 4 wave partials
   __shared__ int abort_flag;
 
@@ -349,11 +458,14 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
   const int n = rgate * H + ru;
   float wreg[KQ];
   {
+    // unconditional loads at clamped addresses, so that all of them are in flight at once
     const float ag = p.a[rgate];
+    const float* wrow = p.w_hh + (size_t)(row_ok ? n : 0) * H;
 #pragma unroll
     for (int kk = 0; kk < KQ; ++kk) {
       const int k = q * KQ + kk;
-      wreg[kk] = (row_ok && k < H) ? ag * p.w_hh[(size_t)n * H + k] : 0.f;
+      const float v = wrow[k < H ? k : H - 1];
+      wreg[kk] = (row_ok && k < H) ? ag * v : 0.f;
     }
   }
 
@@ -365,63 +477,64 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
   if (c_ok) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) bs[g] = p.a[g] * p.b_hh[g * H + cu];
-    const size_t bu = (size_t)cb * H + cu;
-    c_reg = p.c0[bu];
-    p.h_save[bu] = p.h0[bu];
-    p.c_save[bu] = c_reg;
+    const size_t b0 = (size_t)cb * H + cu;
+    c_reg = p.c0[b0];
+    p.h_save[b0] = p.h0[b0];
+    p.c_save[b0] = c_reg;
   }
 
-  // receive words: source j of this wave's quarter, lane -> (batch slot lane%4, unit lane/4)
+  // receive: word j of lane l, wave q at block xbuf[slot][grp][q], lane_word(l, j)
   const int wi = lane & 3, wkk = lane >> 2, wb = grp * Bg + wi;
-  const unsigned long long* wp[NS];
   bool wv[NS];
 #pragma unroll
-  for (int j = 0; j < NS; ++j) {
-    const int k = (q * NS + j) * kUnits + wkk;
-    wv[j] = wi < Bg && wb < B && k < H;
-    wp[j] = p.xbuf + ((size_t)grp * 4 + wi) * HP + k;  // + slot offset per step
-  }
-  const size_t slot_words = (size_t)NG * 4 * HP;
+  for (int j = 0; j < NS; ++j) wv[j] = wi < Bg && wb < B && (q * NS + j) * kUnits + wkk < H;
+  const size_t slot_words = (size_t)NG * GW;
+  const float* rbase = p.xbuf + (size_t)grp * GW + (size_t)q * 64 * NS + lane_word<NS>(lane, 0);
+  // publish: the word of (batch slot q, unit cu) is read by lane 4*(cu%16) + q of wave
+  // cu/KQ, as its word (cu%KQ)/16
+  float* wbase = p.xbuf + (size_t)grp * GW + (size_t)(cu / KQ) * 64 * NS +
+                 lane_word<NS>(4 * (cu & 15) + q, (cu % KQ) / kUnits);
   const size_t plane = (size_t)B * H;
+  const size_t bu = (size_t)cb * H + cu;
 
-  for (int t = 0; t < T; ++t) {
-    float gi[4] = {0.f, 0.f, 0.f, 0.f};
-    if (c_ok) {
-      const float* g = p.gih + ((size_t)t * B + cb) * 4 * H + cu;
+  // Memory traffic of a step is placed so that no wait for it lands between the
+  // receive and the publish: the input-projection row of step t+1 is requested right
+  // after step t's receive (two register sets alternate, so no copy waits for it) and
+  // is forced into registers at the top of step t+1, by when it has long arrived; the
+  // saved activations and the slot clear are stored after the publish.  All of them
+  // have completed once the next receive has (one in-order completion counter).
+  float giA[4] = {0.f, 0.f, 0.f, 0.f}, giB[4] = {0.f, 0.f, 0.f, 0.f};
+  if (c_ok) {
 #pragma unroll
-      for (int gt = 0; gt < 4; ++gt) gi[gt] = g[gt * H];
-    }
+    for (int gt = 0; gt < 4; ++gt) giA[gt] = p.gih[(size_t)cb * 4 * H + gt * H + cu];
+  }
 
+  // One step; gi holds this step's projection row, gn receives the next one.  Returns
+  // false when the group aborted.
+  auto step = [&](int t, float (&gi)[4], float (&gn)[4]) __attribute__((always_inline)) -> bool {
+    asm volatile("" : "+v"(gi[0]), "+v"(gi[1]), "+v"(gi[2]), "+v"(gi[3]));
     float hv[NS];
     if (t == 0) {
 #pragma unroll
       for (int j = 0; j < NS; ++j) {
         const int k = (q * NS + j) * kUnits + wkk;
         hv[j] = wv[j] ? p.h0[(size_t)wb * H + k] : 0.f;
+        asm volatile("" : "+v"(hv[j]));  // wait here, not after the loads below
       }
     } else {
-      const size_t off = (size_t)((t - 1) & 1) * slot_words;
-      const unsigned tag = (unsigned)t;
-      unsigned long long w[NS];
+      unsigned v[NS];
+      words_wait<NS>(rbase + (size_t)((t - 1) & 3) * slot_words, wv, v, p.spin, &abort_flag, p.err);
+      if (!fast) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 #pragma unroll
-      for (int j = 0; j < NS; ++j) w[j] = wv[j] ? tag_load(wp[j] + off) : 0ull;
-      const long long t0 = wall_clock64();
-      while (true) {
-        bool ok = true;
-#pragma unroll
-        for (int j = 0; j < NS; ++j) ok = ok && (!wv[j] || tag_of(w[j]) == tag);
-        if (__all(ok)) break;
-        if (wall_clock64() - t0 > p.spin) {
-          abort_flag = 1;
-          atomicOr(p.err, 1);
-          break;
-        }
-#pragma unroll
-        for (int j = 0; j < NS; ++j)
-          if (wv[j] && tag_of(w[j]) != tag) w[j] = tag_load(wp[j] + off);
+      for (int j = 0; j < NS; ++j) {
+        hv[j] = wv[j] ? __uint_as_float(v[j]) : 0.f;
+        asm volatile("" : "+v"(hv[j]));  // settled before the loads below are issued
       }
+    }
+    if (c_ok && t + 1 < T) {
+      const float* g = p.gih + ((size_t)(t + 1) * B + cb) * 4 * H + cu;
 #pragma unroll
-      for (int j = 0; j < NS; ++j) hv[j] = wv[j] ? val_of(w[j]) : 0.f;
+      for (int gt = 0; gt < 4; ++gt) gn[gt] = g[gt * H];
     }
     f4 acc[8];
 #pragma unroll
@@ -434,8 +547,8 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
     const f4 zs = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
 #pragma unroll
     for (int i = 0; i < 4; ++i) reinterpret_cast<float*>(&red[t & 1][i][lane])[q] = zs[i];
-    __syncthreads();
-    if (abort_flag) return;
+    lds_barrier();
+    if (abort_flag) return false;
 
     if (c_ok) {
       const int uu = lane & 15;
@@ -450,15 +563,22 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
       const float tc = tanh_f(c);
       const float h = act[3] * tc;
       c_reg = c;
-      tag_put(p.xbuf + (size_t)(t & 1) * slot_words + ((size_t)grp * 4 + q) * HP + cu, h, (unsigned)(t + 1), fast);
-      const size_t bu = (size_t)cb * H + cu;
+      if (!fast) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      word_put(wbase + (size_t)(t & 3) * slot_words, canon_nan(h), fast);
       p.h_save[(size_t)(t + 1) * plane + bu] = h;
       p.c_save[(size_t)(t + 1) * plane + bu] = c;
       p.tanh_c[(size_t)t * plane + bu] = tc;
       float* ga = p.gact + ((size_t)t * B + cb) * 4 * H + cu;
 #pragma unroll
       for (int g = 0; g < 4; ++g) ga[g * H] = act[g];
+      word_put(wbase + (size_t)((t + 2) & 3) * slot_words, __uint_as_float(kEmpty), fast);
     }
+    return true;
+  };
+
+  for (int t = 0; t < T; t += 2) {
+    if (!step(t, giA, giB)) return;
+    if (t + 1 < T && !step(t + 1, giB, giA)) return;
   }
 }
 
@@ -475,7 +595,7 @@ struct PBwdArgs {
   double* db_part;  // [B][4H]
   float* dh0;
   float* dc0;
-  unsigned long long* pbuf;   // [2][NG][NWMAX][4][Hp] partial-dh words
+  float* pbuf;                // [3 slots][NG][NWMAX readers][4 batch slots][64 lanes x PER words] partials
   unsigned long long* hello;  // [NG][NWMAX]
   int* err;
   int T, B, H, Hp, NG, NGX, Bg, NW;
@@ -487,14 +607,21 @@ struct PBwdArgs {
 // quarter of the columns for the partial product.  A lane of wave q gathers the
 // partials of sources m, m+4, m+8, ... (m = lane/16) for unit lane%16, adds them in
 // that order, and two cross-lane shuffles finish the fixed-order sum, so the
-// receive needs no LDS and no barrier.  One workgroup barrier per step publishes the
-// step's dgates (double-buffered in LDS) to the four column quarters.
+// receive needs no LDS and no barrier.  A lane's PER partials form its part of a
+// 64-lane block (lane_word).  One workgroup barrier per step publishes the step's dgates
+// (double-buffered in LDS) to the four column quarters.
+//
+// Slots: the partials published in step s go to slot s%3 and have exactly one reader,
+// which clears them right after its receive in step s+1.  They are written again in
+// step s+3, by a writer that has by then received the reader's step-s+2 partials; the
+// reader publishes those only after its step-s+2 receive, which waits for the clear.
 template <int KQ>
 __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
   constexpr int HP = 4 * KQ;
   constexpr int CG = (KQ + 63) / 64;     // 64-column groups per wave
   constexpr int NWMAX = HP / kUnits;     // workgroups per group at most
   constexpr int PER = (NWMAX + 3) / 4;   // partials gathered per lane
+  constexpr int RW = 4 * 64 * PER;       // words per reader workgroup and slot
   __shared__ float dgl[2][4][64 + 4];    // [step parity][batch slot][gate row]
   __shared__ int abort_flag;
 
@@ -511,15 +638,25 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
   float wreg[CG][64];
   int col[CG];
   bool col_ok[CG];
+  float av[4];
+#pragma unroll
+  for (int gt = 0; gt < 4; ++gt) av[gt] = p.a[gt];
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg) {
     const int cl = cg * 64 + lane;
     col[cg] = q * KQ + cl;
     col_ok[cg] = cl < KQ && col[cg] < H;
+    const int cc = col_ok[cg] ? col[cg] : 0;  // clamped: every load is issued unconditionally
+#pragma unroll
+    for (int r = 0; r < 64; ++r) {
+      const int u = wg * kUnits + (r & 15);
+      wreg[cg][r] = p.w_hh[(size_t)((r >> 4) * H + (u < H ? u : H - 1)) * H + cc];
+    }
 #pragma unroll
     for (int r = 0; r < 64; ++r) {
       const int gt = r >> 4, u = wg * kUnits + (r & 15);
-      wreg[cg][r] = (col_ok[cg] && u < H) ? p.a[gt] * p.w_hh[(size_t)(gt * H + u) * H + col[cg]] : 0.f;
+      asm volatile("" : "+v"(wreg[cg][r]));  // keeps the loads above out of the conditional
+      wreg[cg][r] = (col_ok[cg] && u < H) ? av[gt] * wreg[cg][r] : 0.f;
     }
   }
 
@@ -530,102 +667,101 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
   double dbacc[4] = {0.0, 0.0, 0.0, 0.0};
   if (c_ok) dc = p.dc_n[(size_t)cb * H + cu];
 
-  // receive words: source m + 4j, batch slot q, column cu
+  // receive words: partial j of lane l (source l/16 + 4j, batch slot q, column cu) at
+  // block pbuf[slot][grp][wg][q], lane_word(l, j)
   const int m = lane >> 4;
   const bool r_ok = q < Bg && cb < B && cu < H;
-  const unsigned long long* wp[PER];
   bool wv[PER];
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int src = m + 4 * j;
-    wv[j] = r_ok && src < NW;
-    wp[j] = p.pbuf + (((size_t)grp * NWMAX + (src < NWMAX ? src : 0)) * 4 + q) * HP + cu;
-  }
-  const size_t slot_words = (size_t)NG * NWMAX * 4 * HP;
+  for (int j = 0; j < PER; ++j) wv[j] = r_ok && m + 4 * j < NW;
+  const size_t slot_words = (size_t)NG * NWMAX * RW;
+  float* const rbase = p.pbuf + ((size_t)grp * NWMAX + wg) * RW + (size_t)q * 64 * PER + lane_word<PER>(lane, 0);
+  // publish: the partial of column c for batch slot i goes to reader workgroup c/16,
+  // wave i, lane 16*(wg%4) + c%16, word wg/4
+  float* const pbase = p.pbuf + (size_t)grp * NWMAX * RW + lane_word<PER>(16 * (wg & 3), wg >> 2);
   const size_t plane = (size_t)B * H;
 
-  for (int s = 0; s <= T; ++s) {
+  // Memory traffic of a step is placed so that no wait for it lands between the
+  // receive and the publish: the saved activations of step t-1 are requested right
+  // after step t's receive (two register sets alternate, so no copy waits for them)
+  // and forced into registers at the top of the next step, by when they have long
+  // arrived; dgates and the slot clear are stored after the cell.  All of them have
+  // completed once the next receive has (one in-order completion counter).
+  const size_t bu = (size_t)cb * H + cu;
+  auto load_step = [&](int ts, float (&nx)[7]) {  // dout, c_prev, tanh_c, i, f, g, o
+    nx[0] = p.dout[(size_t)ts * plane + bu];
+    nx[1] = p.c_save[(size_t)ts * plane + bu];
+    nx[2] = p.tanh_c[(size_t)ts * plane + bu];
+    const float* ga = p.gact + ((size_t)ts * B + cb) * 4 * H + cu;
+#pragma unroll
+    for (int gt = 0; gt < 4; ++gt) nx[3 + gt] = ga[gt * H];
+  };
+  float nxA[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, nxB[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (c_ok && T > 0) load_step(T - 1, nxA);
+
+  // Step s (time t = T-1-s) with its activations in cur; the next step's go to nxt.
+  // Returns false when done (s == T) or when the group aborted.
+  auto step = [&](int s, float (&cur)[7], float (&nxt)[7]) __attribute__((always_inline)) -> bool {
+    asm volatile("" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]), "+v"(cur[5]),
+                 "+v"(cur[6]));
     const int t = T - 1 - s;
-    float dout_v = 0.f, cp = 0.f, ig = 0.f, fg = 0.f, gg = 0.f, og = 0.f, tc = 0.f;
-    if (c_ok && s < T) {
-      const size_t bu = (size_t)cb * H + cu;
-      dout_v = p.dout[(size_t)t * plane + bu];
-      cp = p.c_save[(size_t)t * plane + bu];
-      tc = p.tanh_c[(size_t)t * plane + bu];
-      const float* ga = p.gact + ((size_t)t * B + cb) * 4 * H + cu;
-      ig = ga[0];
-      fg = ga[H];
-      gg = ga[2 * H];
-      og = ga[3 * H];
-    }
 
     // ---- dh: dh_n, or the fixed-order sum of last step's partials ------------------
     float dh = 0.f;
+    float* src = nullptr;
     if (s == 0) {
       if (c_ok) dh = p.dh_n[(size_t)cb * H + cu];
+      asm volatile("" : "+v"(dh));
     } else {
-      const size_t off = (size_t)((s - 1) & 1) * slot_words;
-      const unsigned tag = (unsigned)s;
-      unsigned long long w[PER];
-#pragma unroll
-      for (int j = 0; j < PER; ++j) w[j] = wv[j] ? tag_load(wp[j] + off) : 0ull;
-      const long long t0 = wall_clock64();
-      while (true) {
-        bool ok = true;
-#pragma unroll
-        for (int j = 0; j < PER; ++j) ok = ok && (!wv[j] || tag_of(w[j]) == tag);
-        if (__all(ok)) break;
-        if (wall_clock64() - t0 > p.spin) {
-          abort_flag = 1;
-          atomicOr(p.err, 1);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-        for (int j = 0; j < PER; ++j)
-          if (wv[j] && tag_of(w[j]) != tag) w[j] = tag_load(wp[j] + off);
-      }
+      src = rbase + (size_t)((s - 1) % 3) * slot_words;
+      unsigned v[PER];
+      words_wait<PER>(src, wv, v, p.spin, &abort_flag, p.err);
+      if (!fast) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       float part = 0.f;
 #pragma unroll
-      for (int j = 0; j < PER; ++j) part += wv[j] ? val_of(w[j]) : 0.f;
+      for (int j = 0; j < PER; ++j) part += wv[j] ? __uint_as_float(v[j]) : 0.f;
       part += __shfl_xor(part, 16);
       part += __shfl_xor(part, 32);
       dh = part;
+      asm volatile("" : "+v"(dh));  // settled before the loads below are issued
     }
     if (s == T) {  // dh is now the gradient w.r.t. h0
       if (c_ok) {
-        const size_t bu = (size_t)cb * H + cu;
         if (p.dh0) p.dh0[bu] = dh;
         if (p.dc0) p.dc0[bu] = dc;
 #pragma unroll
         for (int gt = 0; gt < 4; ++gt) p.db_part[(size_t)cb * 4 * H + gt * H + cu] = dbacc[gt];
       }
-      return;
+      return false;
     }
+    if (c_ok && s + 1 < T) load_step(t - 1, nxt);
 
     // ---- cell backward (wave q: batch slot q) ----------------------------------------
-    if (lane < kUnits) {
-      float d[4] = {0.f, 0.f, 0.f, 0.f};
-      if (c_ok) {
-        dh = dh + dout_v;
-        cell_bwd(dh, dc, cp, ig, fg, gg, og, tc, d);
-        float* dgp = p.dgates + ((size_t)t * B + cb) * 4 * H + cu;
+    float d[4] = {0.f, 0.f, 0.f, 0.f};
+    if (c_ok) {
+      dh = dh + cur[0];
+      cell_bwd(dh, dc, cur[1], cur[3], cur[4], cur[5], cur[6], cur[2], d);
 #pragma unroll
-        for (int gt = 0; gt < 4; ++gt) {
-          dgp[gt * H] = d[gt];
-          dbacc[gt] += (double)d[gt];
-        }
-      }
+      for (int gt = 0; gt < 4; ++gt) dbacc[gt] += (double)d[gt];
+    }
+    if (lane < kUnits) {
 #pragma unroll
       for (int gt = 0; gt < 4; ++gt) dgl[s & 1][q][gt * kUnits + uu] = d[gt];
     }
-    __syncthreads();
-    if (abort_flag) return;
+    if (src) words_clear<PER>(src, fast);
+    if (c_ok) {
+      float* dgp = p.dgates + ((size_t)t * B + cb) * 4 * H + cu;
+#pragma unroll
+      for (int gt = 0; gt < 4; ++gt) dgp[gt * H] = d[gt];
+    }
+    lds_barrier();
+    if (abort_flag) return false;
 
     // ---- partial dh_{t-1}[batch][col] over this workgroup's 64 rows ------------------
     // lane l holds dgates of batch slot l%4 for rows 4(l/4)..4(l/4)+3; the MFMA for row
     // r = 4kk+c broadcasts register c of lanes 4kk..4kk+3 (abid = kk).
     const f4 dv = *reinterpret_cast<const f4*>(&dgl[s & 1][lane & 3][4 * (lane >> 2)]);
+    if (!fast) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) {
       f4 acc[8];
@@ -639,12 +775,19 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
       }
       const f4 part = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
       if (col_ok[cg]) {
-        unsigned long long* dst = p.pbuf + (size_t)(s & 1) * slot_words + ((size_t)grp * NWMAX + wg) * 4 * HP + col[cg];
+        const int c = col[cg];
+        float* dst = pbase + (size_t)(s % 3) * slot_words + (size_t)(c >> 4) * RW + (PER == 1 ? 1 : 2) * (c & 15);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (i < Bg && grp * Bg + i < B) tag_put(dst + (size_t)i * HP, part[i], (unsigned)(s + 1), fast);
+          if (i < Bg && grp * Bg + i < B) word_put(dst + (size_t)i * 64 * PER, canon_nan(part[i]), fast);
       }
     }
+    return true;
+  };
+
+  for (int s = 0; s <= T; s += 2) {
+    if (!step(s, nxA, nxB)) return;
+    if (!step(s + 1, nxB, nxA)) return;
   }
 }
 
@@ -710,11 +853,16 @@ inline int grid_for(size_t n) {
   return (int)b;
 }
 
-int zero_words_impl(unsigned long long* p, size_t n, hipStream_t s) {
+int fill_words(unsigned long long* p, size_t n, unsigned long long v, hipStream_t s) {
   if (n == 0) return HSL_OK;
-  hipLaunchKernelGGL(zero_u64_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, n);
+  hipLaunchKernelGGL(fill_u64_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, n, v);
   HSL_HIP(hipGetLastError());
   return HSL_OK;
+}
+
+// Hand-off slots start out empty (every 4-byte word kEmpty).
+int clear_slots(float* p, size_t floats, hipStream_t s) {
+  return fill_words(reinterpret_cast<unsigned long long*>(p), (floats + 1) / 2, ~0ull, s);
 }
 
 int copy_f32_impl(float* dst, const float* src, size_t n, hipStream_t s) {
@@ -727,12 +875,13 @@ int copy_f32_impl(float* dst, const float* src, size_t n, hipStream_t s) {
 // Workspace layouts.  The int error flag sits at offset 0 of both.
 struct FwdWs {
   int* err;
-  float* gih;                // [T*B*4H]
-  unsigned long long* xbuf;  // [2*NG*4*Hp] + hello [NG*Hp/16] (persistent)
-  unsigned long long* hello;
-  float* w_perm;             // [4H*H]      (per-step)
-  float* bs;                 // [4H]        (per-step)
-  size_t words;
+  float* gih;                 // [T*B*4H]
+  float* xbuf;                // [4*NG*4*Hp] (persistent)
+  size_t xfloats;
+  unsigned long long* hello;  // [NG*Hp/16]  (persistent)
+  size_t hwords;
+  float* w_perm;              // [4H*H]      (per-step)
+  float* bs;                  // [4H]        (per-step)
 };
 
 size_t carve_fwd(void* ws, size_t cap, int T, int B, int H, FwdWs* o) {
@@ -741,10 +890,10 @@ size_t carve_fwd(void* ws, size_t cap, int T, int B, int H, FwdWs* o) {
   o->gih = c.take<float>((size_t)T * B * 4 * H);
   const int kq = pick_kq(H);
   const size_t ng = (size_t)(B + 3) / 4;
-  const size_t hello = kq ? ng * (size_t)(4 * kq / kUnits) : 0;
-  o->words = kq ? 2 * ng * 4 * (size_t)(4 * kq) + hello : 0;
-  o->xbuf = c.take<unsigned long long>(o->words);
-  o->hello = o->xbuf ? o->xbuf + (o->words - hello) : nullptr;
+  o->hwords = kq ? ng * (size_t)(4 * kq / kUnits) : 0;
+  o->xfloats = kq ? 4 * ng * 4 * (size_t)(4 * kq) : 0;
+  o->xbuf = c.take<float>(o->xfloats);
+  o->hello = c.take<unsigned long long>(o->hwords);
   o->w_perm = c.take<float>((size_t)4 * H * H);
   o->bs = c.take<float>((size_t)4 * H);
   return c.off;
@@ -757,9 +906,10 @@ struct BwdWs {
   double* rowdot;            // [4H]
   float* dc;                 // [B*H]   (per-step)
   float* w_s;                // [4H*H]  (per-step)
-  unsigned long long* pbuf;  // [2*NG*NWMAX*4*Hp] + hello [NG*NWMAX] (persistent)
-  unsigned long long* hello;
-  size_t words;
+  float* pbuf;                // [3*NG*NWMAX*4*64*PER] (persistent)
+  size_t pfloats;
+  unsigned long long* hello;  // [NG*NWMAX]           (persistent)
+  size_t hwords;
   float* gemm;               // shared by the weight-gradient GEMMs
   size_t gemm_bytes;
 };
@@ -787,10 +937,12 @@ size_t carve_bwd(void* ws, size_t cap, int T, int B, int D, int H, BwdWs* o) {
   o->w_s = c.take<float>((size_t)4 * H * H);
   const int kq = pick_kq(H);
   const size_t ng = (size_t)(B + 3) / 4;
-  const size_t hello = kq ? ng * (size_t)(4 * kq / kUnits) : 0;
-  o->words = kq ? 2 * ng * (size_t)(4 * kq / kUnits) * 4 * (size_t)(4 * kq) + hello : 0;
-  o->pbuf = c.take<unsigned long long>(o->words);
-  o->hello = o->pbuf ? o->pbuf + (o->words - hello) : nullptr;
+  const size_t nwmax = kq ? (size_t)(4 * kq / kUnits) : 0;
+  const size_t per = (nwmax + 3) / 4;
+  o->hwords = ng * nwmax;
+  o->pfloats = 3 * ng * nwmax * 4 * 64 * per;
+  o->pbuf = c.take<float>(o->pfloats);
+  o->hello = c.take<unsigned long long>(o->hwords);
   o->gemm_bytes = gemm_region_bytes(T, B, D, H);
   o->gemm = c.take<float>(o->gemm_bytes / sizeof(float) + 1);
   return c.off;
@@ -814,7 +966,7 @@ void launch_bwd_persistent(const PBwdArgs& a, int grid, hipStream_t s) {
 
 }  // namespace
 
-int zero_words(unsigned long long* p, size_t n, hipStream_t s) { return zero_words_impl(p, n, s); }
+int zero_words(unsigned long long* p, size_t n, hipStream_t s) { return fill_words(p, n, 0ull, s); }
 int copy_f32(float* dst, const float* src, size_t n, hipStream_t s) { return copy_f32_impl(dst, src, n, s); }
 
 int bias_grads_from_parts(const double* db_part, int B, const double* rowdot, const float* b_hh, const float* a,
@@ -869,7 +1021,8 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
   timing_end(tslot, s);
 
   if (pl.ok) {
-    HSL_CHECK(zero_words(w.xbuf, w.words, s));
+    HSL_CHECK(clear_slots(w.xbuf, w.xfloats, s));
+    HSL_CHECK(zero_words(w.hello, w.hwords, s));
     PFwdArgs pa{w.gih, w_hh, b_hh, a, h0, c0, h_save, c_save, gact, tanh_c, w.xbuf, w.hello, w.err,
                 T, B, H, pl.Hp, pl.NG, pl.NGX, pl.Bg, pl.NW, exchange_scope_mode(), spin_timeout_ticks()};
     const int slot = timing_begin(kTimeRecFwd, s);
@@ -954,7 +1107,8 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     return fail(HSL_ERR_UNSUPPORTED, "persistent path does not fit (B=%d H=%d)", B, H);
 
   if (pl.ok) {
-    HSL_CHECK(zero_words(w.pbuf, w.words, s));
+    HSL_CHECK(clear_slots(w.pbuf, w.pfloats, s));
+    HSL_CHECK(zero_words(w.hello, w.hwords, s));
     PBwdArgs pa{dout, dh_n, dc_n, c_save, gact, tanh_c, w_hh, a, w.dgates, w.db_part, dh0, dc0, w.pbuf, w.hello,
                 w.err, T, B, H, pl.Hp, pl.NG, pl.NGX, pl.Bg, pl.NW, exchange_scope_mode(), spin_timeout_ticks()};
     const int slot = timing_begin(kTimeRecBwd, s);

@@ -503,6 +503,8 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
   // is forced into registers at the top of step t+1, by when it has long arrived; the
   // saved activations and the slot clear are stored after the publish.  All of them
   // have completed once the next receive has (one in-order completion counter).
+  // The streamed activations use non-temporal accesses so that they do not push the
+  // hand-off slots out of L2.
   float giA[4] = {0.f, 0.f, 0.f, 0.f}, giB[4] = {0.f, 0.f, 0.f, 0.f};
   if (c_ok) {
 #pragma unroll
@@ -534,7 +536,7 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
     if (c_ok && t + 1 < T) {
       const float* g = p.gih + ((size_t)(t + 1) * B + cb) * 4 * H + cu;
 #pragma unroll
-      for (int gt = 0; gt < 4; ++gt) gn[gt] = g[gt * H];
+      for (int gt = 0; gt < 4; ++gt) gn[gt] = __builtin_nontemporal_load(g + gt * H);
     }
     f4 acc[8];
 #pragma unroll
@@ -565,12 +567,12 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
       c_reg = c;
       if (!fast) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
       word_put(wbase + (size_t)(t & 3) * slot_words, canon_nan(h), fast);
-      p.h_save[(size_t)(t + 1) * plane + bu] = h;
-      p.c_save[(size_t)(t + 1) * plane + bu] = c;
-      p.tanh_c[(size_t)t * plane + bu] = tc;
+      __builtin_nontemporal_store(h, p.h_save + (size_t)(t + 1) * plane + bu);
+      __builtin_nontemporal_store(c, p.c_save + (size_t)(t + 1) * plane + bu);
+      __builtin_nontemporal_store(tc, p.tanh_c + (size_t)t * plane + bu);
       float* ga = p.gact + ((size_t)t * B + cb) * 4 * H + cu;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) ga[g * H] = act[g];
+      for (int g = 0; g < 4; ++g) __builtin_nontemporal_store(act[g], ga + g * H);
       word_put(wbase + (size_t)((t + 2) & 3) * slot_words, __uint_as_float(kEmpty), fast);
     }
     return true;
@@ -686,15 +688,17 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
   // after step t's receive (two register sets alternate, so no copy waits for them)
   // and forced into registers at the top of the next step, by when they have long
   // arrived; dgates and the slot clear are stored after the cell.  All of them have
-  // completed once the next receive has (one in-order completion counter).
+  // completed once the next receive has (one in-order completion counter).  The
+  // streamed activations use non-temporal accesses so that they do not push the
+  // hand-off slots out of L2.
   const size_t bu = (size_t)cb * H + cu;
   auto load_step = [&](int ts, float (&nx)[7]) {  // dout, c_prev, tanh_c, i, f, g, o
-    nx[0] = p.dout[(size_t)ts * plane + bu];
-    nx[1] = p.c_save[(size_t)ts * plane + bu];
-    nx[2] = p.tanh_c[(size_t)ts * plane + bu];
+    nx[0] = __builtin_nontemporal_load(p.dout + (size_t)ts * plane + bu);
+    nx[1] = __builtin_nontemporal_load(p.c_save + (size_t)ts * plane + bu);
+    nx[2] = __builtin_nontemporal_load(p.tanh_c + (size_t)ts * plane + bu);
     const float* ga = p.gact + ((size_t)ts * B + cb) * 4 * H + cu;
 #pragma unroll
-    for (int gt = 0; gt < 4; ++gt) nx[3 + gt] = ga[gt * H];
+    for (int gt = 0; gt < 4; ++gt) nx[3 + gt] = __builtin_nontemporal_load(ga + gt * H);
   };
   float nxA[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, nxB[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (c_ok && T > 0) load_step(T - 1, nxA);
@@ -752,7 +756,7 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
     if (c_ok) {
       float* dgp = p.dgates + ((size_t)t * B + cb) * 4 * H + cu;
 #pragma unroll
-      for (int gt = 0; gt < 4; ++gt) dgp[gt * H] = d[gt];
+      for (int gt = 0; gt < 4; ++gt) __builtin_nontemporal_store(d[gt], dgp + gt * H);
     }
     lds_barrier();
     if (abort_flag) return false;

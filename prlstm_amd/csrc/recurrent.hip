@@ -500,9 +500,10 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
   // Memory traffic of a step is placed so that no wait for it lands between the
   // receive and the publish: the input-projection row of step t+1 is requested right
   // after step t's receive (two register sets alternate, so no copy waits for it) and
-  // is forced into registers at the top of step t+1, by when it has long arrived; the
-  // saved activations and the slot clear are stored after the publish.  All of them
-  // have completed once the next receive has (one in-order completion counter).
+  // is forced into registers right after step t+1's receive, by when it has long arrived
+  // (forcing it earlier would also wait for the stores of step t, before the first
+  // poll); the saved activations and the slot clear are stored after the publish.  All
+  // of them have completed once the next receive has (one in-order completion counter).
   // The streamed activations use non-temporal accesses so that they do not push the
   // hand-off slots out of L2.
   float giA[4] = {0.f, 0.f, 0.f, 0.f}, giB[4] = {0.f, 0.f, 0.f, 0.f};
@@ -514,7 +515,6 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
   // One step; gi holds this step's projection row, gn receives the next one.  Returns
   // false when the group aborted.
   auto step = [&](int t, float (&gi)[4], float (&gn)[4]) __attribute__((always_inline)) -> bool {
-    asm volatile("" : "+v"(gi[0]), "+v"(gi[1]), "+v"(gi[2]), "+v"(gi[3]));
     float hv[NS];
     if (t == 0) {
 #pragma unroll
@@ -533,6 +533,7 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
         asm volatile("" : "+v"(hv[j]));  // settled before the loads below are issued
       }
     }
+    asm volatile("" : "+v"(gi[0]), "+v"(gi[1]), "+v"(gi[2]), "+v"(gi[3]));
     if (c_ok && t + 1 < T) {
       const float* g = p.gih + ((size_t)(t + 1) * B + cb) * 4 * H + cu;
 #pragma unroll
@@ -686,8 +687,8 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
   // Memory traffic of a step is placed so that no wait for it lands between the
   // receive and the publish: the saved activations of step t-1 are requested right
   // after step t's receive (two register sets alternate, so no copy waits for them)
-  // and forced into registers at the top of the next step, by when they have long
-  // arrived; dgates and the slot clear are stored after the cell.  All of them have
+  // and forced into registers right after the next step's receive, by when they have
+  // long arrived; dgates and the slot clear are stored after the cell.  All of them have
   // completed once the next receive has (one in-order completion counter).  The
   // streamed activations use non-temporal accesses so that they do not push the
   // hand-off slots out of L2.
@@ -706,8 +707,6 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
   // Step s (time t = T-1-s) with its activations in cur; the next step's go to nxt.
   // Returns false when done (s == T) or when the group aborted.
   auto step = [&](int s, float (&cur)[7], float (&nxt)[7]) __attribute__((always_inline)) -> bool {
-    asm volatile("" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]), "+v"(cur[5]),
-                 "+v"(cur[6]));
     const int t = T - 1 - s;
 
     // ---- dh: dh_n, or the fixed-order sum of last step's partials ------------------
@@ -738,6 +737,8 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
       }
       return false;
     }
+    asm volatile("" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]), "+v"(cur[5]),
+                 "+v"(cur[6]));
     if (c_ok && s + 1 < T) load_step(t - 1, nxt);
 
     // ---- cell backward (wave q: batch slot q) ----------------------------------------

@@ -235,9 +235,12 @@ constexpr unsigned kEmpty = 0xFFFFFFFFu;
 
 __device__ __forceinline__ float canon_nan(float v) { return v == v ? v : __uint_as_float(0x7FC00000u); }
 
-__device__ __forceinline__ void word_put(float* p, float v, bool xcd_local) {
-  unsigned* u = reinterpret_cast<unsigned*>(p);
-  if (xcd_local)
+// All hand-off accesses address a uniform base plus a 32-bit lane offset (in words),
+// which maps onto the scalar-base addressing of global memory instructions.
+template <bool FAST>
+__device__ __forceinline__ void word_put(float* base, unsigned off, float v) {
+  unsigned* u = reinterpret_cast<unsigned*>(base) + off;
+  if constexpr (FAST)
     __hip_atomic_store(u, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   else
     __hip_atomic_store(u, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -247,24 +250,24 @@ __device__ __forceinline__ void word_put(float* p, float v, bool xcd_local) {
 // lane l is at l; otherwise word j is at 128*(j/2) + 2*l + j%2, so a lane's words pair
 // up into 8-byte loads and stores and the 64 lanes of a pair are contiguous.
 template <int N>
-__device__ __forceinline__ int lane_word(int l, int j) {
+__device__ __forceinline__ unsigned lane_word(unsigned l, unsigned j) {
   if constexpr (N == 1)
     return l;
   else
-    return 128 * (j >> 1) + 2 * l + (j & 1);
+    return 128u * (j >> 1) + 2u * l + (j & 1u);
 }
 
-// p = block + lane_word<N>(lane, 0).
-template <int N>
-__device__ __forceinline__ void words_clear(float* p, bool xcd_local) {
+// off = block offset + lane_word<N>(lane, 0).
+template <int N, bool FAST>
+__device__ __forceinline__ void words_clear(float* base, unsigned off) {
   if constexpr (N == 1) {
-    word_put(p, __uint_as_float(kEmpty), xcd_local);
+    word_put<FAST>(base, off, __uint_as_float(kEmpty));
   } else {
     const unsigned long long e = ~0ull;
 #pragma unroll
     for (int i = 0; i < N / 2; ++i) {
-      unsigned long long* u = reinterpret_cast<unsigned long long*>(p + 128 * i);
-      if (xcd_local)
+      unsigned long long* u = reinterpret_cast<unsigned long long*>(base + (off + 128u * i));
+      if constexpr (FAST)
         __hip_atomic_store(u, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       else
         __hip_atomic_store(u, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -274,17 +277,18 @@ __device__ __forceinline__ void words_clear(float* p, bool xcd_local) {
 
 // Loads the lane's words whose flag in `need` is set (pairs are loaded together).
 template <int N>
-__device__ __forceinline__ void words_load(const float* p, const bool (&need)[N], unsigned (&v)[N]) {
+__device__ __forceinline__ void words_load(const float* base, unsigned off, const bool (&need)[N],
+                                           unsigned (&v)[N]) {
   if constexpr (N == 1) {
     if (need[0])
-      v[0] = __hip_atomic_load(reinterpret_cast<unsigned*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
+      v[0] = __hip_atomic_load(reinterpret_cast<unsigned*>(const_cast<float*>(base)) + off, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
   } else {
 #pragma unroll
     for (int i = 0; i < N / 2; ++i) {
       if (need[2 * i] || need[2 * i + 1]) {
         const unsigned long long w =
-            __hip_atomic_load(reinterpret_cast<unsigned long long*>(const_cast<float*>(p + 128 * i)),
+            __hip_atomic_load(reinterpret_cast<unsigned long long*>(const_cast<float*>(base + (off + 128u * i))),
                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         v[2 * i] = static_cast<unsigned>(w);
         v[2 * i + 1] = static_cast<unsigned>(w >> 32);
@@ -296,15 +300,15 @@ __device__ __forceinline__ void words_load(const float* p, const bool (&need)[N]
 // Polls the lane's words until every word flagged in `expect` differs from kEmpty.
 // Returns false (after setting the error flags) when the spin limit runs out.
 template <int N>
-__device__ __forceinline__ bool words_wait(const float* p, const bool (&expect)[N], unsigned (&v)[N], long long spin,
-                                           int* abort_flag, int* err) {
+__device__ __forceinline__ bool words_wait(const float* base, unsigned off, const bool (&expect)[N],
+                                           unsigned (&v)[N], long long spin, int* abort_flag, int* err) {
   bool need[N];
 #pragma unroll
   for (int j = 0; j < N; ++j) {
     need[j] = expect[j];
     v[j] = 0u;
   }
-  words_load<N>(p, need, v);
+  words_load<N>(base, off, need, v);
   const long long t0 = wall_clock64();
   while (true) {
     bool ok = true;
@@ -319,7 +323,7 @@ __device__ __forceinline__ bool words_wait(const float* p, const bool (&expect)[
       atomicOr(err, 1);
       return false;
     }
-    words_load<N>(p, need, v);
+    words_load<N>(base, off, need, v);
   }
 }
 
@@ -422,11 +426,11 @@ struct PFwdArgs {
 // Forward.  Wave q multiplies the q-th quarter of k (KQ values).  h_{t-1} of a quarter
 // comes from NS = KQ/16 source workgroups (16 units each).  Lane l of wave q needs
 // h[batch slot l%4][unit q*KQ + 16j + l/4] for j < NS; these NS words form the lane's
-// part of a 64-lane block (lane_word), so the receive is NS/2 8-byte loads per lane.  The 16 MFMAs of
-// source j then read their A operand straight from the received registers: with
-// cbsz=4, abid=kk broadcasts lanes 4kk..4kk+3, i.e. h[0..3][unit kk], to all 16
-// blocks.  One workgroup barrier per step joins the four k-quarters; wave q then runs
-// the cell for batch slot q (lanes 0-15 = units).
+// part of a 64-lane block (lane_word), so the receive is NS/2 8-byte loads per lane.
+// The 16 MFMAs of source j then read their A operand straight from the received
+// registers: with cbsz=4, abid=kk broadcasts lanes 4kk..4kk+3, i.e. h[0..3][unit kk],
+// to all 16 blocks.  One workgroup barrier per step joins the four k-quarters; wave q
+// then runs the cell for batch slot q (lanes 0-15 = units).
 //
 // Slots: h_t goes to slot t%4.  After its publish in step t, the owner of a word clears
 // it in slot (t+2)%4 (h_{t-2}).  By then the four waves together have received h_{t-1}
@@ -435,32 +439,28 @@ struct PFwdArgs {
 // clear comes after the barrier).  The clear completes before the owner's next receive
 // does, hence before it publishes h_{t+1}; a reader of h_{t+2} has seen h_{t+1} first,
 // so it sees the clear or h_{t+2}, never h_{t-2}.
-template <int KQ>
-__global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
+//
+// One wave per SIMD leaves no other wave to hide latency behind, so the step is written
+// for a short dependent chain: uniform bases with 32-bit lane offsets for every access,
+// the hand-off scope fixed at compile time (FAST: XCD-local), and 4 accumulator chains.
+template <int KQ, bool FAST>
+__device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg, f4 (&red)[2][4][64],
+                                             int& abort_flag) {
   constexpr int HP = 4 * KQ;
   constexpr int NS = KQ / kUnits;
-  constexpr int GW = 4 * HP;           // words per group and slot
-  __shared__ f4 red[2][4][64];         // [step parity][batch slot][gate row] -> 4 wave partials
-  __shared__ int abort_flag;
-
+  constexpr int GW = 4 * HP;  // words per group and slot
   const int T = p.T, B = p.B, H = p.H, NG = p.NG, Bg = p.Bg;
-  const int grp = blockIdx.x % p.NGX, wg = blockIdx.x / p.NGX;
-  if (grp >= NG) return;  // unused XCD slot (groups are padded to a multiple of 8)
-  const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
-  if (tid == 0) abort_flag = 0;
-  const bool fast = agree_placement(p.hello + (size_t)grp * (HP / kUnits), wg, p.NW, p.spin, &abort_flag, p.err) &&
-                    !p.device_scope;
-  if (abort_flag) return;
+  const int lane = threadIdx.x & 63;
+  const int q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
   // a-scaled W_hh slice: lane = gate row (gate lane/16, unit lane%16), registers = k quarter
   const int rgate = lane >> 4, ru = wg * kUnits + (lane & 15);
   const bool row_ok = ru < H;
-  const int n = rgate * H + ru;
   float wreg[KQ];
   {
     // unconditional loads at clamped addresses, so that all of them are in flight at once
     const float ag = p.a[rgate];
-    const float* wrow = p.w_hh + (size_t)(row_ok ? n : 0) * H;
+    const float* wrow = p.w_hh + (size_t)(row_ok ? rgate * H + ru : 0) * H;
 #pragma unroll
     for (int kk = 0; kk < KQ; ++kk) {
       const int k = q * KQ + kk;
@@ -469,9 +469,11 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
     }
   }
 
-  // cell thread: wave q, lane < 16 -> (batch slot q, unit cu)
-  const int cb = grp * Bg + q, cu = wg * kUnits + (lane & 15);
-  const bool c_ok = lane < kUnits && q < Bg && cb < B && cu < H;
+  // cell thread: wave q, lane < 16 -> (batch slot q, unit cu); cb is wave-uniform
+  const int cb = grp * Bg + q;
+  const unsigned cu = wg * kUnits + (lane & 15);
+  const bool c_ok = lane < kUnits && q < Bg && cb < B && (int)cu < H;
+  const int cbc = cb < B ? cb : 0;  // clamped for the uniform bases below
   float bs[4] = {0.f, 0.f, 0.f, 0.f};
   float c_reg = 0.f;
   if (c_ok) {
@@ -489,13 +491,18 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
 #pragma unroll
   for (int j = 0; j < NS; ++j) wv[j] = wi < Bg && wb < B && (q * NS + j) * kUnits + wkk < H;
   const size_t slot_words = (size_t)NG * GW;
-  const float* rbase = p.xbuf + (size_t)grp * GW + (size_t)q * 64 * NS + lane_word<NS>(lane, 0);
+  float* const xg = p.xbuf + (size_t)grp * GW;
+  const unsigned roff = q * 64 * NS + lane_word<NS>(lane, 0);
   // publish: the word of (batch slot q, unit cu) is read by lane 4*(cu%16) + q of wave
   // cu/KQ, as its word (cu%KQ)/16
-  float* wbase = p.xbuf + (size_t)grp * GW + (size_t)(cu / KQ) * 64 * NS +
-                 lane_word<NS>(4 * (cu & 15) + q, (cu % KQ) / kUnits);
-  const size_t plane = (size_t)B * H;
-  const size_t bu = (size_t)cb * H + cu;
+  const unsigned woff = (cu / KQ) * 64 * NS + lane_word<NS>(4 * (cu & 15) + q, (cu % KQ) / kUnits);
+  const size_t plane = (size_t)B * H, plane4 = 4 * plane;
+  // per-step rows of the streamed arrays: uniform base + cu (+ g*H)
+  const float* gih_row = p.gih + (size_t)cbc * 4 * H;
+  float* hs_row = p.h_save + (size_t)cbc * H;
+  float* cs_row = p.c_save + (size_t)cbc * H;
+  float* tc_row = p.tanh_c + (size_t)cbc * H;
+  float* ga_row = p.gact + (size_t)cbc * 4 * H;
 
   // Memory traffic of a step is placed so that no wait for it lands between the
   // receive and the publish: the input-projection row of step t+1 is requested right
@@ -509,7 +516,7 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
   float giA[4] = {0.f, 0.f, 0.f, 0.f}, giB[4] = {0.f, 0.f, 0.f, 0.f};
   if (c_ok) {
 #pragma unroll
-    for (int gt = 0; gt < 4; ++gt) giA[gt] = p.gih[(size_t)cb * 4 * H + gt * H + cu];
+    for (int gt = 0; gt < 4; ++gt) giA[gt] = gih_row[gt * H + cu];
   }
 
   // One step; gi holds this step's projection row, gn receives the next one.  Returns
@@ -525,8 +532,8 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
       }
     } else {
       unsigned v[NS];
-      words_wait<NS>(rbase + (size_t)((t - 1) & 3) * slot_words, wv, v, p.spin, &abort_flag, p.err);
-      if (!fast) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      words_wait<NS>(xg + (size_t)((t - 1) & 3) * slot_words, roff, wv, v, p.spin, &abort_flag, p.err);
+      if constexpr (!FAST) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 #pragma unroll
       for (int j = 0; j < NS; ++j) {
         hv[j] = wv[j] ? __uint_as_float(v[j]) : 0.f;
@@ -535,19 +542,19 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
     }
     asm volatile("" : "+v"(gi[0]), "+v"(gi[1]), "+v"(gi[2]), "+v"(gi[3]));
     if (c_ok && t + 1 < T) {
-      const float* g = p.gih + ((size_t)(t + 1) * B + cb) * 4 * H + cu;
+      const float* g = gih_row + (size_t)(t + 1) * plane4;
 #pragma unroll
-      for (int gt = 0; gt < 4; ++gt) gn[gt] = __builtin_nontemporal_load(g + gt * H);
+      for (int gt = 0; gt < 4; ++gt) gn[gt] = __builtin_nontemporal_load(g + (gt * H + cu));
     }
-    f4 acc[8];
+    f4 acc[4];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < 4; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NS; ++j)
 #pragma unroll
       for (int kk = 0; kk < kUnits; ++kk)
-        acc[kk & 7] = mfma4_bcast(hv[j], wreg[j * kUnits + kk], acc[kk & 7], kk);
-    const f4 zs = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+        acc[kk & 3] = mfma4_bcast(hv[j], wreg[j * kUnits + kk], acc[kk & 3], kk);
+    const f4 zs = (acc[0] + acc[1]) + (acc[2] + acc[3]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) reinterpret_cast<float*>(&red[t & 1][i][lane])[q] = zs[i];
     lds_barrier();
@@ -566,15 +573,15 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
       const float tc = tanh_f(c);
       const float h = act[3] * tc;
       c_reg = c;
-      if (!fast) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-      word_put(wbase + (size_t)(t & 3) * slot_words, canon_nan(h), fast);
-      __builtin_nontemporal_store(h, p.h_save + (size_t)(t + 1) * plane + bu);
-      __builtin_nontemporal_store(c, p.c_save + (size_t)(t + 1) * plane + bu);
-      __builtin_nontemporal_store(tc, p.tanh_c + (size_t)t * plane + bu);
-      float* ga = p.gact + ((size_t)t * B + cb) * 4 * H + cu;
+      if constexpr (!FAST) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      word_put<FAST>(xg + (size_t)(t & 3) * slot_words, woff, canon_nan(h));
+      __builtin_nontemporal_store(h, hs_row + (size_t)(t + 1) * plane + cu);
+      __builtin_nontemporal_store(c, cs_row + (size_t)(t + 1) * plane + cu);
+      __builtin_nontemporal_store(tc, tc_row + (size_t)t * plane + cu);
+      float* ga = ga_row + (size_t)t * plane4;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) __builtin_nontemporal_store(act[g], ga + g * H);
-      word_put(wbase + (size_t)((t + 2) & 3) * slot_words, __uint_as_float(kEmpty), fast);
+      for (int g = 0; g < 4; ++g) __builtin_nontemporal_store(act[g], ga + (g * H + cu));
+      word_put<FAST>(xg + (size_t)((t + 2) & 3) * slot_words, woff, __uint_as_float(kEmpty));
     }
     return true;
   };
@@ -583,6 +590,23 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
     if (!step(t, giA, giB)) return;
     if (t + 1 < T && !step(t + 1, giB, giA)) return;
   }
+}
+
+template <int KQ>
+__global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
+  constexpr int HP = 4 * KQ;
+  __shared__ f4 red[2][4][64];  // [step parity][batch slot][gate row] -> 4 wave partials
+  __shared__ int abort_flag;
+  const int grp = blockIdx.x % p.NGX, wg = blockIdx.x / p.NGX;
+  if (grp >= p.NG) return;  // unused XCD slot (groups are padded to a multiple of 8)
+  if (threadIdx.x == 0) abort_flag = 0;
+  const bool fast = agree_placement(p.hello + (size_t)grp * (HP / kUnits), wg, p.NW, p.spin, &abort_flag, p.err) &&
+                    !p.device_scope;
+  if (abort_flag) return;
+  if (fast)
+    rec_fwd_body<KQ, true>(p, grp, wg, red, abort_flag);
+  else
+    rec_fwd_body<KQ, false>(p, grp, wg, red, abort_flag);
 }
 
 struct PBwdArgs {
@@ -611,31 +635,27 @@ struct PBwdArgs {
 // partials of sources m, m+4, m+8, ... (m = lane/16) for unit lane%16, adds them in
 // that order, and two cross-lane shuffles finish the fixed-order sum, so the
 // receive needs no LDS and no barrier.  A lane's PER partials form its part of a
-// 64-lane block (lane_word).  One workgroup barrier per step publishes the step's dgates
-// (double-buffered in LDS) to the four column quarters.
+// 64-lane block (lane_word).  One workgroup barrier per step publishes the step's
+// dgates (double-buffered in LDS) to the four column quarters.
 //
 // Slots: the partials published in step s go to slot s%3 and have exactly one reader,
 // which clears them right after its receive in step s+1.  They are written again in
 // step s+3, by a writer that has by then received the reader's step-s+2 partials; the
 // reader publishes those only after its step-s+2 receive, which waits for the clear.
-template <int KQ>
-__global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
+//
+// As in the forward, every access uses a uniform base plus a 32-bit lane offset and the
+// hand-off scope is a compile-time choice, keeping the per-step dependent chain short.
+template <int KQ, bool FAST>
+__device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg, float (&dgl)[2][4][68],
+                                             int& abort_flag) {
   constexpr int HP = 4 * KQ;
   constexpr int CG = (KQ + 63) / 64;     // 64-column groups per wave
   constexpr int NWMAX = HP / kUnits;     // workgroups per group at most
   constexpr int PER = (NWMAX + 3) / 4;   // partials gathered per lane
   constexpr int RW = 4 * 64 * PER;       // words per reader workgroup and slot
-  __shared__ float dgl[2][4][64 + 4];    // [step parity][batch slot][gate row]
-  __shared__ int abort_flag;
-
   const int T = p.T, B = p.B, H = p.H, NG = p.NG, Bg = p.Bg, NW = p.NW;
-  const int grp = blockIdx.x % p.NGX, wg = blockIdx.x / p.NGX;
-  if (grp >= NG) return;
-  const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
-  if (tid == 0) abort_flag = 0;
-  const bool fast = agree_placement(p.hello + (size_t)grp * NWMAX, wg, NW, p.spin, &abort_flag, p.err) &&
-                    !p.device_scope;
-  if (abort_flag) return;
+  const int lane = threadIdx.x & 63;
+  const int q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
   // W_s columns owned by this lane: col = q*KQ + cg*64 + lane; registers over the 64 rows.
   float wreg[CG][64];
@@ -663,9 +683,11 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
     }
   }
 
-  // cell thread: wave q, lane < 16 -> (batch slot q, unit cu)
-  const int uu = lane & 15, cu = wg * kUnits + uu, cb = grp * Bg + q;
-  const bool c_ok = lane < kUnits && q < Bg && cb < B && cu < H;
+  // cell thread: wave q, lane < 16 -> (batch slot q, unit cu); cb is wave-uniform
+  const int uu = lane & 15, cb = grp * Bg + q;
+  const unsigned cu = wg * kUnits + uu;
+  const bool c_ok = lane < kUnits && q < Bg && cb < B && (int)cu < H;
+  const int cbc = cb < B ? cb : 0;
   float dc = 0.f;
   double dbacc[4] = {0.0, 0.0, 0.0, 0.0};
   if (c_ok) dc = p.dc_n[(size_t)cb * H + cu];
@@ -673,16 +695,22 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
   // receive words: partial j of lane l (source l/16 + 4j, batch slot q, column cu) at
   // block pbuf[slot][grp][wg][q], lane_word(l, j)
   const int m = lane >> 4;
-  const bool r_ok = q < Bg && cb < B && cu < H;
+  const bool r_ok = q < Bg && cb < B && (int)cu < H;
   bool wv[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) wv[j] = r_ok && m + 4 * j < NW;
   const size_t slot_words = (size_t)NG * NWMAX * RW;
-  float* const rbase = p.pbuf + ((size_t)grp * NWMAX + wg) * RW + (size_t)q * 64 * PER + lane_word<PER>(lane, 0);
+  float* const pg = p.pbuf + (size_t)grp * NWMAX * RW;
+  const unsigned roff = wg * RW + q * 64 * PER + lane_word<PER>(lane, 0);
   // publish: the partial of column c for batch slot i goes to reader workgroup c/16,
   // wave i, lane 16*(wg%4) + c%16, word wg/4
-  float* const pbase = p.pbuf + (size_t)grp * NWMAX * RW + lane_word<PER>(16 * (wg & 3), wg >> 2);
-  const size_t plane = (size_t)B * H;
+  const unsigned poff0 = lane_word<PER>(16 * (wg & 3), wg >> 2);
+  const size_t plane = (size_t)B * H, plane4 = 4 * plane;
+  const float* dout_row = p.dout + (size_t)cbc * H;
+  const float* cs_row = p.c_save + (size_t)cbc * H;
+  const float* tc_row = p.tanh_c + (size_t)cbc * H;
+  const float* ga_row = p.gact + (size_t)cbc * 4 * H;
+  float* dg_row = p.dgates + (size_t)cbc * 4 * H;
 
   // Memory traffic of a step is placed so that no wait for it lands between the
   // receive and the publish: the saved activations of step t-1 are requested right
@@ -692,14 +720,13 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
   // completed once the next receive has (one in-order completion counter).  The
   // streamed activations use non-temporal accesses so that they do not push the
   // hand-off slots out of L2.
-  const size_t bu = (size_t)cb * H + cu;
   auto load_step = [&](int ts, float (&nx)[7]) {  // dout, c_prev, tanh_c, i, f, g, o
-    nx[0] = __builtin_nontemporal_load(p.dout + (size_t)ts * plane + bu);
-    nx[1] = __builtin_nontemporal_load(p.c_save + (size_t)ts * plane + bu);
-    nx[2] = __builtin_nontemporal_load(p.tanh_c + (size_t)ts * plane + bu);
-    const float* ga = p.gact + ((size_t)ts * B + cb) * 4 * H + cu;
+    nx[0] = __builtin_nontemporal_load(dout_row + (size_t)ts * plane + cu);
+    nx[1] = __builtin_nontemporal_load(cs_row + (size_t)ts * plane + cu);
+    nx[2] = __builtin_nontemporal_load(tc_row + (size_t)ts * plane + cu);
+    const float* ga = ga_row + (size_t)ts * plane4;
 #pragma unroll
-    for (int gt = 0; gt < 4; ++gt) nx[3 + gt] = __builtin_nontemporal_load(ga + gt * H);
+    for (int gt = 0; gt < 4; ++gt) nx[3 + gt] = __builtin_nontemporal_load(ga + (gt * H + cu));
   };
   float nxA[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, nxB[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (c_ok && T > 0) load_step(T - 1, nxA);
@@ -711,15 +738,15 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
 
     // ---- dh: dh_n, or the fixed-order sum of last step's partials ------------------
     float dh = 0.f;
-    float* src = nullptr;
+    const float* src = nullptr;
     if (s == 0) {
       if (c_ok) dh = p.dh_n[(size_t)cb * H + cu];
       asm volatile("" : "+v"(dh));
     } else {
-      src = rbase + (size_t)((s - 1) % 3) * slot_words;
+      src = pg + (size_t)((s - 1) % 3) * slot_words;
       unsigned v[PER];
-      words_wait<PER>(src, wv, v, p.spin, &abort_flag, p.err);
-      if (!fast) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      words_wait<PER>(src, roff, wv, v, p.spin, &abort_flag, p.err);
+      if constexpr (!FAST) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       float part = 0.f;
 #pragma unroll
       for (int j = 0; j < PER; ++j) part += wv[j] ? __uint_as_float(v[j]) : 0.f;
@@ -730,6 +757,7 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
     }
     if (s == T) {  // dh is now the gradient w.r.t. h0
       if (c_ok) {
+        const size_t bu = (size_t)cb * H + cu;
         if (p.dh0) p.dh0[bu] = dh;
         if (p.dc0) p.dc0[bu] = dc;
 #pragma unroll
@@ -753,11 +781,11 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
 #pragma unroll
       for (int gt = 0; gt < 4; ++gt) dgl[s & 1][q][gt * kUnits + uu] = d[gt];
     }
-    if (src) words_clear<PER>(src, fast);
+    if (src) words_clear<PER, FAST>(const_cast<float*>(src), roff);
     if (c_ok) {
-      float* dgp = p.dgates + ((size_t)t * B + cb) * 4 * H + cu;
+      float* dgp = dg_row + (size_t)t * plane4;
 #pragma unroll
-      for (int gt = 0; gt < 4; ++gt) __builtin_nontemporal_store(d[gt], dgp + gt * H);
+      for (int gt = 0; gt < 4; ++gt) __builtin_nontemporal_store(d[gt], dgp + (gt * H + cu));
     }
     lds_barrier();
     if (abort_flag) return false;
@@ -766,25 +794,25 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
     // lane l holds dgates of batch slot l%4 for rows 4(l/4)..4(l/4)+3; the MFMA for row
     // r = 4kk+c broadcasts register c of lanes 4kk..4kk+3 (abid = kk).
     const f4 dv = *reinterpret_cast<const f4*>(&dgl[s & 1][lane & 3][4 * (lane >> 2)]);
-    if (!fast) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if constexpr (!FAST) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    float* const dst_slot = pg + (size_t)(s % 3) * slot_words;
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) {
-      f4 acc[8];
+      f4 acc[4];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < 4; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 16; ++kk) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          acc[(kk & 1) * 4 + c] = mfma4_bcast(dv[c], wreg[cg][4 * kk + c], acc[(kk & 1) * 4 + c], kk);
+        for (int c = 0; c < 4; ++c) acc[c] = mfma4_bcast(dv[c], wreg[cg][4 * kk + c], acc[c], kk);
       }
-      const f4 part = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+      const f4 part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
       if (col_ok[cg]) {
-        const int c = col[cg];
-        float* dst = pbase + (size_t)(s % 3) * slot_words + (size_t)(c >> 4) * RW + (PER == 1 ? 1 : 2) * (c & 15);
+        const unsigned c = col[cg];
+        const unsigned off = (c >> 4) * RW + poff0 + (PER == 1 ? 1u : 2u) * (c & 15u);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (i < Bg && grp * Bg + i < B) word_put(dst + (size_t)i * 64 * PER, canon_nan(part[i]), fast);
+          if (i < Bg && grp * Bg + i < B) word_put<FAST>(dst_slot, off + i * 64 * PER, canon_nan(part[i]));
       }
     }
     return true;
@@ -794,6 +822,23 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
     if (!step(s, nxA, nxB)) return;
     if (!step(s + 1, nxB, nxA)) return;
   }
+}
+
+template <int KQ>
+__global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
+  constexpr int NWMAX = 4 * KQ / kUnits;
+  __shared__ float dgl[2][4][64 + 4];  // [step parity][batch slot][gate row]
+  __shared__ int abort_flag;
+  const int grp = blockIdx.x % p.NGX, wg = blockIdx.x / p.NGX;
+  if (grp >= p.NG) return;
+  if (threadIdx.x == 0) abort_flag = 0;
+  const bool fast = agree_placement(p.hello + (size_t)grp * NWMAX, wg, p.NW, p.spin, &abort_flag, p.err) &&
+                    !p.device_scope;
+  if (abort_flag) return;
+  if (fast)
+    rec_bwd_body<KQ, true>(p, grp, wg, dgl, abort_flag);
+  else
+    rec_bwd_body<KQ, false>(p, grp, wg, dgl, abort_flag);
 }
 
 // ---------------------------------------------------------------------------------

@@ -16,12 +16,14 @@
 //    v_mfma_f32_4x4x1_16b_f32 with the A operand (4 batch rows) broadcast to all 16
 //    blocks (cbsz=4), so one instruction covers 4 batch rows x 64 gate rows.
 //    Workgroups of a group hand h_t (forward) and partial dh (backward) to each other
-//    through tagged 64-bit words (hsl_internal.h), with bounded waits.
+//    through 4-byte words in rotating slots, with bounded waits.
 //  * per-step (any shape): one fused GEMM+cell kernel per time step.
 //
 // v_mfma_f32_4x4x1_16b_f32 layout (verified on gfx950): A from lane 4b+i is
 // A_b[i][0], B from lane 4b+j is B_b[0][j], result lane 4b+j, reg i holds D_b[i][j].
 // With cbsz=4, abid=0 every block uses block 0's A (lanes 0-3).
+#include <type_traits>
+
 #include "gemm_core.h"
 
 namespace hsl {
@@ -235,11 +237,19 @@ constexpr unsigned kEmpty = 0xFFFFFFFFu;
 
 __device__ __forceinline__ float canon_nan(float v) { return v == v ? v : __uint_as_float(0x7FC00000u); }
 
-// All hand-off accesses address a uniform base plus a 32-bit lane offset (in words),
-// which maps onto the scalar-base addressing of global memory instructions.
+// base + a byte offset held in 32 bits.  With a wave-uniform base this is the form
+// global memory instructions take directly (scalar base + 32-bit vector offset), so
+// no 64-bit address arithmetic runs per lane.
+template <class T>
+__device__ __forceinline__ T* byte_at(T* base, unsigned off) {
+  using C = std::conditional_t<std::is_const_v<T>, const char, char>;
+  return reinterpret_cast<T*>(reinterpret_cast<C*>(base) + off);
+}
+
+// All hand-off accesses address a uniform base plus a 32-bit lane offset (in words).
 template <bool FAST>
 __device__ __forceinline__ void word_put(float* base, unsigned off, float v) {
-  unsigned* u = reinterpret_cast<unsigned*>(base) + off;
+  unsigned* u = byte_at(reinterpret_cast<unsigned*>(base), 4u * off);
   if constexpr (FAST)
     __hip_atomic_store(u, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   else
@@ -266,7 +276,7 @@ __device__ __forceinline__ void words_clear(float* base, unsigned off) {
     const unsigned long long e = ~0ull;
 #pragma unroll
     for (int i = 0; i < N / 2; ++i) {
-      unsigned long long* u = reinterpret_cast<unsigned long long*>(base + (off + 128u * i));
+      unsigned long long* u = byte_at(reinterpret_cast<unsigned long long*>(base), 4u * (off + 128u * i));
       if constexpr (FAST)
         __hip_atomic_store(u, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       else
@@ -281,14 +291,15 @@ __device__ __forceinline__ void words_load(const float* base, unsigned off, cons
                                            unsigned (&v)[N]) {
   if constexpr (N == 1) {
     if (need[0])
-      v[0] = __hip_atomic_load(reinterpret_cast<unsigned*>(const_cast<float*>(base)) + off, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+      v[0] = __hip_atomic_load(byte_at(reinterpret_cast<unsigned*>(const_cast<float*>(base)), 4u * off),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
 #pragma unroll
     for (int i = 0; i < N / 2; ++i) {
       if (need[2 * i] || need[2 * i + 1]) {
         const unsigned long long w =
-            __hip_atomic_load(reinterpret_cast<unsigned long long*>(const_cast<float*>(base + (off + 128u * i))),
+            __hip_atomic_load(byte_at(reinterpret_cast<unsigned long long*>(const_cast<float*>(base)),
+                                      4u * (off + 128u * i)),
                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         v[2 * i] = static_cast<unsigned>(w);
         v[2 * i + 1] = static_cast<unsigned>(w >> 32);
@@ -544,7 +555,7 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
     if (c_ok && t + 1 < T) {
       const float* g = gih_row + (size_t)(t + 1) * plane4;
 #pragma unroll
-      for (int gt = 0; gt < 4; ++gt) gn[gt] = __builtin_nontemporal_load(g + (gt * H + cu));
+      for (int gt = 0; gt < 4; ++gt) gn[gt] = __builtin_nontemporal_load(byte_at(g, 4u * (gt * H + cu)));
     }
     f4 acc[4];
 #pragma unroll
@@ -575,12 +586,12 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
       c_reg = c;
       if constexpr (!FAST) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
       word_put<FAST>(xg + (size_t)(t & 3) * slot_words, woff, canon_nan(h));
-      __builtin_nontemporal_store(h, hs_row + (size_t)(t + 1) * plane + cu);
-      __builtin_nontemporal_store(c, cs_row + (size_t)(t + 1) * plane + cu);
-      __builtin_nontemporal_store(tc, tc_row + (size_t)t * plane + cu);
+      __builtin_nontemporal_store(h, byte_at(hs_row + (size_t)(t + 1) * plane, 4u * cu));
+      __builtin_nontemporal_store(c, byte_at(cs_row + (size_t)(t + 1) * plane, 4u * cu));
+      __builtin_nontemporal_store(tc, byte_at(tc_row + (size_t)t * plane, 4u * cu));
       float* ga = ga_row + (size_t)t * plane4;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) __builtin_nontemporal_store(act[g], ga + (g * H + cu));
+      for (int g = 0; g < 4; ++g) __builtin_nontemporal_store(act[g], byte_at(ga, 4u * (g * H + cu)));
       word_put<FAST>(xg + (size_t)((t + 2) & 3) * slot_words, woff, __uint_as_float(kEmpty));
     }
     return true;
@@ -706,6 +717,7 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
   // wave i, lane 16*(wg%4) + c%16, word wg/4
   const unsigned poff0 = lane_word<PER>(16 * (wg & 3), wg >> 2);
   const size_t plane = (size_t)B * H, plane4 = 4 * plane;
+  const bool full_group = Bg == 4 && grp * 4 + 3 < B;  // all four batch slots in use
   const float* dout_row = p.dout + (size_t)cbc * H;
   const float* cs_row = p.c_save + (size_t)cbc * H;
   const float* tc_row = p.tanh_c + (size_t)cbc * H;
@@ -720,16 +732,22 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
   // completed once the next receive has (one in-order completion counter).  The
   // streamed activations use non-temporal accesses so that they do not push the
   // hand-off slots out of L2.
-  auto load_step = [&](int ts, float (&nx)[7]) {  // dout, c_prev, tanh_c, i, f, g, o
-    nx[0] = __builtin_nontemporal_load(dout_row + (size_t)ts * plane + cu);
-    nx[1] = __builtin_nontemporal_load(cs_row + (size_t)ts * plane + cu);
-    nx[2] = __builtin_nontemporal_load(tc_row + (size_t)ts * plane + cu);
+  // nx = dout, c_{t-1}, (slot 2 unused), i, f, g, o of time ts.  tanh(c_t) is not
+  // loaded: c_t is the previous (later-in-time) step's c_{t-1}, and tanh_f of it equals
+  // the forward's saved value bit for bit (same function, same input).
+  auto load_step = [&](int ts, float (&nx)[7]) {
+    nx[0] = __builtin_nontemporal_load(byte_at(dout_row + (size_t)ts * plane, 4u * cu));
+    nx[1] = __builtin_nontemporal_load(byte_at(cs_row + (size_t)ts * plane, 4u * cu));
     const float* ga = ga_row + (size_t)ts * plane4;
 #pragma unroll
-    for (int gt = 0; gt < 4; ++gt) nx[3 + gt] = __builtin_nontemporal_load(ga + (gt * H + cu));
+    for (int gt = 0; gt < 4; ++gt) nx[3 + gt] = __builtin_nontemporal_load(byte_at(ga, 4u * (gt * H + cu)));
   };
   float nxA[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, nxB[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (c_ok && T > 0) load_step(T - 1, nxA);
+  float tc_next = 0.f;  // tanh(c_t) of the next step to run
+  if (c_ok && T > 0) {
+    load_step(T - 1, nxA);
+    tc_next = __builtin_nontemporal_load(byte_at(tc_row + (size_t)(T - 1) * plane, 4u * cu));
+  }
 
   // Step s (time t = T-1-s) with its activations in cur; the next step's go to nxt.
   // Returns false when done (s == T) or when the group aborted.
@@ -765,15 +783,17 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
       }
       return false;
     }
-    asm volatile("" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]), "+v"(cur[5]),
-                 "+v"(cur[6]));
+    asm volatile("" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[3]), "+v"(cur[4]), "+v"(cur[5]), "+v"(cur[6]),
+                 "+v"(tc_next));
     if (c_ok && s + 1 < T) load_step(t - 1, nxt);
+    const float tc = tc_next;
+    tc_next = tanh_f(cur[1]);
 
     // ---- cell backward (wave q: batch slot q) ----------------------------------------
     float d[4] = {0.f, 0.f, 0.f, 0.f};
     if (c_ok) {
       dh = dh + cur[0];
-      cell_bwd(dh, dc, cur[1], cur[3], cur[4], cur[5], cur[6], cur[2], d);
+      cell_bwd(dh, dc, cur[1], cur[3], cur[4], cur[5], cur[6], tc, d);
 #pragma unroll
       for (int gt = 0; gt < 4; ++gt) dbacc[gt] += (double)d[gt];
     }
@@ -785,7 +805,7 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
     if (c_ok) {
       float* dgp = dg_row + (size_t)t * plane4;
 #pragma unroll
-      for (int gt = 0; gt < 4; ++gt) __builtin_nontemporal_store(d[gt], dgp + (gt * H + cu));
+      for (int gt = 0; gt < 4; ++gt) __builtin_nontemporal_store(d[gt], byte_at(dgp, 4u * (gt * H + cu)));
     }
     lds_barrier();
     if (abort_flag) return false;
@@ -810,9 +830,14 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
       if (col_ok[cg]) {
         const unsigned c = col[cg];
         const unsigned off = (c >> 4) * RW + poff0 + (PER == 1 ? 1u : 2u) * (c & 15u);
+        if (full_group) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (i < Bg && grp * Bg + i < B) word_put<FAST>(dst_slot, off + i * 64 * PER, canon_nan(part[i]));
+          for (int i = 0; i < 4; ++i) word_put<FAST>(dst_slot, off + i * 64 * PER, canon_nan(part[i]));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (i < Bg && grp * Bg + i < B) word_put<FAST>(dst_slot, off + i * 64 * PER, canon_nan(part[i]));
+        }
       }
     }
     return true;

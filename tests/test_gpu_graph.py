@@ -49,3 +49,48 @@ def test_graph_replays_match_eager(dev, parallel, shape):
         assert set(grads_g) == set(grads_e)
         for n in grads_e:
             assert torch.allclose(grads_g[n], grads_e[n], rtol=1e-5, atol=1e-6), (rep, n)
+
+
+@pytest.mark.parametrize("shape", [(16, 8, 32, 64), (128, 32, 256, 256)])
+def test_head_start_schedule_mode_switch(dev, shape):
+    """The head-start schedule (README.md:13-16): parallel steps, then recurrent, then
+    parallel again, with an SGD update after every step.  One GraphedTrainStep follows
+    the module's mode (one graph per mode); an eager twin runs the same schedule.  After
+    every step the outputs, the gradients (None where eager leaves None) and the updated
+    parameters must agree."""
+    T, B, D, H = shape
+    print(f"schedule T={T} B={B} D={D} H={H}", flush=True)
+    torch.manual_seed(1)
+    m = prlstm_amd.HeadStartLSTM(D, H, parallel=True).to(dev)
+    with torch.no_grad():
+        m.a.fill_(0.2)
+    twin = prlstm_amd.HeadStartLSTM(D, H, parallel=True).to(dev)
+    twin.load_state_dict(m.state_dict())
+    xs = [torch.randn(T, B, D, device=dev) for _ in range(6)]
+    step = GraphedTrainStep(m, xs[0])
+    lr = 1e-3
+    schedule = [True, True, False, False, True, False]
+    for i, (parallel, x) in enumerate(zip(schedule, xs)):
+        m.set_mode(parallel)
+        twin.set_mode(parallel)
+        out_g = step.step(x).detach().clone()
+        grads_g = {n: (None if p.grad is None else p.grad.detach().clone()) for n, p in m.named_parameters()}
+        twin.zero_grad(set_to_none=True)
+        out_e, _ = twin(x)
+        out_e.sum().backward()
+        assert torch.allclose(out_g, out_e, rtol=1e-5, atol=1e-6), i
+        for n, p in twin.named_parameters():
+            if p.grad is None:
+                assert grads_g[n] is None, (i, n)
+            else:
+                assert grads_g[n] is not None, (i, n)
+                assert torch.allclose(grads_g[n], p.grad, rtol=1e-4, atol=1e-5), (i, n)
+        with torch.no_grad():
+            for mod in (m, twin):
+                for p in mod.parameters():
+                    if p.grad is not None:
+                        p.add_(p.grad, alpha=-lr)
+        torch.cuda.synchronize()
+    for (n, p), (_, q) in zip(m.named_parameters(), twin.named_parameters()):
+        assert torch.allclose(p, q, rtol=1e-5, atol=1e-6), n
+    assert set(step._graphs) == {True, False}

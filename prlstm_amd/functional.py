@@ -57,7 +57,8 @@ def _check(x, h0, c0, w_ih, w_hh, b_ih, b_hh, a):
         if t.device != x.device:
             raise RuntimeError(f"{name} is on {t.device}, x is on {x.device}")
         if t.dtype != torch.float32:
-            raise RuntimeError(f"prlstm_amd kernels compute in float32; {name} is {t.dtype}")
+            raise RuntimeError(f"prlstm_amd kernels compute in float32 (bf16/fp16 modules are widened "
+                               f"at the functional); {name} is {t.dtype}")
     return T, B, D, H
 
 
@@ -169,11 +170,31 @@ class ParallelFn(torch.autograd.Function):
         return dx, None, dc0, dw_ih, None, db_ih, None, None, None
 
 
+_HALF = (torch.bfloat16, torch.float16)
+
+
+def _widen(args):
+    """bf16/fp16 operands (a module moved with ``.to(dtype)``, as the reference's tests do for
+    bf16, ``test_parallel.py:22-38``) are cast to fp32 here; the kernels then compute and
+    accumulate in fp32 and the outputs are cast back.  The casts are autograd ops, so the
+    gradients arrive in each operand's own dtype.  Returns (args, output dtype or None)."""
+    dtype = args[0].dtype
+    if dtype not in _HALF:
+        return args, None
+    return tuple(t.float() if torch.is_tensor(t) and t.dtype in _HALF else t for t in args), dtype
+
+
+def _narrow(outs, dtype):
+    return outs if dtype is None else tuple(t.to(dtype) for t in outs)
+
+
 def headstartlstm_recurrent(x, h0, c0, W_ih, W_hh, b_ih, b_hh, a):
     """Recurrent-mode functional (drop-in for ``headstartlstm_torch``, ``_torch.py:173``)."""
-    return RecurrentFn.apply(x, h0, c0, W_ih, W_hh, b_ih, b_hh, a)
+    args, dtype = _widen((x, h0, c0, W_ih, W_hh, b_ih, b_hh, a))
+    return _narrow(RecurrentFn.apply(*args), dtype)
 
 
 def headstartlstm_parallel(x, h0, c0, W_ih, W_hh, b_ih, b_hh, a, eps=EPS):
     """Parallel-mode functional (drop-in for ``headstartlstm_parallel``, ``_parallel.py:38``)."""
-    return ParallelFn.apply(x, h0, c0, W_ih, W_hh, b_ih, b_hh, a, eps)
+    args, dtype = _widen((x, h0, c0, W_ih, W_hh, b_ih, b_hh, a))
+    return _narrow(ParallelFn.apply(*args, eps), dtype)

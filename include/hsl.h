@@ -85,7 +85,7 @@ size_t hsl_rec_fwd_ws_bytes(int T, int B, int D, int H);
  * :111-120).  Writes
  *   h_save [T+1,B,H]   h_save[0] = h0, h_save[t+1] = h_t  (output = h_save[1:])
  *   c_save [T+1,B,H]   c_save[0] = c0, c_save[t+1] = c_t
- *   gact   [T,B,4H]    sigmoid gate activations [i|f|g|o]
+ *   gact   [T,B,H,4]   sigmoid gate activations (i, f, g, o) of each unit
  *   tanh_c [T,B,H]     tanh(c_t)
  * gact and tanh_c are what hsl_rec_bwd reads back. */
 int hsl_rec_fwd(const float* x, const float* h0, const float* c0,

@@ -143,7 +143,7 @@ struct EpiCellFwd {
   const float* c_prev;  // [B,H]
   float* h_out;         // [B,H]
   float* c_out;         // [B,H]
-  float* gact;          // [B,4H] at t
+  float* gact;          // [B,H,4] at t
   float* tanh_c;        // [B,H] at t
   int B, H;
   template <class Cfg>
@@ -159,8 +159,8 @@ struct EpiCellFwd {
         const int n = gt * H + u;
         const float z = (gih[(size_t)b * 4 * H + n] + tile_value<Cfg>(Cs, m, 4 * uu + gt)) + bs[n];
         act[gt] = sigmoid_f(z);
-        gact[(size_t)b * 4 * H + n] = act[gt];
       }
+      *reinterpret_cast<f4*>(gact + ((size_t)b * H + u) * 4) = f4{act[0], act[1], act[2], act[3]};
       const float c = act[1] * c_prev[(size_t)b * H + u] + act[0] * act[2];
       const float tc = tanh_f(c);
       h_out[(size_t)b * H + u] = act[3] * tc;
@@ -190,7 +190,7 @@ struct EpiCellBwd {
   const float* dout;     // [B,H] at t
   const float* dh_extra; // dh_n at t == T-1, else null
   const float* c_prev;   // c_save[t]
-  const float* gact;     // [B,4H] at t
+  const float* gact;     // [B,H,4] at t
   const float* tanh_c;   // [B,H] at t
   float* dc;             // [B,H] carry, updated in place
   float* dg;             // [B,4H] at t
@@ -205,10 +205,10 @@ struct EpiCellBwd {
       float dh = tile_value<Cfg>(Cs, m, nn);
       if (dh_extra) dh = dh + dh_extra[bu];
       dh = dh + dout[bu];
-      const float* ga = gact + (size_t)b * 4 * H + u;
+      const f4 ga = *reinterpret_cast<const f4*>(gact + ((size_t)b * H + u) * 4);
       float dcv = dc[bu];
       float d[4];
-      cell_bwd(dh, dcv, c_prev[bu], ga[0], ga[H], ga[2 * H], ga[3 * H], tanh_c[bu], d);
+      cell_bwd(dh, dcv, c_prev[bu], ga[0], ga[1], ga[2], ga[3], tanh_c[bu], d);
       dc[bu] = dcv;
 #pragma unroll
       for (int gt = 0; gt < 4; ++gt) dg[(size_t)b * 4 * H + gt * H + u] = d[gt];
@@ -220,11 +220,12 @@ struct EpiCellBwd {
 // persistent path
 // ---------------------------------------------------------------------------------
 // Hand-off between the workgroups of a batch group.  Values travel as 4-byte words in
-// rotating slots that start out holding kEmpty, a NaN pattern that no result takes
-// (results are NaN-canonicalised before they are published), so a word is ready as
-// soon as it differs from kEmpty.  A word is set back to kEmpty by the lane that owns
-// it once every reader is known to be done with it, and written again only slots
-// later; see the two kernels for the exact schedule.
+// rotating slots that start out holding kEmpty, a signalling-NaN pattern: arithmetic
+// never produces one (NaN results are quiet, i.e. have bit 22 set), and every published
+// value is an arithmetic result, so a word is ready as soon as it differs from kEmpty.
+// A word is set back to kEmpty by the lane that owns it once every reader is known to
+// be done with it, and written again only slots later; see the two kernels for the
+// exact schedule.
 //
 // Readers poll with relaxed device-scope loads (sc1), which are served by the reader's
 // L2.  When every member of the group runs on the same XCD (checked at launch start,
@@ -234,7 +235,7 @@ struct EpiCellBwd {
 // and each step adds a device-scope release before its publish and an acquire after
 // its receive (write-back and invalidation of the XCD's L2).
 constexpr unsigned kEmpty = 0xFFFFFFFFu;
-
+constexpr unsigned long long kEmpty2 = ~0ull;
 __device__ __forceinline__ float canon_nan(float v) { return v == v ? v : __uint_as_float(0x7FC00000u); }
 
 // base + a byte offset held in 32 bits.  With a wave-uniform base this is the form
@@ -273,7 +274,7 @@ __device__ __forceinline__ void words_clear(float* base, unsigned off) {
   if constexpr (N == 1) {
     word_put<FAST>(base, off, __uint_as_float(kEmpty));
   } else {
-    const unsigned long long e = ~0ull;
+    const unsigned long long e = kEmpty2;
 #pragma unroll
     for (int i = 0; i < N / 2; ++i) {
       unsigned long long* u = byte_at(reinterpret_cast<unsigned long long*>(base), 4u * (off + 128u * i));
@@ -513,7 +514,7 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
   float* hs_row = p.h_save + (size_t)cbc * H;
   float* cs_row = p.c_save + (size_t)cbc * H;
   float* tc_row = p.tanh_c + (size_t)cbc * H;
-  float* ga_row = p.gact + (size_t)cbc * 4 * H;
+  float* ga_row = p.gact + (size_t)cbc * H * 4;  // [T][B][H][4]
 
   // Memory traffic of a step is placed so that no wait for it lands between the
   // receive and the publish: the input-projection row of step t+1 is requested right
@@ -589,9 +590,8 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
       __builtin_nontemporal_store(h, byte_at(hs_row + (size_t)(t + 1) * plane, 4u * cu));
       __builtin_nontemporal_store(c, byte_at(cs_row + (size_t)(t + 1) * plane, 4u * cu));
       __builtin_nontemporal_store(tc, byte_at(tc_row + (size_t)t * plane, 4u * cu));
-      float* ga = ga_row + (size_t)t * plane4;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) __builtin_nontemporal_store(act[g], byte_at(ga, 4u * (g * H + cu)));
+      __builtin_nontemporal_store(f4{act[0], act[1], act[2], act[3]},
+                                  reinterpret_cast<f4*>(byte_at(ga_row + (size_t)t * plane4, 16u * cu)));
       word_put<FAST>(xg + (size_t)((t + 2) & 3) * slot_words, woff, __uint_as_float(kEmpty));
     }
     return true;
@@ -619,6 +619,13 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
   else
     rec_fwd_body<KQ, false>(p, grp, wg, red, abort_flag);
 }
+
+// Per-step inputs of the persistent backward, loaded one step ahead: dout[t], c_{t-1}
+// and the four gate activations of one (batch, unit).
+struct StepIn {
+  float dout, cp;
+  f4 g;
+};
 
 struct PBwdArgs {
   const float* dout;
@@ -721,7 +728,7 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
   const float* dout_row = p.dout + (size_t)cbc * H;
   const float* cs_row = p.c_save + (size_t)cbc * H;
   const float* tc_row = p.tanh_c + (size_t)cbc * H;
-  const float* ga_row = p.gact + (size_t)cbc * 4 * H;
+  const float* ga_row = p.gact + (size_t)cbc * H * 4;  // [T][B][H][4]
   float* dg_row = p.dgates + (size_t)cbc * 4 * H;
 
   // Memory traffic of a step is placed so that no wait for it lands between the
@@ -732,17 +739,15 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
   // completed once the next receive has (one in-order completion counter).  The
   // streamed activations use non-temporal accesses so that they do not push the
   // hand-off slots out of L2.
-  // nx = dout, c_{t-1}, (slot 2 unused), i, f, g, o of time ts.  tanh(c_t) is not
-  // loaded: c_t is the previous (later-in-time) step's c_{t-1}, and tanh_f of it equals
-  // the forward's saved value bit for bit (same function, same input).
-  auto load_step = [&](int ts, float (&nx)[7]) {
-    nx[0] = __builtin_nontemporal_load(byte_at(dout_row + (size_t)ts * plane, 4u * cu));
-    nx[1] = __builtin_nontemporal_load(byte_at(cs_row + (size_t)ts * plane, 4u * cu));
-    const float* ga = ga_row + (size_t)ts * plane4;
-#pragma unroll
-    for (int gt = 0; gt < 4; ++gt) nx[3 + gt] = __builtin_nontemporal_load(byte_at(ga, 4u * (gt * H + cu)));
+  // tanh(c_t) is not loaded: c_t is the previous (later-in-time) step's c_{t-1}, and
+  // tanh_f of it equals the forward's saved value bit for bit (same function, same
+  // input).
+  auto load_step = [&](int ts, StepIn& nx) {
+    nx.dout = __builtin_nontemporal_load(byte_at(dout_row + (size_t)ts * plane, 4u * cu));
+    nx.cp = __builtin_nontemporal_load(byte_at(cs_row + (size_t)ts * plane, 4u * cu));
+    nx.g = __builtin_nontemporal_load(reinterpret_cast<const f4*>(byte_at(ga_row + (size_t)ts * plane4, 16u * cu)));
   };
-  float nxA[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, nxB[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  StepIn nxA{0.f, 0.f, f4{0.f, 0.f, 0.f, 0.f}}, nxB{0.f, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
   float tc_next = 0.f;  // tanh(c_t) of the next step to run
   if (c_ok && T > 0) {
     load_step(T - 1, nxA);
@@ -751,7 +756,7 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
 
   // Step s (time t = T-1-s) with its activations in cur; the next step's go to nxt.
   // Returns false when done (s == T) or when the group aborted.
-  auto step = [&](int s, float (&cur)[7], float (&nxt)[7]) __attribute__((always_inline)) -> bool {
+  auto step = [&](int s, StepIn& cur, StepIn& nxt) __attribute__((always_inline)) -> bool {
     const int t = T - 1 - s;
 
     // ---- dh: dh_n, or the fixed-order sum of last step's partials ------------------
@@ -783,17 +788,16 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
       }
       return false;
     }
-    asm volatile("" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[3]), "+v"(cur[4]), "+v"(cur[5]), "+v"(cur[6]),
-                 "+v"(tc_next));
+    asm volatile("" : "+v"(cur.dout), "+v"(cur.cp), "+v"(cur.g), "+v"(tc_next));
     if (c_ok && s + 1 < T) load_step(t - 1, nxt);
     const float tc = tc_next;
-    tc_next = tanh_f(cur[1]);
+    tc_next = tanh_f(cur.cp);
 
     // ---- cell backward (wave q: batch slot q) ----------------------------------------
     float d[4] = {0.f, 0.f, 0.f, 0.f};
     if (c_ok) {
-      dh = dh + cur[0];
-      cell_bwd(dh, dc, cur[1], cur[3], cur[4], cur[5], cur[6], tc, d);
+      dh = dh + cur.dout;
+      cell_bwd(dh, dc, cur.cp, cur.g[0], cur.g[1], cur.g[2], cur.g[3], tc, d);
 #pragma unroll
       for (int gt = 0; gt < 4; ++gt) dbacc[gt] += (double)d[gt];
     }
@@ -937,7 +941,7 @@ int fill_words(unsigned long long* p, size_t n, unsigned long long v, hipStream_
 
 // Hand-off slots start out empty (every 4-byte word kEmpty).
 int clear_slots(float* p, size_t floats, hipStream_t s) {
-  return fill_words(reinterpret_cast<unsigned long long*>(p), (floats + 1) / 2, ~0ull, s);
+  return fill_words(reinterpret_cast<unsigned long long*>(p), (floats + 1) / 2, kEmpty2, s);
 }
 
 int copy_f32_impl(float* dst, const float* src, size_t n, hipStream_t s) {

@@ -84,7 +84,7 @@ class RecurrentFn(torch.autograd.Function):
         x, h0, c0, w_ih, w_hh, b_ih, b_hh, a = map(_c, (x, h0, c0, w_ih, w_hh, b_ih, b_hh, a))
         h_save = x.new_empty(T + 1, B, H)
         c_save = x.new_empty(T + 1, B, H)
-        gact = x.new_empty(T, B, 4 * H)
+        gact = x.new_empty(T, B, H, 4)
         tanh_c = x.new_empty(T, B, H)
         lib = _lib.load()
         nbytes = lib.hsl_rec_fwd_ws_bytes(T, B, D, H)

@@ -13,6 +13,10 @@
  *  - the last argument is the HIP stream (hipStream_t passed as void*; NULL is
  *    the null stream); work is only enqueued, nothing is synchronised, and no
  *    device memory is allocated, so every call can be captured in a hipGraph;
+ *  - the initial states h0/c0 and the incoming gradients dh_n/dc_n may be
+ *    NULL, which every entry point reads as all-zero [B,H] (the reference's
+ *    hx=None, __init__.py:174-176, and an unused h_n/c_n), so no zero buffers
+ *    need to be filled;
  *  - the return value is HSL_OK (0) or an HSL_ERR_* code; hsl_last_error()
  *    then returns a message (per host thread);
  *  - scratch memory is passed in as (ws, ws_bytes); the needed size is given by

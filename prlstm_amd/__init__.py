@@ -81,8 +81,7 @@ class HeadStartLSTM(nn.Module):
             x = x.transpose(0, 1).contiguous()
         T, B, _ = x.shape
         if hx is None:
-            h0 = x.new_zeros(B, self.hidden_size)
-            c0 = x.new_zeros(B, self.hidden_size)
+            h0 = c0 = None  # zero initial states, passed to the kernels as NULL
         else:
             h0, c0 = hx
             if h0.dim() == 3:

@@ -116,8 +116,15 @@ __global__ __launch_bounds__(256) void bias_da_finalize_kernel(const double* __r
   double acc = 0.0;
   for (int u = threadIdx.x; u < H; u += blockDim.x) {
     const int n = g * H + u;
-    double s = 0.0;
-    for (int b = 0; b < B; ++b) s += db_part[(size_t)b * 4 * H + n];
+    // eight independent partial sums keep eight loads in flight (fixed order: deterministic)
+    double ps[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+    int b = 0;
+    for (; b + 8 <= B; b += 8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ps[i] += db_part[(size_t)(b + i) * 4 * H + n];
+    }
+    for (; b < B; ++b) ps[0] += db_part[(size_t)b * 4 * H + n];
+    const double s = ((ps[0] + ps[1]) + (ps[2] + ps[3])) + ((ps[4] + ps[5]) + (ps[6] + ps[7]));
     const float db = (float)s;
     if (db_ih) db_ih[n] = db;
     if (db_hh) db_hh[n] = ag * db;
@@ -492,8 +499,8 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
 #pragma unroll
     for (int g = 0; g < 4; ++g) bs[g] = p.a[g] * p.b_hh[g * H + cu];
     const size_t b0 = (size_t)cb * H + cu;
-    c_reg = p.c0[b0];
-    p.h_save[b0] = p.h0[b0];
+    c_reg = p.c0 ? p.c0[b0] : 0.f;
+    p.h_save[b0] = p.h0 ? p.h0[b0] : 0.f;
     p.c_save[b0] = c_reg;
   }
 
@@ -539,7 +546,7 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
 #pragma unroll
       for (int j = 0; j < NS; ++j) {
         const int k = (q * NS + j) * kUnits + wkk;
-        hv[j] = wv[j] ? p.h0[(size_t)wb * H + k] : 0.f;
+        hv[j] = (wv[j] && p.h0) ? p.h0[(size_t)wb * H + k] : 0.f;
         asm volatile("" : "+v"(hv[j]));  // wait here, not after the loads below
       }
     } else {
@@ -708,7 +715,7 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
   const int cbc = cb < B ? cb : 0;
   float dc = 0.f;
   double dbacc[4] = {0.0, 0.0, 0.0, 0.0};
-  if (c_ok) dc = p.dc_n[(size_t)cb * H + cu];
+  if (c_ok && p.dc_n) dc = p.dc_n[(size_t)cb * H + cu];
 
   // receive words: partial j of lane l (source l/16 + 4j, batch slot q, column cu) at
   // block pbuf[slot][grp][wg][q], lane_word(l, j)
@@ -763,7 +770,7 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
     float dh = 0.f;
     const float* src = nullptr;
     if (s == 0) {
-      if (c_ok) dh = p.dh_n[(size_t)cb * H + cu];
+      if (c_ok && p.dh_n) dh = p.dh_n[(size_t)cb * H + cu];
       asm volatile("" : "+v"(dh));
     } else {
       src = pg + (size_t)((s - 1) % 3) * slot_words;
@@ -1076,7 +1083,7 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
   HSL_CHECK(check_dims(T, B, D, H));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (B == 0 || H == 0) return HSL_OK;
-  if (!h0 || !c0 || !w_hh || !b_hh || !a || !h_save || !c_save || (T > 0 && (!x || !w_ih || !b_ih || !gact || !tanh_c)))
+  if (!w_hh || !b_hh || !a || !h_save || !c_save || (T > 0 && (!x || !w_ih || !b_ih || !gact || !tanh_c)))
     return fail(HSL_ERR_ARG, "hsl_rec_fwd: null pointer");
   FwdWs w;
   const size_t need = carve_fwd(ws, ws_bytes, T, B, H, &w);
@@ -1160,7 +1167,7 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (!dw_ih || !dw_hh || !db_ih || !db_hh || !da || !w_ih || !w_hh || !b_hh || !a)
     return fail(HSL_ERR_ARG, "hsl_rec_bwd: null pointer");
-  if (T > 0 && B > 0 && H > 0 && (!dout || !dh_n || !dc_n || !x || !h_save || !c_save || !gact || !tanh_c))
+  if (T > 0 && B > 0 && H > 0 && (!dout || !x || !h_save || !c_save || !gact || !tanh_c))
     return fail(HSL_ERR_ARG, "hsl_rec_bwd: null pointer");
   BwdWs w;
   const size_t need = carve_bwd(ws, ws_bytes, T, B, D, H, &w);

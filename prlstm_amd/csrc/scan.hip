@@ -42,7 +42,7 @@ __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restri
   const size_t gstride = (size_t)B * 4 * H;  // per time step
   const float* gbase = gates + (size_t)b * 4 * H + j;
   const size_t ostride = (size_t)B * H;
-  if (w == 0) sC[lane] = ok ? fmaxf(c0[ch], eps) : 0.f;
+  if (w == 0) sC[lane] = ok ? fmaxf(c0 ? c0[ch] : 0.f, eps) : 0.f;
 
   constexpr int CH = NW * L;
   const int nchunks = (T + CH - 1) / CH;
@@ -120,9 +120,10 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
   const float* gbase = gates + (size_t)b * 4 * H + j;
   float* dgbase = dgates + (size_t)b * 4 * H + j;
   const size_t ostride = (size_t)B * H;
-  const float c0c = ok ? fmaxf(c0[ch], eps) : 0.f;
-  const bool c0_pass = ok && c0[ch] >= eps;
-  const float dhn = ok ? dh_n[ch] : 0.f, dcn = ok ? dc_n[ch] : 0.f;
+  const float c0v = (ok && c0) ? c0[ch] : 0.f;
+  const float c0c = ok ? fmaxf(c0v, eps) : 0.f;
+  const bool c0_pass = ok && c0v >= eps;
+  const float dhn = (ok && dh_n) ? dh_n[ch] : 0.f, dcn = (ok && dc_n) ? dc_n[ch] : 0.f;
   if (w == 0) sG[lane] = 0.f;
 
   constexpr int CH = NW * L;
@@ -306,7 +307,7 @@ extern "C" {
 int hsl_scan_fwd(const float* gates, const float* c0, float eps, float* out, float* c_seq, int T, int B, int H,
                  void* stream) {
   HSL_CHECK(check_scan_dims(T, B, H));
-  if (T > 0 && B > 0 && H > 0 && (!gates || !c0 || !out || !c_seq)) return fail(HSL_ERR_ARG, "hsl_scan_fwd: null pointer");
+  if (T > 0 && B > 0 && H > 0 && (!gates || !out || !c_seq)) return fail(HSL_ERR_ARG, "hsl_scan_fwd: null pointer");
   return scan_fwd(gates, c0, eps, out, c_seq, T, B, H, static_cast<hipStream_t>(stream));
 }
 
@@ -314,7 +315,7 @@ int hsl_scan_bwd(const float* gates, const float* c0, const float* c_seq, const 
                  const float* dc_n, float eps, float* dgates, double* db_part, float* dc0, int T, int B, int H,
                  void* stream) {
   HSL_CHECK(check_scan_dims(T, B, H));
-  if (B > 0 && H > 0 && T > 0 && (!gates || !c0 || !c_seq || !dout || !dh_n || !dc_n || !dgates))
+  if (B > 0 && H > 0 && T > 0 && (!gates || !c_seq || !dout || !dgates))
     return fail(HSL_ERR_ARG, "hsl_scan_bwd: null pointer");
   return scan_bwd(gates, c0, c_seq, dout, dh_n, dc_n, eps, dgates, db_part, dc0, T, B, H,
                   static_cast<hipStream_t>(stream));
@@ -326,7 +327,7 @@ int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float*
   if (D < 0) return fail(HSL_ERR_ARG, "negative D");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (T == 0 || B == 0 || H == 0) return HSL_OK;
-  if (!x || !c0 || !w_ih || !b_ih || !gates || !out || !c_seq) return fail(HSL_ERR_ARG, "hsl_par_fwd: null pointer");
+  if (!x || !w_ih || !b_ih || !gates || !out || !c_seq) return fail(HSL_ERR_ARG, "hsl_par_fwd: null pointer");
   GemmDesc g1{x, w_ih, b_ih, gates, T * B, 4 * H, D, D, D, 4 * H, 0, 1};
   const int slot = timing_begin(kTimeInputProj, s);
   HSL_CHECK(gemm_run(g1, nullptr, 0, s));
@@ -357,7 +358,7 @@ int hsl_par_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     if (dc0) HSL_CHECK(copy_f32(dc0, nullptr, (size_t)B * H, s));
     return HSL_OK;
   }
-  if (!dout || !dh_n || !dc_n || !x || !c0 || !gates || !c_seq)
+  if (!dout || !x || !gates || !c_seq)
     return fail(HSL_ERR_ARG, "hsl_par_bwd: null pointer");
   HSL_CHECK(scan_bwd(gates, c0, c_seq, dout, dh_n, dc_n, eps, w.dgates, w.db_part, dc0, T, B, H, s));
   HSL_CHECK(bias_grads_from_parts(w.db_part, B, nullptr, nullptr, nullptr, db_ih, nullptr, nullptr, H, s));

@@ -46,6 +46,7 @@ def _check(x, h0, c0, w_ih, w_hh, b_ih, b_hh, a):
         "weight_ih_l0": (w_ih, (4 * H, D)), "weight_hh_l0": (w_hh, (4 * H, H)),
         "bias_ih_l0": (b_ih, (4 * H,)), "bias_hh_l0": (b_hh, (4 * H,)), "a": (a, (4,)),
     }
+    want = {k: v for k, v in want.items() if v[0] is not None}  # h0/c0 None: zero states
     for name, (t, shape) in want.items():
         if tuple(t.shape) != shape:
             raise RuntimeError(f"{name} must have shape {shape}, got {tuple(t.shape)}")
@@ -63,11 +64,15 @@ def _check(x, h0, c0, w_ih, w_hh, b_ih, b_hh, a):
 
 
 def _c(t):
-    return t if t.is_contiguous() else t.contiguous()
+    return t if t is None or t.is_contiguous() else t.contiguous()
 
 
 def _grad_or_zeros(g, like):
     return _c(g) if g is not None else torch.zeros_like(like)
+
+# h0/c0 may be None (zero initial states) and the gradients of h_n/c_n arrive as None
+# when the loss does not use them (set_materialize_grads(False)); both reach the C ABI
+# as NULL, which it reads as zeros, so no zero tensors are filled per step.
 
 
 class RecurrentFn(torch.autograd.Function):
@@ -82,6 +87,7 @@ class RecurrentFn(torch.autograd.Function):
     def forward(ctx, x, h0, c0, w_ih, w_hh, b_ih, b_hh, a):
         T, B, D, H = _check(x, h0, c0, w_ih, w_hh, b_ih, b_hh, a)
         x, h0, c0, w_ih, w_hh, b_ih, b_hh, a = map(_c, (x, h0, c0, w_ih, w_hh, b_ih, b_hh, a))
+        ctx.set_materialize_grads(False)
         h_save = x.new_empty(T + 1, B, H)
         c_save = x.new_empty(T + 1, B, H)
         gact = x.new_empty(T, B, H, 4)
@@ -103,8 +109,7 @@ class RecurrentFn(torch.autograd.Function):
         x, w_ih, w_hh, b_hh, a, h_save, c_save, gact, tanh_c = ctx.saved_tensors
         T, B, D, H = ctx.dims
         dout = _grad_or_zeros(dout, h_save[1:])
-        dh_n = _grad_or_zeros(dh_n, h_save[T])
-        dc_n = _grad_or_zeros(dc_n, c_save[T])
+        dh_n, dc_n = _c(dh_n), _c(dc_n)
         need = ctx.needs_input_grad
         dx = torch.empty_like(x) if need[0] else None
         dh0 = x.new_empty(B, H) if need[1] else None
@@ -137,6 +142,7 @@ class ParallelFn(torch.autograd.Function):
     def forward(ctx, x, h0, c0, w_ih, w_hh, b_ih, b_hh, a, eps):
         T, B, D, H = _check(x, h0, c0, w_ih, w_hh, b_ih, b_hh, a)
         x, c0, w_ih, b_ih = map(_c, (x, c0, w_ih, b_ih))
+        ctx.set_materialize_grads(False)
         gates = x.new_empty(T, B, 4 * H)
         out = x.new_empty(T, B, H)
         c_seq = x.new_empty(T, B, H)
@@ -153,8 +159,7 @@ class ParallelFn(torch.autograd.Function):
         x, c0, w_ih, gates, c_seq = ctx.saved_tensors
         T, B, D, H = ctx.dims
         dout = _grad_or_zeros(dout, c_seq)
-        dh_n = _grad_or_zeros(dh_n, c0)
-        dc_n = _grad_or_zeros(dc_n, c0)
+        dh_n, dc_n = _c(dh_n), _c(dc_n)
         need = ctx.needs_input_grad
         dx = torch.empty_like(x) if need[0] else None
         dc0 = x.new_empty(B, H) if need[2] else None

@@ -193,3 +193,41 @@ def test_repeated_calls_are_deterministic(dev):
         outs.append(out.detach().clone())
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
+
+
+@pytest.mark.parametrize("mode", ["rec1", "rec2", "par"])
+def test_null_states_equal_explicit_zeros(dev, mode):
+    """hx=None and an unused h_n/c_n reach the kernels as NULL pointers, read as zeros.
+    The result must equal, bit for bit, the run with explicit zero states and a loss that
+    touches h_n/c_n with weight zero (zero tensors passed instead of NULL)."""
+    T, B, D, H = 20, 6, 16, 40
+    print(f"null states {mode}", flush=True)
+    if mode != "par":
+        prlstm_amd.set_recurrent_path(1 if mode == "rec1" else 2)
+    torch.manual_seed(0)
+    m = prlstm_amd.HeadStartLSTM(D, H, parallel=(mode == "par")).to(dev)
+    with torch.no_grad():
+        m.a.fill_(0.6)
+        m.bias_ih_l0.normal_()
+    x = torch.randn(T, B, D, device=dev)
+    w = torch.randn(T, B, H, device=dev)
+    runs = []
+    for explicit in (False, True):
+        m.zero_grad(set_to_none=True)
+        xx = x.clone().requires_grad_(True)
+        if explicit:
+            hx = (torch.zeros(1, B, H, device=dev), torch.zeros(1, B, H, device=dev))
+            out, (h_n, c_n) = m(xx, hx)
+            loss = (out * w).sum() + (h_n * 0).sum() + (c_n * 0).sum()
+        else:
+            out, (h_n, c_n) = m(xx)
+            loss = (out * w).sum()
+        loss.backward()
+        res = {"out": out, "h_n": h_n, "c_n": c_n, "dx": xx.grad}
+        res.update({n: p.grad for n, p in m.named_parameters()})
+        runs.append(res)
+    for k, v in runs[0].items():
+        if v is None:
+            assert runs[1][k] is None, k
+        else:
+            assert torch.equal(v, runs[1][k]), k

@@ -168,10 +168,15 @@ int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s) {
     EpiPartial epi{P, d.M, d.N};
     HSL_CHECK(dispatch(t, make_args(d), d.trans_a, d.trans_b, splits, epi, s, d.acc64));
   }
-  const size_t total = (size_t)d.M * d.N;
+  return splitk_reduce(P, splits, d.bias, d.C, d.M, d.N, d.ldc, s);
+}
+
+int splitk_reduce(const float* P, int splits, const float* bias, float* C, int M, int N, int ldc, hipStream_t s) {
+  const size_t total = (size_t)M * N;
+  if (total == 0) return HSL_OK;
   int blocks = (int)((total + 255) / 256);
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, P, splits, d.bias, d.C, d.M, d.N, d.ldc);
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, P, splits, bias, C, M, N, ldc);
   HSL_HIP(hipGetLastError());
   return HSL_OK;
 }

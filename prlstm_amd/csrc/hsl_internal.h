@@ -78,6 +78,9 @@ int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s);
 // planes); *used receives the number of planes written (<= splits).  Used by the
 // fused epilogues of the weight gradients.
 int gemm_partials(const GemmDesc& d, float* partials, int splits, hipStream_t s, int* used);
+// C[M][N] (row stride ldc) = sum over the `splits` fp32 planes P[z][M][N], added in fp64
+// (+ bias[N] when non-null).
+int splitk_reduce(const float* P, int splits, const float* bias, float* C, int M, int N, int ldc, hipStream_t s);
 int gemm_pick_splits(int M, int N, int K, int acc64);
 
 // ---- shared finalisation (recurrent.hip) ------------------------------------------

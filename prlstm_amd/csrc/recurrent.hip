@@ -22,6 +22,7 @@
 // v_mfma_f32_4x4x1_16b_f32 layout (verified on gfx950): A from lane 4b+i is
 // A_b[i][0], B from lane 4b+j is B_b[0][j], result lane 4b+j, reg i holds D_b[i][j].
 // With cbsz=4, abid=0 every block uses block 0's A (lanes 0-3).
+#include <cstdlib>
 #include <type_traits>
 
 #include "gemm_core.h"
@@ -64,6 +65,15 @@ __global__ void scale_whh_kernel(const float* __restrict__ w_hh, const float* __
   }
   if (bs) {
     for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < 4 * H; n += gridDim.x * blockDim.x) bs[n] = a[n / H] * b_hh[n];
+  }
+}
+
+// out[e] = sum_z P[z][e] over fp64 planes, rounded once to fp32.
+__global__ void sum_planes_f64_kernel(const double* __restrict__ P, int planes, float* __restrict__ out, size_t n) {
+  for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < n; e += (size_t)gridDim.x * blockDim.x) {
+    double acc = 0.0;
+    for (int z = 0; z < planes; ++z) acc += P[(size_t)z * n + e];
+    out[e] = (float)acc;
   }
 }
 
@@ -653,6 +663,14 @@ struct PBwdArgs {
   int T, B, H, Hp, NG, NGX, Bg, NW;
   int device_scope;
   long long spin;
+  // weight-gradient waves (launches with 512 threads): fp32 partial sums of
+  // dW_hh_s = dg^T h_prev and dW_ih = dg^T x, one plane per (chunk of TS steps, group)
+  const float* h_save;  // [T+1][B][H]
+  const float* x;       // [T][B][D]
+  float* wph;           // [chunks*NG][4H][H] fp32
+  double* wpx;          // [NG][4H][D] fp64 (when dW_ih is fused)
+  int D, TS;
+  int store_dg;  // 0: dgates are not needed after the kernel (not written)
 };
 
 // Backward.  Wave q owns batch slot q for the dh receive and the cell, and the q-th
@@ -670,9 +688,9 @@ struct PBwdArgs {
 //
 // As in the forward, every access uses a uniform base plus a 32-bit lane offset and the
 // hand-off scope is a compile-time choice, keeping the per-step dependent chain short.
-template <int KQ, bool FAST>
+template <int KQ, bool FAST, bool GW>
 __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg, float (&dgl)[2][4][68],
-                                             int& abort_flag) {
+                                             int* mdone, int& abort_flag) {
   constexpr int HP = 4 * KQ;
   constexpr int CG = (KQ + 63) / 64;     // 64-column groups per wave
   constexpr int NWMAX = HP / kUnits;     // workgroups per group at most
@@ -813,7 +831,7 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
       for (int gt = 0; gt < 4; ++gt) dgl[s & 1][q][gt * kUnits + uu] = d[gt];
     }
     if (src) words_clear<PER, FAST>(const_cast<float*>(src), roff);
-    if (c_ok) {
+    if (c_ok && p.store_dg) {
       float* dgp = dg_row + (size_t)t * plane4;
 #pragma unroll
       for (int gt = 0; gt < 4; ++gt) __builtin_nontemporal_store(d[gt], byte_at(dgp, 4u * (gt * H + cu)));
@@ -837,17 +855,24 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[c] = mfma4_bcast(dv[c], wreg[cg][4 * kk + c], acc[c], kk);
       }
+      if (GW && cg == CG - 1) {
+        // the matrix pipe is free from here until the next step's products: tell the
+        // weight-gradient wave on this SIMD (every lane writes the same value)
+        __builtin_amdgcn_sched_barrier(0);
+        *reinterpret_cast<volatile int*>(&mdone[q]) = s + 1;
+        __builtin_amdgcn_sched_barrier(0);
+      }
       const f4 part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
       if (col_ok[cg]) {
         const unsigned c = col[cg];
         const unsigned off = (c >> 4) * RW + poff0 + (PER == 1 ? 1u : 2u) * (c & 15u);
         if (full_group) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) word_put<FAST>(dst_slot, off + i * 64 * PER, canon_nan(part[i]));
+          for (int i = 0; i < 4; ++i) word_put<FAST>(dst_slot + i * 64 * PER, off, canon_nan(part[i]));
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (i < Bg && grp * Bg + i < B) word_put<FAST>(dst_slot, off + i * 64 * PER, canon_nan(part[i]));
+            if (i < Bg && grp * Bg + i < B) word_put<FAST>(dst_slot + i * 64 * PER, off, canon_nan(part[i]));
         }
       }
     }
@@ -860,21 +885,250 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
   }
 }
 
-template <int KQ>
-__global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
+// Weight-gradient waves (waves 4-7 of a 512-thread backward workgroup).  The recurrent
+// waves leave the matrix pipes idle for most of a step (waiting for partials, running
+// the cell), so a second wave per SIMD accumulates this workgroup's 64 rows of
+//   dW_hh_s[n][k] += sum_b dg_t[b][n] h_{t-1}[b][k],   dW_ih[n][d] += sum_b dg_t[b][n] x_t[b][d]
+// in registers while they wait.  Per step, the dgates of the four batch slots are read
+// from the LDS copy the recurrent waves already make (dgl, valid between the step's
+// barrier and the next), h_{t-1} and x_t rows are loaded one step ahead, and the
+// products are v_mfma_f32_32x32x2_f32 with the batch as the reduction index (two
+// instructions per 32x32 tile).  The products start only after the recurrent waves
+// have issued theirs (mdone), so they fill the idle part of the step.  Wave w owns the
+// 32-column tiles w, w+4, ... of h (HT of them) and of x (XT).
+//
+// Accuracy: no fp32 running sum spans more than a few hundred products.  dW_hh_s is
+// written as an fp32 partial plane every TS steps (its gradient dW_hh = a dW_hh_s is
+// a-scaled); dW_ih goes into an fp64 accumulator in LDS (64 rows x D, written once as
+// an fp64 plane per group): at the start of each step one of the wave's 2*XT
+// accumulator tiles is added to it with ds_add_f64 (no returned value) and restarted,
+// so an fp32 run covers 2*XT steps.  The planes are summed in fp64 afterwards.
+//
+// The wave takes part in every workgroup barrier of the recurrent waves (one per step)
+// and leaves when the group aborts, as they do.
+constexpr int kXaccLdsBytes = 64 * 256 * 8;  // fp64 dW_ih accumulator for D <= 256
+
+template <int KQ, int XT>
+__device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg, float (&dgl)[2][4][68],
+                                              int* mdone, double* xacc, int& abort_flag) {
+  constexpr int HT = KQ >= 32 ? KQ / 32 : 1;  // h column tiles per wave (4*KQ >= H)
+  constexpr int XA = XT > 0 ? XT : 1;
+  const int T = p.T, B = p.B, H = p.H, D = p.D, Bg = p.Bg, NG = p.NG, TS = p.TS;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) - 4);
+  const int half = lane >> 5, l32 = lane & 31;
+  // k index of the products = batch slot 2*ks + half
+  bool bok[2];
+  int brow[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int b = 2 * ks + half, cb = grp * Bg + b;
+    bok[ks] = b < Bg && cb < B;
+    brow[ks] = bok[ks] ? cb : 0;
+  }
+  const int nth = (H + 31) / 32, ntx = (D + 31) / 32;
+  // operand columns: clamped in range, so that the loads need no condition (a column
+  // past H or D only feeds an output column that is never written)
+  auto hcol = [&](int i) { return min((w + 4 * i) * 32 + l32, H - 1); };
+  auto xcol = [&](int i) { return min((w + 4 * i) * 32 + l32, D - 1); };
+  f16v acch[HT][2], accx[XA][2];
+  auto zero_h = [&]() {
+#pragma unroll
+    for (int i = 0; i < HT; ++i)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) acch[i][rt] = f16v{};
+  };
+  auto zero_x = [&]() {
+#pragma unroll
+    for (int i = 0; i < XA; ++i)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) accx[i][rt] = f16v{};
+  };
+  zero_h();
+  zero_x();
+  // D-layout of a 32x32 tile: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column l%32
+  auto tile_row = [&](int rt, int r) { return rt * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
+  if constexpr (XT > 0) {
+#pragma unroll
+    for (int i = 0; i < XT; ++i) {
+      if (w + 4 * i >= ntx) continue;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xacc[tile_row(rt, r) * 256 + (w + 4 * i) * 32 + l32] = 0.0;
+    }
+  }
+
+  // operand rows of step s (time t = T-1-s): h_{t-1} = h_save[t], x_t
+  struct Ops {
+    float h[HT][2];
+    float x[XA][2];
+  };
+  auto load_ops = [&](int t, Ops& o) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const float* hr = p.h_save + ((size_t)t * B + brow[ks]) * H;
+#pragma unroll
+      for (int i = 0; i < HT; ++i) o.h[i][ks] = hr[hcol(i)];
+      if constexpr (XT > 0) {
+        const float* xr = p.x + ((size_t)t * B + brow[ks]) * D;
+#pragma unroll
+        for (int i = 0; i < XT; ++i) o.x[i][ks] = xr[xcol(i)];
+      }
+    }
+  };
+  // Row r64 = R0 + 4*half of a tile register (R0 = rt*32 + 8(r/4) + r%4) is gate R0/16,
+  // unit wg*16 + R0%16 + 4*half: the store address splits into a uniform part (R0) and
+  // a 32-bit lane part shared by all registers.
+  const int ulane = wg * kUnits + 4 * half;
+  auto dump_h = [&](int chunk) {
+    float* const plane = p.wph + ((size_t)chunk * NG + grp) * 4 * H * H;
+#pragma unroll
+    for (int i = 0; i < HT; ++i) {
+      const int c = (w + 4 * i) * 32 + l32;
+      if (w + 4 * i >= nth) continue;
+      const unsigned lo = 4u * ((unsigned)ulane * H + c);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int R0 = rt * 32 + 8 * (r >> 2) + (r & 3);
+          float* const rb = plane + (size_t)((R0 >> 4) * H + (R0 & 15)) * H;
+          if (ulane + (R0 & 15) < H && c < H) *byte_at(rb, lo) = acch[i][rt][r];
+        }
+    }
+    zero_h();
+  };
+  // adds accumulator tile f = 2*i + rt of every wave whose flag is set to the fp64 copy
+  auto fold_x = [&](int sel) {
+#pragma unroll
+    for (int i = 0; i < XT; ++i) {
+      if (w + 4 * i >= ntx) continue;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        if (sel >= 0 && sel != 2 * i + rt) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          __hip_atomic_fetch_add(&xacc[tile_row(rt, r) * 256 + (w + 4 * i) * 32 + l32], (double)accx[i][rt][r],
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        accx[i][rt] = f16v{};
+      }
+    }
+  };
+
+  // One operand set: the next step's rows are requested right after this step's
+  // products are issued, and have arrived long before the next barrier ends.
+  auto step = [&](int s, Ops& cur) __attribute__((always_inline)) -> bool {
+    lds_barrier();  // the recurrent waves' barrier of step s: dgl[s&1] is complete
+    if (abort_flag) return false;
+    float a[2][2];  // [row tile][ks]
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) a[rt][ks] = dgl[s & 1][2 * ks + half][rt * 32 + l32];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (!bok[ks]) {  // operand rows of absent batch slots are zero (their dgates are zero too)
+#pragma unroll
+        for (int i = 0; i < HT; ++i) cur.h[i][ks] = 0.f;
+#pragma unroll
+        for (int i = 0; i < XA; ++i) cur.x[i][ks] = 0.f;
+      }
+    }
+    // one accumulator tile goes to the fp64 copy while the recurrent waves still issue
+    // their products (its last products were issued a step ago)
+    if constexpr (XT > 0)
+      if (s > 0) fold_x((s - 1) % (2 * XT));
+    // wait until every recurrent wave has issued this step's products (bounded like
+    // every other wait of the persistent kernels)
+    const long long t0 = wall_clock64();
+    while (true) {
+      const int m0 = reinterpret_cast<volatile int*>(mdone)[0], m1 = reinterpret_cast<volatile int*>(mdone)[1];
+      const int m2 = reinterpret_cast<volatile int*>(mdone)[2], m3 = reinterpret_cast<volatile int*>(mdone)[3];
+      if (min(min(m0, m1), min(m2, m3)) > s) break;
+      if (abort_flag) return false;
+      if (wall_clock64() - t0 > p.spin) {
+        abort_flag = 1;
+        atomicOr(p.err, 1);
+        return false;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int i = 0; i < HT; ++i) {
+      if (w + 4 * i >= nth) continue;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          acch[i][rt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[rt][ks], cur.h[i][ks], acch[i][rt], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < XT; ++i) {
+      if (w + 4 * i >= ntx) continue;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          accx[i][rt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[rt][ks], cur.x[i][ks], accx[i][rt], 0, 0, 0);
+    }
+    if (s + 1 < T) load_ops(T - 2 - s, cur);
+    if (s % TS == TS - 1 || s == T - 1) dump_h(s / TS);
+    return true;
+  };
+
+  Ops op;
+  if (T > 0) load_ops(T - 1, op);
+  for (int s = 0; s < T; ++s)
+    if (!step(s, op)) return;
+
+  if constexpr (XT > 0) {  // this group's dW_ih rows as an fp64 plane
+    fold_x(-1);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the wave's own LDS adds
+    double* const plane = p.wpx + (size_t)grp * 4 * H * D;
+#pragma unroll
+    for (int i = 0; i < XT; ++i) {
+      const int c = (w + 4 * i) * 32 + l32;
+      if (w + 4 * i >= ntx) continue;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int r64 = tile_row(rt, r), u = wg * kUnits + (r64 & 15);
+          if (u < H && c < D) plane[((size_t)(r64 >> 4) * H + u) * D + c] = xacc[r64 * 256 + c];
+        }
+    }
+  }
+}
+
+// XT < 0: 256 threads, recurrent waves only (weight gradients by separate GEMMs).
+// XT >= 0: 512 threads; waves 4-7 accumulate dW_hh_s and, when XT > 0, dW_ih.
+template <int KQ, int XT>
+__global__ __launch_bounds__(XT >= 0 ? 512 : 256, 1) void rec_bwd_persistent(PBwdArgs p) {
   constexpr int NWMAX = 4 * KQ / kUnits;
+  constexpr bool GW = XT >= 0;
   __shared__ float dgl[2][4][64 + 4];  // [step parity][batch slot][gate row]
   __shared__ int abort_flag;
+  __shared__ int mdone[4];  // steps whose products recurrent wave q has issued
   const int grp = blockIdx.x % p.NGX, wg = blockIdx.x / p.NGX;
   if (grp >= p.NG) return;
   if (threadIdx.x == 0) abort_flag = 0;
+  if (threadIdx.x < 4) mdone[threadIdx.x] = 0;
   const bool fast = agree_placement(p.hello + (size_t)grp * NWMAX, wg, p.NW, p.spin, &abort_flag, p.err) &&
                     !p.device_scope;
   if (abort_flag) return;
+  if constexpr (GW) {
+    if (threadIdx.x >= 256) {
+      extern __shared__ double xacc[];  // [64][256] fp64 dW_ih accumulator (dynamic LDS)
+      rec_bwd_wgrad<KQ, (XT > 0 ? XT : 0)>(p, grp, wg, dgl, mdone, xacc, abort_flag);
+      return;
+    }
+    __builtin_amdgcn_s_setprio(2);  // the recurrent chain first when both waves can issue
+  }
   if (fast)
-    rec_bwd_body<KQ, true>(p, grp, wg, dgl, abort_flag);
+    rec_bwd_body<KQ, true, GW>(p, grp, wg, dgl, mdone, abort_flag);
   else
-    rec_bwd_body<KQ, false>(p, grp, wg, dgl, abort_flag);
+    rec_bwd_body<KQ, false, GW>(p, grp, wg, dgl, mdone, abort_flag);
 }
 
 // ---------------------------------------------------------------------------------
@@ -883,6 +1137,7 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_persistent(PBwdArgs p) {
 struct PersistentPlan {
   bool ok = false;
   int KQ = 0, Hp = 0, NG = 0, NGX = 0, Bg = 0, NW = 0, grid = 0;
+  int XT = -1;  // backward: -1 no weight-gradient waves, 0 dW_hh only, 2 dW_hh and dW_ih
 };
 
 int pick_kq(int H) {
@@ -894,14 +1149,37 @@ int pick_kq(int H) {
 }
 
 template <class K>
-int max_resident(K kernel, int* out) {
+int max_resident(K kernel, int threads, int* out) {
   int occ = 0;
-  HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 256, kPadLdsBytes));
+  HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, kPadLdsBytes));
   *out = occ;
   return HSL_OK;
 }
 
-int plan_persistent(int B, int H, bool bwd, PersistentPlan* pl) {
+// Weight-gradient waves in the persistent backward: on unless HSL_FUSED_WGRAD=0.
+bool fused_wgrad_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("HSL_FUSED_WGRAD");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+template <int KQ>
+int bwd_resident(int xt, int* occ) {
+  switch (xt) {
+    case -1: return max_resident(rec_bwd_persistent<KQ, -1>, 256, occ);
+    case 0: return max_resident(rec_bwd_persistent<KQ, 0>, 512, occ);
+    default: {
+      int o = 0;
+      HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, rec_bwd_persistent<KQ, 2>, 512, kXaccLdsBytes));
+      *occ = o;
+      return HSL_OK;
+    }
+  }
+}
+
+int plan_persistent(int B, int H, int D, bool bwd, PersistentPlan* pl) {
   *pl = PersistentPlan{};
   const int mode = recurrent_path_mode();
   if (mode == 1) return HSL_OK;
@@ -919,17 +1197,40 @@ int plan_persistent(int B, int H, bool bwd, PersistentPlan* pl) {
   p.NGX = (p.NG + di.num_xcds - 1) / di.num_xcds * di.num_xcds;
   p.NW = (H + kUnits - 1) / kUnits;
   p.grid = p.NGX * p.NW;
+  // dW_ih joins the weight-gradient waves when its 32-column tiles fit two per wave
+  if (bwd && fused_wgrad_enabled()) p.XT = (D > 0 && D <= 256) ? 2 : 0;
   int occ = 0;
-  switch (kq) {
-    case 16: HSL_CHECK(bwd ? max_resident(rec_bwd_persistent<16>, &occ) : max_resident(rec_fwd_persistent<16>, &occ)); break;
-    case 32: HSL_CHECK(bwd ? max_resident(rec_bwd_persistent<32>, &occ) : max_resident(rec_fwd_persistent<32>, &occ)); break;
-    case 64: HSL_CHECK(bwd ? max_resident(rec_bwd_persistent<64>, &occ) : max_resident(rec_fwd_persistent<64>, &occ)); break;
-    default: HSL_CHECK(bwd ? max_resident(rec_bwd_persistent<128>, &occ) : max_resident(rec_fwd_persistent<128>, &occ)); break;
+  for (;;) {
+    if (bwd) {
+      switch (kq) {
+        case 16: HSL_CHECK(bwd_resident<16>(p.XT, &occ)); break;
+        case 32: HSL_CHECK(bwd_resident<32>(p.XT, &occ)); break;
+        case 64: HSL_CHECK(bwd_resident<64>(p.XT, &occ)); break;
+        default: HSL_CHECK(bwd_resident<128>(p.XT, &occ)); break;
+      }
+    } else {
+      switch (kq) {
+        case 16: HSL_CHECK(max_resident(rec_fwd_persistent<16>, 256, &occ)); break;
+        case 32: HSL_CHECK(max_resident(rec_fwd_persistent<32>, 256, &occ)); break;
+        case 64: HSL_CHECK(max_resident(rec_fwd_persistent<64>, 256, &occ)); break;
+        default: HSL_CHECK(max_resident(rec_fwd_persistent<128>, 256, &occ)); break;
+      }
+    }
+    // every workgroup must be resident at once: the waits are between workgroups
+    p.ok = occ >= 1 && (long)occ * di.num_cus >= p.grid;
+    if (p.ok || p.XT < 0) break;
+    p.XT = -1;  // retry without the weight-gradient waves
   }
-  // every workgroup must be resident at once: the waits are between workgroups
-  p.ok = occ >= 1 && (long)occ * di.num_cus >= p.grid;
   *pl = p;
   return HSL_OK;
+}
+
+// Steps per fp32 partial plane of the fused weight gradients: at most 128 steps
+// (512 products per running sum at four batch slots) while there are at most 8 planes
+// per group.
+int wgrad_chunks(int T) {
+  const int c = (T + 127) / 128;
+  return c < 1 ? 1 : (c > 8 ? 8 : c);
 }
 
 inline int grid_for(size_t n) {
@@ -1010,6 +1311,12 @@ size_t gemm_region_bytes(int T, int B, int D, int H) {
   if (g6 > need) need = g6;
   const size_t g7 = gemm_ws_bytes(B, H, 4 * H, 1);
   if (g7 > need) need = g7;
+  if (pick_kq(H) && fused_wgrad_enabled()) {  // planes of the fused weight gradients
+    const size_t ng = (B + 3) / 4;
+    const size_t wg = sizeof(float) * wgrad_chunks(T) * ng * 4 * H * H +
+                      (D <= 256 ? sizeof(double) * ng * 4 * H * D : 0);
+    if (wg > need) need = wg;
+  }
   return need;
 }
 
@@ -1046,8 +1353,12 @@ void launch_fwd_persistent(const PFwdArgs& a, int grid, hipStream_t s) {
   hipLaunchKernelGGL(rec_fwd_persistent<KQ>, dim3(grid), dim3(256), kPadLdsBytes, s, a);
 }
 template <int KQ>
-void launch_bwd_persistent(const PBwdArgs& a, int grid, hipStream_t s) {
-  hipLaunchKernelGGL(rec_bwd_persistent<KQ>, dim3(grid), dim3(256), kPadLdsBytes, s, a);
+void launch_bwd_persistent(const PBwdArgs& a, int grid, int xt, hipStream_t s) {
+  switch (xt) {
+    case -1: hipLaunchKernelGGL((rec_bwd_persistent<KQ, -1>), dim3(grid), dim3(256), kPadLdsBytes, s, a); break;
+    case 0: hipLaunchKernelGGL((rec_bwd_persistent<KQ, 0>), dim3(grid), dim3(512), kPadLdsBytes, s, a); break;
+    default: hipLaunchKernelGGL((rec_bwd_persistent<KQ, 2>), dim3(grid), dim3(512), kXaccLdsBytes, s, a); break;
+  }
 }
 
 }  // namespace
@@ -1090,7 +1401,7 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
   if (!ws || ws_bytes < need) return fail(HSL_ERR_ARG, "hsl_rec_fwd: workspace %zu bytes, need %zu", ws_bytes, need);
 
   PersistentPlan pl;
-  HSL_CHECK(plan_persistent(B, H, false, &pl));
+  HSL_CHECK(plan_persistent(B, H, D, false, &pl));
   if (recurrent_path_mode() == 2 && !pl.ok)
     return fail(HSL_ERR_UNSUPPORTED, "persistent path does not fit (B=%d H=%d)", B, H);
 
@@ -1188,21 +1499,37 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
   }
 
   PersistentPlan pl;
-  HSL_CHECK(plan_persistent(B, H, true, &pl));
+  HSL_CHECK(plan_persistent(B, H, D, true, &pl));
   if (recurrent_path_mode() == 2 && !pl.ok)
     return fail(HSL_ERR_UNSUPPORTED, "persistent path does not fit (B=%d H=%d)", B, H);
 
+  // fused weight gradients: fp32 partial planes [nsplit][4H][H] and [nsplit][4H][D]
+  // (the GEMM region, which the GEMMs below only use after these planes are reduced)
+  const bool fused = pl.ok && pl.XT >= 0;
+  const bool fused_ih = fused && pl.XT > 0;
+  int wts = T, nsplit = 0;
+  float* const wph = w.gemm;
+  double* wpx = nullptr;
+  if (fused) {
+    const int nch = wgrad_chunks(T);
+    wts = (T + nch - 1) / nch;
+    nsplit = (T + wts - 1) / wts * pl.NG;
+    wpx = reinterpret_cast<double*>(wph + (size_t)nsplit * 4 * H * H);
+  }
   if (pl.ok) {
     HSL_CHECK(clear_slots(w.pbuf, w.pfloats, s));
     HSL_CHECK(zero_words(w.hello, w.hwords, s));
     PBwdArgs pa{dout, dh_n, dc_n, c_save, gact, tanh_c, w_hh, a, w.dgates, w.db_part, dh0, dc0, w.pbuf, w.hello,
-                w.err, T, B, H, pl.Hp, pl.NG, pl.NGX, pl.Bg, pl.NW, exchange_scope_mode(), spin_timeout_ticks()};
+                w.err, T, B, H, pl.Hp, pl.NG, pl.NGX, pl.Bg, pl.NW, exchange_scope_mode(), spin_timeout_ticks(),
+                h_save, x, wph, fused_ih ? wpx : nullptr, D, wts,
+                // dgates feed the GEMMs for whatever the kernel does not produce itself
+                (!fused_ih || dx != nullptr) ? 1 : 0};
     const int slot = timing_begin(kTimeRecBwd, s);
     switch (pl.KQ) {
-      case 16: launch_bwd_persistent<16>(pa, pl.grid, s); break;
-      case 32: launch_bwd_persistent<32>(pa, pl.grid, s); break;
-      case 64: launch_bwd_persistent<64>(pa, pl.grid, s); break;
-      default: launch_bwd_persistent<128>(pa, pl.grid, s); break;
+      case 16: launch_bwd_persistent<16>(pa, pl.grid, pl.XT, s); break;
+      case 32: launch_bwd_persistent<32>(pa, pl.grid, pl.XT, s); break;
+      case 64: launch_bwd_persistent<64>(pa, pl.grid, pl.XT, s); break;
+      default: launch_bwd_persistent<128>(pa, pl.grid, pl.XT, s); break;
     }
     HSL_HIP(hipGetLastError());
     timing_end(slot, s);
@@ -1241,19 +1568,26 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
   }
 
   // dW_hh_s = dg^T h_prev (staged partials), then dW_hh = a dW_hh_s and the da row sums
-  int splits = 1;
-  {
+  int splits = nsplit;
+  if (!fused) {
     GemmDesc g4{w.dgates, h_save, nullptr, w.gemm, 4 * H, H, TB, 4 * H, H, H, 1, 0, 1};
     HSL_CHECK(gemm_partials(g4, w.gemm, gemm_pick_splits(4 * H, H, TB, 1), s, &splits));
   }
-  hipLaunchKernelGGL(whh_grad_finalize_kernel, dim3(4 * H), dim3(256), 0, s, w.gemm, splits, w_hh, a, dw_hh,
+  hipLaunchKernelGGL(whh_grad_finalize_kernel, dim3(4 * H), dim3(256), 0, s, wph, splits, w_hh, a, dw_hh,
                      w.rowdot, H);
   HSL_HIP(hipGetLastError());
   HSL_CHECK(bias_grads_from_parts(w.db_part, B, w.rowdot, b_hh, a, db_ih, db_hh, da, H, s));
   // dW_ih = dg^T x ; dx = dg W_ih
+  if (fused_ih) {
+    const size_t n = (size_t)4 * H * D;
+    hipLaunchKernelGGL(sum_planes_f64_kernel, dim3(grid_for(n)), dim3(256), 0, s, wpx, pl.NG, dw_ih, n);
+    HSL_HIP(hipGetLastError());
+  }
   if (D > 0) {
-    GemmDesc g5{w.dgates, x, nullptr, dw_ih, 4 * H, D, TB, 4 * H, D, D, 1, 0, 1};
-    HSL_CHECK(gemm_run(g5, w.gemm, w.gemm_bytes, s));
+    if (!fused_ih) {
+      GemmDesc g5{w.dgates, x, nullptr, dw_ih, 4 * H, D, TB, 4 * H, D, D, 1, 0, 1};
+      HSL_CHECK(gemm_run(g5, w.gemm, w.gemm_bytes, s));
+    }
     if (dx) {
       GemmDesc g6{w.dgates, w_ih, nullptr, dx, TB, D, 4 * H, 4 * H, D, D, 0, 0, 1};
       HSL_CHECK(gemm_run(g6, w.gemm, w.gemm_bytes, s));

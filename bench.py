@@ -3,14 +3,16 @@
 
 Workload (the headline): recurrent mode, fp32,
 T=256 B=32 D=256 H=512, a=1e-4, x ~ N(0,1), nn.LSTM init, h0=c0=0,
-loss = out.sum(); one step = forward + backward (all parameter gradients and
-dx), captured whole in one HIP graph and replayed.  Synthetic data, seeded.
+loss = out.sum(); one step = forward + backward (all parameter gradients; x is
+data, so no dx, as in the reference's training loop), captured whole in one HIP
+graph and replayed.  Synthetic data, seeded.
 
 Prints ONE JSON line:
   value       timesteps*batch/s = T*B / step time
   roofline    the dominant kernel of the step (persistent recurrent kernel),
               algorithmic fp32 MFMA FLOPs per launch / its mean launch time,
-              timed with HIP events on its launch stream
+              timed with HIP events on its launch stream; the backward kernel's
+              FLOPs include the weight-gradient products it accumulates
   cpu_baseline the CPU restatement of the reference torch backend (oracle/),
               same workload, timed on this host's cores
   scan        configs[4] parallel scan (T=4096 B=16 H=1024) forward and
@@ -98,8 +100,9 @@ def bench_gpu(args):
         if n:
             kern[k] = tot / n
     _lib.set_timing(False)
-    log(f"graph step {ms:.4f} ms (wall {wall_ms:.4f} ms), path {path}, kernels(ms) {kern}")
-    return ms, wall_ms, kern, path
+    fused = _lib.last_backward_fused()
+    log(f"graph step {ms:.4f} ms (wall {wall_ms:.4f} ms), path {path}, fused wgrad {fused}, kernels(ms) {kern}")
+    return ms, wall_ms, kern, path, fused
 
 
 def bench_scan(args):
@@ -211,12 +214,15 @@ def main():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
 
-    ms, wall_ms, kern, path = bench_gpu(args)
+    ms, wall_ms, kern, path, fused = bench_gpu(args)
     scan = None if args.no_scan else bench_scan(args)
     cpu = None if args.no_cpu else bench_cpu(args)
 
     step_flops = 24.0 * T * B * H * (D + H)           # algorithmic fwd+bwd FLOPs
     rec_flops = 2.0 * T * B * H * 4 * H               # recurrent product of one direction
+    # per-launch FLOPs: the backward kernel also accumulates dW_hh (and dW_ih) when fused
+    kflops = {"rec_fwd": rec_flops, "step_fwd": rec_flops, "step_bwd": rec_flops,
+              "rec_bwd": rec_flops * (1 + (fused >= 1)) + (2.0 * T * B * 4 * H * D if fused == 2 else 0.0)}
     if "rec_fwd" in kern or "rec_bwd" in kern:
         name = max((k for k in ("rec_fwd", "rec_bwd") if k in kern), key=lambda k: kern[k])
         kname = {"rec_fwd": "rec_fwd_persistent", "rec_bwd": "rec_bwd_persistent"}[name]
@@ -224,7 +230,7 @@ def main():
         name = max((k for k in ("step_fwd", "step_bwd") if k in kern), key=lambda k: kern[k])
         kname = name + " (per-step launches)"
     kms = kern[name]
-    achieved = rec_flops / (kms * 1e-3) / 1e12
+    achieved = kflops[name] / (kms * 1e-3) / 1e12
     value = T * B / (ms * 1e-3)
     line = {
         "metric": METRIC,
@@ -246,7 +252,7 @@ def main():
                      "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic(kname) if kname.endswith("persistent") else None,
-                     "kernel_ms": round(kms, 5), "flops_per_launch": rec_flops},
+                     "kernel_ms": round(kms, 5), "flops_per_launch": kflops[name]},
         "step_tflops": round(step_flops / (ms * 1e-3) / 1e12, 3),
         "kernels_ms": {k: round(v, 5) for k, v in kern.items()},
         "wall_ms_per_step": round(wall_ms, 5),

@@ -66,6 +66,10 @@ int hsl_set_exchange_scope(int mode);
 /* Which path the last hsl_rec_fwd / hsl_rec_bwd on this host thread used:
  * 1 = per-step, 2 = persistent. */
 int hsl_last_recurrent_path(void);
+/* Whether the last hsl_rec_bwd (in this process, on any thread) accumulated the
+ * weight gradients inside the persistent kernel: 0 = no (separate GEMMs), 1 = dW_hh,
+ * 2 = dW_hh and dW_ih (D <= 256).  (No reference counterpart.) */
+int hsl_last_backward_fused(void);
 /* Measurement hook (no reference counterpart): with timing on, the library
  * records a pair of HIP events on the launch stream around each launch of the
  * persistent recurrent kernels (kind 1 forward, 2 backward), the scan kernels

@@ -25,6 +25,7 @@ SIGNATURES = {
     "hsl_set_recurrent_path": (_I, [_I]),
     "hsl_set_spin_timeout_us": (ctypes.c_longlong, [ctypes.c_longlong]),
     "hsl_last_recurrent_path": (_I, []),
+    "hsl_last_backward_fused": (_I, []),
     "hsl_set_exchange_scope": (_I, [_I]),
     "hsl_poll_error": (_I, [_P, _P, _P]),
     "hsl_set_timing": (_I, [_I]),
@@ -103,6 +104,12 @@ def set_spin_timeout_us(us):
 
 def last_recurrent_path():
     return load().hsl_last_recurrent_path()
+
+
+def last_backward_fused():
+    """0: weight gradients by separate GEMMs; 1: dW_hh, 2: dW_hh and dW_ih inside the
+    persistent backward kernel (last backward in this process, any thread)."""
+    return load().hsl_last_backward_fused()
 
 
 TIMING_KINDS = {"rec_fwd": 1, "rec_bwd": 2, "scan_fwd": 3, "scan_bwd": 4, "input_proj": 5,

@@ -12,6 +12,7 @@ namespace hsl {
 namespace {
 thread_local char g_err[512] = "";
 thread_local int g_last_path = 0;
+std::atomic<int> g_last_fused{0};  // process-wide: autograd runs backward on its own thread
 std::atomic<int> g_path_mode{0};
 std::atomic<int> g_exchange_scope{0};
 std::atomic<long long> g_spin_us{2000000};
@@ -79,6 +80,7 @@ int recurrent_path_mode() { return g_path_mode.load(); }
 int exchange_scope_mode() { return g_exchange_scope.load(); }
 long long spin_timeout_ticks() { return g_spin_us.load() * 100; }  // 100 MHz clock
 void note_recurrent_path(int path) { g_last_path = path; }
+void note_backward_fused(int fused) { g_last_fused.store(fused); }
 
 }  // namespace hsl
 
@@ -99,6 +101,7 @@ long long hsl_set_spin_timeout_us(long long us) {
 }
 
 int hsl_last_recurrent_path(void) { return hsl::g_last_path; }
+int hsl_last_backward_fused(void) { return hsl::g_last_fused.load(); }
 
 int hsl_set_exchange_scope(int mode) { return hsl::g_exchange_scope.exchange(mode == 1 ? 1 : 0); }
 

@@ -42,6 +42,7 @@ int timing_begin(int kind, hipStream_t s);
 void timing_end(int slot, hipStream_t s);
 long long spin_timeout_ticks();   // in wall_clock64 ticks (100 MHz)
 void note_recurrent_path(int path);
+void note_backward_fused(int fused);  // 0, 1 (dW_hh) or 2 (dW_hh and dW_ih)
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 

@@ -1534,7 +1534,9 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     HSL_HIP(hipGetLastError());
     timing_end(slot, s);
     note_recurrent_path(2);
+    note_backward_fused(fused_ih ? 2 : fused ? 1 : 0);
   } else {
+    note_backward_fused(0);
     hipLaunchKernelGGL(scale_whh_kernel, dim3(grid_for((size_t)4 * H * H)), dim3(256), 0, s, w_hh, b_hh, a, w.w_s,
                        (float*)nullptr, (float*)nullptr, H);
     HSL_HIP(hipGetLastError());

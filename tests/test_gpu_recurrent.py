@@ -231,3 +231,11 @@ def test_null_states_equal_explicit_zeros(dev, mode):
             assert runs[1][k] is None, k
         else:
             assert torch.equal(v, runs[1][k]), k
+
+
+@pytest.mark.parametrize("shape,fused", [((12, 5, 16, 40), 2), ((12, 5, 300, 40), 1), ((130, 6, 32, 72), 2)])
+def test_fused_weight_gradients(dev, shape, fused):
+    """The persistent backward accumulates dW_hh (and dW_ih when D <= 256) itself; the
+    parity bar is the same as for the separate GEMMs.  (130 steps: two dW_hh planes.)"""
+    check(*shape, dev, 2, a=[0.4, 0.3, 0.2, 0.1])
+    assert prlstm_amd._lib.last_backward_fused() == fused

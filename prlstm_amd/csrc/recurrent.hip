@@ -44,6 +44,21 @@ __global__ void fill_u64_kernel(unsigned long long* p, size_t n, unsigned long l
     p[i] = v;
 }
 
+// Fills three word ranges in one launch (error flag, hand-off slots, placement words).
+__global__ void fill3_u64_kernel(unsigned long long* a, size_t na, unsigned long long va, unsigned long long* b,
+                                 size_t nb, unsigned long long vb, unsigned long long* c, size_t nc,
+                                 unsigned long long vc) {
+  const size_t n = na + nb + nc;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    if (i < na)
+      a[i] = va;
+    else if (i < na + nb)
+      b[i - na] = vb;
+    else
+      c[i - na - nb] = vc;
+  }
+}
+
 __global__ void copy_f32_kernel(float* dst, const float* src, size_t n) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
     dst[i] = src ? src[i] : 0.f;
@@ -1247,9 +1262,16 @@ int fill_words(unsigned long long* p, size_t n, unsigned long long v, hipStream_
   return HSL_OK;
 }
 
-// Hand-off slots start out empty (every 4-byte word kEmpty).
-int clear_slots(float* p, size_t floats, hipStream_t s) {
-  return fill_words(reinterpret_cast<unsigned long long*>(p), (floats + 1) / 2, kEmpty2, s);
+// Before a persistent launch: error flag cleared, hand-off slots empty (every 4-byte
+// word kEmpty), placement words cleared, in one launch.
+int prepare_persistent(int* err, float* slots, size_t slot_floats, unsigned long long* hello, size_t hwords,
+                       hipStream_t s) {
+  const size_t n1 = 32, n2 = (slot_floats + 1) / 2;
+  hipLaunchKernelGGL(fill3_u64_kernel, dim3(grid_for(n1 + n2 + hwords)), dim3(256), 0, s,
+                     reinterpret_cast<unsigned long long*>(err), n1, 0ull,
+                     reinterpret_cast<unsigned long long*>(slots), n2, kEmpty2, hello, hwords, 0ull);
+  HSL_HIP(hipGetLastError());
+  return HSL_OK;
 }
 
 int copy_f32_impl(float* dst, const float* src, size_t n, hipStream_t s) {
@@ -1405,7 +1427,10 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
   if (recurrent_path_mode() == 2 && !pl.ok)
     return fail(HSL_ERR_UNSUPPORTED, "persistent path does not fit (B=%d H=%d)", B, H);
 
-  HSL_CHECK(zero_words(reinterpret_cast<unsigned long long*>(w.err), 32, s));
+  if (pl.ok && T > 0)
+    HSL_CHECK(prepare_persistent(w.err, w.xbuf, w.xfloats, w.hello, w.hwords, s));
+  else
+    HSL_CHECK(zero_words(reinterpret_cast<unsigned long long*>(w.err), 32, s));
   if (T == 0) {
     HSL_CHECK(copy_f32(h_save, h0, (size_t)B * H, s));
     HSL_CHECK(copy_f32(c_save, c0, (size_t)B * H, s));
@@ -1418,8 +1443,6 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
   timing_end(tslot, s);
 
   if (pl.ok) {
-    HSL_CHECK(clear_slots(w.xbuf, w.xfloats, s));
-    HSL_CHECK(zero_words(w.hello, w.hwords, s));
     PFwdArgs pa{w.gih, w_hh, b_hh, a, h0, c0, h_save, c_save, gact, tanh_c, w.xbuf, w.hello, w.err,
                 T, B, H, pl.Hp, pl.NG, pl.NGX, pl.Bg, pl.NW, exchange_scope_mode(), spin_timeout_ticks()};
     const int slot = timing_begin(kTimeRecFwd, s);
@@ -1483,11 +1506,10 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
   BwdWs w;
   const size_t need = carve_bwd(ws, ws_bytes, T, B, D, H, &w);
   if (!ws || ws_bytes < need) return fail(HSL_ERR_ARG, "hsl_rec_bwd: workspace %zu bytes, need %zu", ws_bytes, need);
-  HSL_CHECK(zero_words(reinterpret_cast<unsigned long long*>(w.err), 32, s));
-
   const int TB = T * B;
   const size_t plane = (size_t)B * H, plane4 = (size_t)B * 4 * H;
   if (T == 0 || B == 0 || H == 0) {  // no time steps: all gradients are zero except the carries
+    HSL_CHECK(zero_words(reinterpret_cast<unsigned long long*>(w.err), 32, s));
     HSL_CHECK(copy_f32(dw_ih, nullptr, (size_t)4 * H * D, s));
     HSL_CHECK(copy_f32(dw_hh, nullptr, (size_t)4 * H * H, s));
     HSL_CHECK(copy_f32(db_ih, nullptr, (size_t)4 * H, s));
@@ -1516,9 +1538,11 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     nsplit = (T + wts - 1) / wts * pl.NG;
     wpx = reinterpret_cast<double*>(wph + (size_t)nsplit * 4 * H * H);
   }
+  if (pl.ok)
+    HSL_CHECK(prepare_persistent(w.err, w.pbuf, w.pfloats, w.hello, w.hwords, s));
+  else
+    HSL_CHECK(zero_words(reinterpret_cast<unsigned long long*>(w.err), 32, s));
   if (pl.ok) {
-    HSL_CHECK(clear_slots(w.pbuf, w.pfloats, s));
-    HSL_CHECK(zero_words(w.hello, w.hwords, s));
     PBwdArgs pa{dout, dh_n, dc_n, c_save, gact, tanh_c, w_hh, a, w.dgates, w.db_part, dh0, dc0, w.pbuf, w.hello,
                 w.err, T, B, H, pl.Hp, pl.NG, pl.NGX, pl.Bg, pl.NW, exchange_scope_mode(), spin_timeout_ticks(),
                 h_save, x, wph, fused_ih ? wpx : nullptr, D, wts,

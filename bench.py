@@ -220,8 +220,11 @@ def main():
 
     step_flops = 24.0 * T * B * H * (D + H)           # algorithmic fwd+bwd FLOPs
     rec_flops = 2.0 * T * B * H * 4 * H               # recurrent product of one direction
-    # per-launch FLOPs: the backward kernel also accumulates dW_hh (and dW_ih) when fused
-    kflops = {"rec_fwd": rec_flops, "step_fwd": rec_flops, "step_bwd": rec_flops,
+    # per-launch FLOPs: the backward kernel also accumulates dW_hh (and dW_ih) when fused,
+    # the forward kernel computes the input projection when no separate launch ran
+    proj_flops = 2.0 * T * B * 4 * H * D               # input projection, inside rec_fwd when fused
+    kflops = {"rec_fwd": rec_flops + (proj_flops if "input_proj" not in kern else 0.0),
+              "step_fwd": rec_flops, "step_bwd": rec_flops,
               "rec_bwd": rec_flops * (1 + (fused >= 1)) + (2.0 * T * B * 4 * H * D if fused == 2 else 0.0)}
     if "rec_fwd" in kern or "rec_bwd" in kern:
         name = max((k for k in ("rec_fwd", "rec_bwd") if k in kern), key=lambda k: kern[k])

@@ -465,7 +465,19 @@ struct PFwdArgs {
   int T, B, H, Hp, NG, NGX, Bg, NW;
   int device_scope;  // 1: never use the XCD-local stores
   long long spin;
+  // input-projection waves (launches with 512 threads; gih is then unused)
+  const float* x;     // [T][B][D]
+  const float* w_ih;  // [4H][D]
+  const float* b_ih;  // [4H]
+  int D;
 };
+
+// Input projection inside the forward: xin[block parity][t%8 * 4 + batch slot][WG row]
+// holds the four projection waves' partial sums (one per quarter of D) of
+// x_t[b] . W_ih[row] for the 8 steps of a block.
+constexpr int kXinSteps = 8;
+constexpr bool kXprojAfterPublish = true;  // projection products wait for the step's publish
+typedef f4 XinBuf[2][64][kXinSteps * 4 + 1];  // [parity][WG row][t%8 * 4 + slot], padded row
 
 // Forward.  Wave q multiplies the q-th quarter of k (KQ values).  h_{t-1} of a quarter
 // comes from NS = KQ/16 source workgroups (16 units each).  Lane l of wave q needs
@@ -487,9 +499,9 @@ struct PFwdArgs {
 // One wave per SIMD leaves no other wave to hide latency behind, so the step is written
 // for a short dependent chain: uniform bases with 32-bit lane offsets for every access,
 // the hand-off scope fixed at compile time (FAST: XCD-local), and 4 accumulator chains.
-template <int KQ, bool FAST>
+template <int KQ, bool FAST, bool XP>
 __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg, f4 (&red)[2][4][64],
-                                             int& abort_flag) {
+                                             XinBuf* xin, int* pdone, int& abort_flag) {
   constexpr int HP = 4 * KQ;
   constexpr int NS = KQ / kUnits;
   constexpr int GW = 4 * HP;  // words per group and slot
@@ -522,7 +534,10 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
   float c_reg = 0.f;
   if (c_ok) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) bs[g] = p.a[g] * p.b_hh[g * H + cu];
+    for (int g = 0; g < 4; ++g) {
+      bs[g] = p.a[g] * p.b_hh[g * H + cu];
+      if constexpr (XP) bs[g] = p.b_ih[g * H + cu] + bs[g];  // the projection's bias joins here
+    }
     const size_t b0 = (size_t)cb * H + cu;
     c_reg = p.c0 ? p.c0[b0] : 0.f;
     p.h_save[b0] = p.h0 ? p.h0[b0] : 0.f;
@@ -558,7 +573,7 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
   // The streamed activations use non-temporal accesses so that they do not push the
   // hand-off slots out of L2.
   float giA[4] = {0.f, 0.f, 0.f, 0.f}, giB[4] = {0.f, 0.f, 0.f, 0.f};
-  if (c_ok) {
+  if (!XP && c_ok) {
 #pragma unroll
     for (int gt = 0; gt < 4; ++gt) giA[gt] = gih_row[gt * H + cu];
   }
@@ -585,7 +600,7 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
       }
     }
     asm volatile("" : "+v"(gi[0]), "+v"(gi[1]), "+v"(gi[2]), "+v"(gi[3]));
-    if (c_ok && t + 1 < T) {
+    if (!XP && c_ok && t + 1 < T) {
       const float* g = gih_row + (size_t)(t + 1) * plane4;
 #pragma unroll
       for (int gt = 0; gt < 4; ++gt) gn[gt] = __builtin_nontemporal_load(byte_at(g, 4u * (gt * H + cu)));
@@ -607,6 +622,13 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
     if (c_ok) {
       const int uu = lane & 15;
       float act[4];
+      if constexpr (XP) {  // the projection waves' quarter sums of x_t . W_ih
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f4 px = (*xin)[(t / kXinSteps) & 1][g * kUnits + uu][(t % kXinSteps) * 4 + q];
+          gi[g] = (px[0] + px[1]) + (px[2] + px[3]);
+        }
+      }
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const f4 pr = red[t & 1][q][g * kUnits + uu];
@@ -626,6 +648,11 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
                                   reinterpret_cast<f4*>(byte_at(ga_row + (size_t)t * plane4, 16u * cu)));
       word_put<FAST>(xg + (size_t)((t + 2) & 3) * slot_words, woff, __uint_as_float(kEmpty));
     }
+    if constexpr (XP && kXprojAfterPublish) {  // the projection waves' products may start now
+      __builtin_amdgcn_sched_barrier(0);
+      *reinterpret_cast<volatile int*>(&pdone[q]) = t + 1;  // every lane writes the same value
+      __builtin_amdgcn_sched_barrier(0);
+    }
     return true;
   };
 
@@ -635,21 +662,148 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
   }
 }
 
+// Input-projection waves (waves 4-7 of a 512-thread forward workgroup): they compute
+// x_t W_ih^T for this workgroup's 64 gate rows and the group's four batch slots
+// (_torch.py:96, there one GEMM before the loop) while the recurrent waves run, so the
+// [T,B,4H] projection never goes through HBM.  Wave w takes the quarter k in
+// [64w, 64w+64) of D (D <= 256); the 8 steps of a block form the 32 columns of one
+// v_mfma_f32_32x32x2_f32 tile (column = t%8 * 4 + batch slot), rows = the 64 gate rows
+// (two tiles), W_ih's rows held in registers for the whole launch.  The two half-waves
+// take the two 32-wide halves of the quarter (A and B use the same k order).  Block m+1
+// is computed during the 8 steps of block m (8 products per step), written to xin at the
+// end of the block (parity m+1, read by the cells of block m+1 after the barrier of its
+// first step), and its x operands are loaded two blocks ahead.  Block 0 is computed
+// before the first step.  The waves take part in every workgroup barrier of the
+// recurrent waves (one per step) and leave when the group aborts, as they do.
 template <int KQ>
-__global__ __launch_bounds__(256, 1) void rec_fwd_persistent(PFwdArgs p) {
+__device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg, XinBuf* xin, int* pdone,
+                                              int& abort_flag) {
+  const int T = p.T, B = p.B, H = p.H, D = p.D, Bg = p.Bg;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) - 4);
+  const int half = lane >> 5, l32 = lane & 31;
+  const int kb = 64 * w + 32 * half;
+  float wa[2][32];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int r = rt * 32 + l32, u = wg * kUnits + (r & 15);
+    const bool ok = u < H;
+    const float* wrow = p.w_ih + (size_t)((r >> 4) * H + (ok ? u : 0)) * D;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int k = kb + i;
+      wa[rt][i] = (ok && k < D) ? wrow[k] : 0.f;
+    }
+  }
+  // column l32 = t%8 * 4 + batch slot; absent slots read batch 0 (their column is unused)
+  const int bsl = l32 & 3, tl = l32 >> 2, cb = grp * Bg + bsl;
+  const int cbr = (bsl < Bg && cb < B) ? cb : 0;
+  auto load_blk = [&](int m, float (&xo)[32]) {
+    const int t = m * kXinSteps + tl;
+    const float* row = p.x + ((size_t)(t < T ? t : T - 1) * B + cbr) * D;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int k4 = kb + 4 * j;
+      f4 v = f4{0.f, 0.f, 0.f, 0.f};
+      if (k4 < D) v = *reinterpret_cast<const f4*>(row + k4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xo[4 * j + e] = v[e];
+    }
+  };
+  f16v acc[2] = {f16v{}, f16v{}};
+  auto products = [&](const float (&xo)[32], int sub) {  // k-steps 4 sub .. 4 sub + 3
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+        acc[rt] = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[rt][4 * sub + i4], xo[4 * sub + i4], acc[rt], 0, 0, 0);
+  };
+  auto write_blk = [&](int m) {  // D layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column l%32
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = rt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        reinterpret_cast<float*>(&(*xin)[m & 1][row][l32])[w] = acc[rt][r];
+      }
+      acc[rt] = f16v{};
+    }
+  };
+
+  float xa[32], xb[32];  // x operands of even / odd blocks
+  load_blk(0, xa);
+  load_blk(1, xb);
+#pragma unroll
+  for (int sub = 0; sub < 8; ++sub) products(xa, sub);
+  write_blk(0);
+  load_blk(2, xa);
+  // window j: the 8 steps of block j, computing block j+1 from its operand set
+  auto window = [&](int j, float (&xu)[32]) __attribute__((always_inline)) -> bool {
+    const bool next = (j + 1) * kXinSteps < T;
+#pragma unroll
+    for (int sub = 0; sub < 8; ++sub) {
+      const int t = j * kXinSteps + sub;
+      if (t >= T) return false;
+      lds_barrier();  // the recurrent waves' barrier of this step
+      if (abort_flag) return false;
+      if (next) {
+        if constexpr (kXprojAfterPublish) {  // after the recurrent waves' publish of h_t
+          const long long t0 = wall_clock64();
+          while (true) {
+            const int m0 = reinterpret_cast<volatile int*>(pdone)[0], m1 = reinterpret_cast<volatile int*>(pdone)[1];
+            const int m2 = reinterpret_cast<volatile int*>(pdone)[2], m3 = reinterpret_cast<volatile int*>(pdone)[3];
+            if (min(min(m0, m1), min(m2, m3)) > t) break;
+            if (abort_flag) return false;
+            if (wall_clock64() - t0 > p.spin) {
+              abort_flag = 1;
+              atomicOr(p.err, 1);
+              return false;
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+        }
+        products(xu, sub);
+      }
+    }
+    if (next) {
+      write_blk(j + 1);
+      load_blk(j + 3, xu);
+    }
+    return true;
+  };
+  for (int j = 0;; j += 2) {
+    if (!window(j, xb)) break;
+    if (!window(j + 1, xa)) break;
+  }
+}
+
+// XP: 512 threads; waves 4-7 compute the input projection (rec_fwd_xproj), which then
+// is not read from gih.
+template <int KQ, bool XP>
+__global__ __launch_bounds__(XP ? 512 : 256, 1) void rec_fwd_persistent(PFwdArgs p) {
   constexpr int HP = 4 * KQ;
   __shared__ f4 red[2][4][64];  // [step parity][batch slot][gate row] -> 4 wave partials
   __shared__ int abort_flag;
+  __shared__ int pdone[4];  // steps whose h recurrent wave q has published
+  extern __shared__ char dyn_lds[];  // keeps one workgroup per CU; holds xin when XP
+  XinBuf* const xin = reinterpret_cast<XinBuf*>(dyn_lds);
   const int grp = blockIdx.x % p.NGX, wg = blockIdx.x / p.NGX;
   if (grp >= p.NG) return;  // unused XCD slot (groups are padded to a multiple of 8)
   if (threadIdx.x == 0) abort_flag = 0;
+  if (threadIdx.x < 4) pdone[threadIdx.x] = 0;
   const bool fast = agree_placement(p.hello + (size_t)grp * (HP / kUnits), wg, p.NW, p.spin, &abort_flag, p.err) &&
                     !p.device_scope;
   if (abort_flag) return;
+  if constexpr (XP) {
+    if (threadIdx.x >= 256) {
+      rec_fwd_xproj<KQ>(p, grp, wg, xin, pdone, abort_flag);
+      return;
+    }
+  }
   if (fast)
-    rec_fwd_body<KQ, true>(p, grp, wg, red, abort_flag);
+    rec_fwd_body<KQ, true, XP>(p, grp, wg, red, xin, pdone, abort_flag);
   else
-    rec_fwd_body<KQ, false>(p, grp, wg, red, abort_flag);
+    rec_fwd_body<KQ, false, XP>(p, grp, wg, red, xin, pdone, abort_flag);
 }
 
 // Per-step inputs of the persistent backward, loaded one step ahead: dout[t], c_{t-1}
@@ -1153,6 +1307,7 @@ struct PersistentPlan {
   bool ok = false;
   int KQ = 0, Hp = 0, NG = 0, NGX = 0, Bg = 0, NW = 0, grid = 0;
   int XT = -1;  // backward: -1 no weight-gradient waves, 0 dW_hh only, 2 dW_hh and dW_ih
+  bool XP = false;  // forward: input projection inside the kernel (512 threads)
 };
 
 int pick_kq(int H) {
@@ -1172,6 +1327,15 @@ int max_resident(K kernel, int threads, int* out) {
 }
 
 // Weight-gradient waves in the persistent backward: on unless HSL_FUSED_WGRAD=0.
+// Input projection inside the persistent forward: on unless HSL_FUSED_XPROJ=0.
+bool fused_xproj_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("HSL_FUSED_XPROJ");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 bool fused_wgrad_enabled() {
   static const bool on = [] {
     const char* e = getenv("HSL_FUSED_WGRAD");
@@ -1214,6 +1378,9 @@ int plan_persistent(int B, int H, int D, bool bwd, PersistentPlan* pl) {
   p.grid = p.NGX * p.NW;
   // dW_ih joins the weight-gradient waves when its 32-column tiles fit two per wave
   if (bwd && fused_wgrad_enabled()) p.XT = (D > 0 && D <= 256) ? 2 : 0;
+  // the forward's projection waves hold W_ih rows for a quarter of D <= 256 each and read
+  // x rows with 16-byte loads
+  if (!bwd && fused_xproj_enabled()) p.XP = D > 0 && D <= 256 && D % 4 == 0;
   int occ = 0;
   for (;;) {
     if (bwd) {
@@ -1224,17 +1391,19 @@ int plan_persistent(int B, int H, int D, bool bwd, PersistentPlan* pl) {
         default: HSL_CHECK(bwd_resident<128>(p.XT, &occ)); break;
       }
     } else {
+      const int th = p.XP ? 512 : 256;
       switch (kq) {
-        case 16: HSL_CHECK(max_resident(rec_fwd_persistent<16>, 256, &occ)); break;
-        case 32: HSL_CHECK(max_resident(rec_fwd_persistent<32>, 256, &occ)); break;
-        case 64: HSL_CHECK(max_resident(rec_fwd_persistent<64>, 256, &occ)); break;
-        default: HSL_CHECK(max_resident(rec_fwd_persistent<128>, 256, &occ)); break;
+        case 16: HSL_CHECK(p.XP ? max_resident(rec_fwd_persistent<16, true>, th, &occ) : max_resident(rec_fwd_persistent<16, false>, th, &occ)); break;
+        case 32: HSL_CHECK(p.XP ? max_resident(rec_fwd_persistent<32, true>, th, &occ) : max_resident(rec_fwd_persistent<32, false>, th, &occ)); break;
+        case 64: HSL_CHECK(p.XP ? max_resident(rec_fwd_persistent<64, true>, th, &occ) : max_resident(rec_fwd_persistent<64, false>, th, &occ)); break;
+        default: HSL_CHECK(p.XP ? max_resident(rec_fwd_persistent<128, true>, th, &occ) : max_resident(rec_fwd_persistent<128, false>, th, &occ)); break;
       }
     }
     // every workgroup must be resident at once: the waits are between workgroups
     p.ok = occ >= 1 && (long)occ * di.num_cus >= p.grid;
-    if (p.ok || p.XT < 0) break;
-    p.XT = -1;  // retry without the weight-gradient waves
+    if (p.ok || (p.XT < 0 && !p.XP)) break;
+    p.XT = -1;  // retry without the weight-gradient / projection waves
+    p.XP = false;
   }
   *pl = p;
   return HSL_OK;
@@ -1371,8 +1540,12 @@ int check_dims(int T, int B, int D, int H) {
 }
 
 template <int KQ>
-void launch_fwd_persistent(const PFwdArgs& a, int grid, hipStream_t s) {
-  hipLaunchKernelGGL(rec_fwd_persistent<KQ>, dim3(grid), dim3(256), kPadLdsBytes, s, a);
+void launch_fwd_persistent(const PFwdArgs& a, int grid, bool xp, hipStream_t s) {
+  static_assert(sizeof(XinBuf) <= (size_t)kPadLdsBytes, "xin lives in the padding LDS");
+  if (xp)
+    hipLaunchKernelGGL((rec_fwd_persistent<KQ, true>), dim3(grid), dim3(512), kPadLdsBytes, s, a);
+  else
+    hipLaunchKernelGGL((rec_fwd_persistent<KQ, false>), dim3(grid), dim3(256), kPadLdsBytes, s, a);
 }
 template <int KQ>
 void launch_bwd_persistent(const PBwdArgs& a, int grid, int xt, hipStream_t s) {
@@ -1436,21 +1609,25 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
     HSL_CHECK(copy_f32(c_save, c0, (size_t)B * H, s));
     return HSL_OK;
   }
-  // input projection for all T at once (_torch.py:96)
-  GemmDesc g1{x, w_ih, b_ih, w.gih, T * B, 4 * H, D, D, D, 4 * H, 0, 1};
-  const int tslot = timing_begin(kTimeInputProj, s);
-  HSL_CHECK(gemm_run(g1, nullptr, 0, s));
-  timing_end(tslot, s);
+  if (pl.XP && reinterpret_cast<uintptr_t>(x) % 16 != 0) pl.XP = false;  // 16-byte x loads
+  if (!(pl.ok && pl.XP)) {
+    // input projection for all T at once (_torch.py:96)
+    GemmDesc g1{x, w_ih, b_ih, w.gih, T * B, 4 * H, D, D, D, 4 * H, 0, 1};
+    const int tslot = timing_begin(kTimeInputProj, s);
+    HSL_CHECK(gemm_run(g1, nullptr, 0, s));
+    timing_end(tslot, s);
+  }
 
   if (pl.ok) {
     PFwdArgs pa{w.gih, w_hh, b_hh, a, h0, c0, h_save, c_save, gact, tanh_c, w.xbuf, w.hello, w.err,
-                T, B, H, pl.Hp, pl.NG, pl.NGX, pl.Bg, pl.NW, exchange_scope_mode(), spin_timeout_ticks()};
+                T, B, H, pl.Hp, pl.NG, pl.NGX, pl.Bg, pl.NW, exchange_scope_mode(), spin_timeout_ticks(),
+                x, w_ih, b_ih, D};
     const int slot = timing_begin(kTimeRecFwd, s);
     switch (pl.KQ) {
-      case 16: launch_fwd_persistent<16>(pa, pl.grid, s); break;
-      case 32: launch_fwd_persistent<32>(pa, pl.grid, s); break;
-      case 64: launch_fwd_persistent<64>(pa, pl.grid, s); break;
-      default: launch_fwd_persistent<128>(pa, pl.grid, s); break;
+      case 16: launch_fwd_persistent<16>(pa, pl.grid, pl.XP, s); break;
+      case 32: launch_fwd_persistent<32>(pa, pl.grid, pl.XP, s); break;
+      case 64: launch_fwd_persistent<64>(pa, pl.grid, pl.XP, s); break;
+      default: launch_fwd_persistent<128>(pa, pl.grid, pl.XP, s); break;
     }
     HSL_HIP(hipGetLastError());
     timing_end(slot, s);

@@ -83,15 +83,6 @@ __global__ void scale_whh_kernel(const float* __restrict__ w_hh, const float* __
   }
 }
 
-// out[e] = sum_z P[z][e] over fp64 planes, rounded once to fp32.
-__global__ void sum_planes_f64_kernel(const double* __restrict__ P, int planes, float* __restrict__ out, size_t n) {
-  for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < n; e += (size_t)gridDim.x * blockDim.x) {
-    double acc = 0.0;
-    for (int z = 0; z < planes; ++z) acc += P[(size_t)z * n + e];
-    out[e] = (float)acc;
-  }
-}
-
 // db_part[b][n] = sum_t dg[t][b][n] in fp64.
 __global__ void colsum_time_kernel(const float* __restrict__ dg, double* __restrict__ db_part, int T, int BN4) {
   for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < BN4; e += gridDim.x * blockDim.x) {
@@ -102,18 +93,33 @@ __global__ void colsum_time_kernel(const float* __restrict__ dg, double* __restr
 }
 
 // dW_hh_s = sum of split-K partials (fp64); dW_hh = a * dW_hh_s; rowdot[n] = sum_k W_hh[n][k] dW_hh_s[n][k].
+// Blocks past the 4H rows (when X is non-null) add the fp64 dW_ih planes X[xplanes][xn]
+// of the fused backward into dw_ih, in the same launch.
 __global__ __launch_bounds__(256) void whh_grad_finalize_kernel(const float* __restrict__ P, int splits,
                                                                 const float* __restrict__ w_hh,
                                                                 const float* __restrict__ a, float* __restrict__ dw_hh,
-                                                                double* __restrict__ rowdot, int H) {
+                                                                double* __restrict__ rowdot, int H,
+                                                                const double* __restrict__ X, int xplanes,
+                                                                float* __restrict__ dw_ih, size_t xn) {
   __shared__ double red[256];
   const int n = blockIdx.x;
+  if (n >= 4 * H) {
+    const size_t nb = gridDim.x - 4 * H;
+    for (size_t e = (size_t)(n - 4 * H) * blockDim.x + threadIdx.x; e < xn; e += nb * blockDim.x) {
+      double v = 0.0;
+#pragma unroll 4
+      for (int z = 0; z < xplanes; ++z) v += X[(size_t)z * xn + e];
+      dw_ih[e] = (float)v;
+    }
+    return;
+  }
   const size_t plane = (size_t)4 * H * H;
   const float ag = a[n / H];
   double acc = 0.0;
   for (int k = threadIdx.x; k < H; k += blockDim.x) {
     const size_t e = (size_t)n * H + k;
     double v = 0.0;
+#pragma unroll 4
     for (int z = 0; z < splits; ++z) v += (double)P[(size_t)z * plane + e];
     const float s = (float)v;
     dw_hh[e] = ag * s;
@@ -1776,16 +1782,15 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     GemmDesc g4{w.dgates, h_save, nullptr, w.gemm, 4 * H, H, TB, 4 * H, H, H, 1, 0, 1};
     HSL_CHECK(gemm_partials(g4, w.gemm, gemm_pick_splits(4 * H, H, TB, 1), s, &splits));
   }
-  hipLaunchKernelGGL(whh_grad_finalize_kernel, dim3(4 * H), dim3(256), 0, s, wph, splits, w_hh, a, dw_hh,
-                     w.rowdot, H);
-  HSL_HIP(hipGetLastError());
-  HSL_CHECK(bias_grads_from_parts(w.db_part, B, w.rowdot, b_hh, a, db_ih, db_hh, da, H, s));
-  // dW_ih = dg^T x ; dx = dg W_ih
-  if (fused_ih) {
-    const size_t n = (size_t)4 * H * D;
-    hipLaunchKernelGGL(sum_planes_f64_kernel, dim3(grid_for(n)), dim3(256), 0, s, wpx, pl.NG, dw_ih, n);
+  {  // dW_hh (and the fused dW_ih planes in extra blocks of the same launch)
+    const size_t xn = fused_ih ? (size_t)4 * H * D : 0;
+    const int xblocks = fused_ih ? grid_for(xn) : 0;
+    hipLaunchKernelGGL(whh_grad_finalize_kernel, dim3(4 * H + xblocks), dim3(256), 0, s, wph, splits, w_hh, a,
+                       dw_hh, w.rowdot, H, (const double*)wpx, pl.NG, dw_ih, xn);
     HSL_HIP(hipGetLastError());
   }
+  HSL_CHECK(bias_grads_from_parts(w.db_part, B, w.rowdot, b_hh, a, db_ih, db_hh, da, H, s));
+  // dW_ih = dg^T x ; dx = dg W_ih
   if (D > 0) {
     if (!fused_ih) {
       GemmDesc g5{w.dgates, x, nullptr, dw_ih, 4 * H, D, TB, 4 * H, D, D, 1, 0, 1};

@@ -478,6 +478,15 @@ struct PFwdArgs {
   int D;
 };
 
+// Per-wave step flags between the recurrent waves and the extra waves of a persistent
+// workgroup (forward: h published; backward: products issued).  Accessed through an
+// explicit LDS (address space 3) volatile pointer, so that the accesses are LDS
+// instructions: as generic volatile accesses they become flat ones, after which the
+// compiler waits for every outstanding global access of the wave.
+__shared__ int s_step_flag[4];
+typedef __attribute__((address_space(3))) volatile int lds_vint;
+__device__ __forceinline__ lds_vint* step_flags() { return (lds_vint*)(s_step_flag); }
+
 // Input projection inside the forward: xin[block parity][t%8 * 4 + batch slot][WG row]
 // holds the four projection waves' partial sums (one per quarter of D) of
 // x_t[b] . W_ih[row] for the 8 steps of a block.
@@ -507,7 +516,7 @@ typedef f4 XinBuf[2][64][kXinSteps * 4 + 1];  // [parity][WG row][t%8 * 4 + slot
 // the hand-off scope fixed at compile time (FAST: XCD-local), and 4 accumulator chains.
 template <int KQ, bool FAST, bool XP>
 __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg, f4 (&red)[2][4][64],
-                                             XinBuf* xin, int* pdone, int& abort_flag) {
+                                             XinBuf* xin, int& abort_flag) {
   constexpr int HP = 4 * KQ;
   constexpr int NS = KQ / kUnits;
   constexpr int GW = 4 * HP;  // words per group and slot
@@ -656,7 +665,7 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
     }
     if constexpr (XP && kXprojAfterPublish) {  // the projection waves' products may start now
       __builtin_amdgcn_sched_barrier(0);
-      *reinterpret_cast<volatile int*>(&pdone[q]) = t + 1;  // every lane writes the same value
+      step_flags()[q] = t + 1;  // every lane writes the same value
       __builtin_amdgcn_sched_barrier(0);
     }
     return true;
@@ -682,8 +691,7 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
 // before the first step.  The waves take part in every workgroup barrier of the
 // recurrent waves (one per step) and leave when the group aborts, as they do.
 template <int KQ>
-__device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg, XinBuf* xin, int* pdone,
-                                              int& abort_flag) {
+__device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg, XinBuf* xin, int& abort_flag) {
   const int T = p.T, B = p.B, H = p.H, D = p.D, Bg = p.Bg;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) - 4);
@@ -756,8 +764,8 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
         if constexpr (kXprojAfterPublish) {  // after the recurrent waves' publish of h_t
           const long long t0 = wall_clock64();
           while (true) {
-            const int m0 = reinterpret_cast<volatile int*>(pdone)[0], m1 = reinterpret_cast<volatile int*>(pdone)[1];
-            const int m2 = reinterpret_cast<volatile int*>(pdone)[2], m3 = reinterpret_cast<volatile int*>(pdone)[3];
+            lds_vint* const f = step_flags();
+            const int m0 = f[0], m1 = f[1], m2 = f[2], m3 = f[3];
             if (min(min(m0, m1), min(m2, m3)) > t) break;
             if (abort_flag) return false;
             if (wall_clock64() - t0 > p.spin) {
@@ -790,26 +798,25 @@ __global__ __launch_bounds__(XP ? 512 : 256, 1) void rec_fwd_persistent(PFwdArgs
   constexpr int HP = 4 * KQ;
   __shared__ f4 red[2][4][64];  // [step parity][batch slot][gate row] -> 4 wave partials
   __shared__ int abort_flag;
-  __shared__ int pdone[4];  // steps whose h recurrent wave q has published
   extern __shared__ char dyn_lds[];  // keeps one workgroup per CU; holds xin when XP
   XinBuf* const xin = reinterpret_cast<XinBuf*>(dyn_lds);
   const int grp = blockIdx.x % p.NGX, wg = blockIdx.x / p.NGX;
   if (grp >= p.NG) return;  // unused XCD slot (groups are padded to a multiple of 8)
   if (threadIdx.x == 0) abort_flag = 0;
-  if (threadIdx.x < 4) pdone[threadIdx.x] = 0;
+  if (threadIdx.x < 4) step_flags()[threadIdx.x] = 0;  // steps whose h wave q has published
   const bool fast = agree_placement(p.hello + (size_t)grp * (HP / kUnits), wg, p.NW, p.spin, &abort_flag, p.err) &&
                     !p.device_scope;
   if (abort_flag) return;
   if constexpr (XP) {
     if (threadIdx.x >= 256) {
-      rec_fwd_xproj<KQ>(p, grp, wg, xin, pdone, abort_flag);
+      rec_fwd_xproj<KQ>(p, grp, wg, xin, abort_flag);
       return;
     }
   }
   if (fast)
-    rec_fwd_body<KQ, true, XP>(p, grp, wg, red, xin, pdone, abort_flag);
+    rec_fwd_body<KQ, true, XP>(p, grp, wg, red, xin, abort_flag);
   else
-    rec_fwd_body<KQ, false, XP>(p, grp, wg, red, xin, pdone, abort_flag);
+    rec_fwd_body<KQ, false, XP>(p, grp, wg, red, xin, abort_flag);
 }
 
 // Per-step inputs of the persistent backward, loaded one step ahead: dout[t], c_{t-1}
@@ -865,7 +872,7 @@ struct PBwdArgs {
 // hand-off scope is a compile-time choice, keeping the per-step dependent chain short.
 template <int KQ, bool FAST, bool GW>
 __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg, float (&dgl)[2][4][68],
-                                             int* mdone, int& abort_flag) {
+                                             int& abort_flag) {
   constexpr int HP = 4 * KQ;
   constexpr int CG = (KQ + 63) / 64;     // 64-column groups per wave
   constexpr int NWMAX = HP / kUnits;     // workgroups per group at most
@@ -1034,7 +1041,7 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
         // the matrix pipe is free from here until the next step's products: tell the
         // weight-gradient wave on this SIMD (every lane writes the same value)
         __builtin_amdgcn_sched_barrier(0);
-        *reinterpret_cast<volatile int*>(&mdone[q]) = s + 1;
+        step_flags()[q] = s + 1;
         __builtin_amdgcn_sched_barrier(0);
       }
       const f4 part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
@@ -1069,7 +1076,7 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
 // barrier and the next), h_{t-1} and x_t rows are loaded one step ahead, and the
 // products are v_mfma_f32_32x32x2_f32 with the batch as the reduction index (two
 // instructions per 32x32 tile).  The products start only after the recurrent waves
-// have issued theirs (mdone), so they fill the idle part of the step.  Wave w owns the
+// have issued theirs (s_step_flag), so they fill the idle part of the step.  Wave w owns the
 // 32-column tiles w, w+4, ... of h (HT of them) and of x (XT).
 //
 // Accuracy: no fp32 running sum spans more than a few hundred products.  dW_hh_s is
@@ -1085,7 +1092,7 @@ constexpr int kXaccLdsBytes = 64 * 256 * 8;  // fp64 dW_ih accumulator for D <= 
 
 template <int KQ, int XT>
 __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg, float (&dgl)[2][4][68],
-                                              int* mdone, double* xacc, int& abort_flag) {
+                                              double* xacc, int& abort_flag) {
   constexpr int HT = KQ >= 32 ? KQ / 32 : 1;  // h column tiles per wave (4*KQ >= H)
   constexpr int XA = XT > 0 ? XT : 1;
   const int T = p.T, B = p.B, H = p.H, D = p.D, Bg = p.Bg, NG = p.NG, TS = p.TS;
@@ -1218,8 +1225,8 @@ __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg
     // every other wait of the persistent kernels)
     const long long t0 = wall_clock64();
     while (true) {
-      const int m0 = reinterpret_cast<volatile int*>(mdone)[0], m1 = reinterpret_cast<volatile int*>(mdone)[1];
-      const int m2 = reinterpret_cast<volatile int*>(mdone)[2], m3 = reinterpret_cast<volatile int*>(mdone)[3];
+      lds_vint* const f = step_flags();
+      const int m0 = f[0], m1 = f[1], m2 = f[2], m3 = f[3];
       if (min(min(m0, m1), min(m2, m3)) > s) break;
       if (abort_flag) return false;
       if (wall_clock64() - t0 > p.spin) {
@@ -1284,26 +1291,25 @@ __global__ __launch_bounds__(XT >= 0 ? 512 : 256, 1) void rec_bwd_persistent(PBw
   constexpr bool GW = XT >= 0;
   __shared__ float dgl[2][4][64 + 4];  // [step parity][batch slot][gate row]
   __shared__ int abort_flag;
-  __shared__ int mdone[4];  // steps whose products recurrent wave q has issued
   const int grp = blockIdx.x % p.NGX, wg = blockIdx.x / p.NGX;
   if (grp >= p.NG) return;
   if (threadIdx.x == 0) abort_flag = 0;
-  if (threadIdx.x < 4) mdone[threadIdx.x] = 0;
+  if (threadIdx.x < 4) step_flags()[threadIdx.x] = 0;  // steps whose products wave q has issued
   const bool fast = agree_placement(p.hello + (size_t)grp * NWMAX, wg, p.NW, p.spin, &abort_flag, p.err) &&
                     !p.device_scope;
   if (abort_flag) return;
   if constexpr (GW) {
     if (threadIdx.x >= 256) {
       extern __shared__ double xacc[];  // [64][256] fp64 dW_ih accumulator (dynamic LDS)
-      rec_bwd_wgrad<KQ, (XT > 0 ? XT : 0)>(p, grp, wg, dgl, mdone, xacc, abort_flag);
+      rec_bwd_wgrad<KQ, (XT > 0 ? XT : 0)>(p, grp, wg, dgl, xacc, abort_flag);
       return;
     }
     __builtin_amdgcn_s_setprio(2);  // the recurrent chain first when both waves can issue
   }
   if (fast)
-    rec_bwd_body<KQ, true, GW>(p, grp, wg, dgl, mdone, abort_flag);
+    rec_bwd_body<KQ, true, GW>(p, grp, wg, dgl, abort_flag);
   else
-    rec_bwd_body<KQ, false, GW>(p, grp, wg, dgl, mdone, abort_flag);
+    rec_bwd_body<KQ, false, GW>(p, grp, wg, dgl, abort_flag);
 }
 
 // ---------------------------------------------------------------------------------

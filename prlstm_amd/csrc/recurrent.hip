@@ -487,12 +487,12 @@ __shared__ int s_step_flag[4];
 typedef __attribute__((address_space(3))) volatile int lds_vint;
 __device__ __forceinline__ lds_vint* step_flags() { return (lds_vint*)(s_step_flag); }
 
-// Input projection inside the forward: xin[block parity][t%8 * 4 + batch slot][WG row]
-// holds the four projection waves' partial sums (one per quarter of D) of
-// x_t[b] . W_ih[row] for the 8 steps of a block.
+// Input projection inside the forward: xin[block parity][w][WG row][t%8 * 4 + batch slot]
+// holds projection wave w's partial sum (over the w-th quarter of D) of x_t[b] . W_ih[row]
+// for the 8 steps of a block.  Rows are padded to 36 floats.
 constexpr int kXinSteps = 8;
 constexpr bool kXprojAfterPublish = true;  // projection products wait for the step's publish
-typedef f4 XinBuf[2][64][kXinSteps * 4 + 1];  // [parity][WG row][t%8 * 4 + slot], padded row
+typedef float XinBuf[2][4][64][kXinSteps * 4 + 4];
 
 // Forward.  Wave q multiplies the q-th quarter of k (KQ values).  h_{t-1} of a quarter
 // comes from NS = KQ/16 source workgroups (16 units each).  Lane l of wave q needs
@@ -596,6 +596,11 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
   // One step; gi holds this step's projection row, gn receives the next one.  Returns
   // false when the group aborted.
   auto step = [&](int t, float (&gi)[4], float (&gn)[4]) __attribute__((always_inline)) -> bool {
+    // XP: projection wave q's partials of this step (lane = gate row, element = batch
+    // slot) seed the accumulator of wave q, so the workgroup sum below includes x_t W_ih^T
+    f4 xp = f4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (XP)
+      xp = *reinterpret_cast<const f4*>(&(*xin)[(t / kXinSteps) & 1][q][lane][(t % kXinSteps) * 4]);
     float hv[NS];
     if (t == 0) {
 #pragma unroll
@@ -621,8 +626,9 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
       for (int gt = 0; gt < 4; ++gt) gn[gt] = __builtin_nontemporal_load(byte_at(g, 4u * (gt * H + cu)));
     }
     f4 acc[4];
+    acc[0] = xp;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 1; c < 4; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NS; ++j)
 #pragma unroll
@@ -637,18 +643,14 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
     if (c_ok) {
       const int uu = lane & 15;
       float act[4];
-      if constexpr (XP) {  // the projection waves' quarter sums of x_t . W_ih
+      f4 pr[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f4 px = (*xin)[(t / kXinSteps) & 1][g * kUnits + uu][(t % kXinSteps) * 4 + q];
-          gi[g] = (px[0] + px[1]) + (px[2] + px[3]);
-        }
-      }
+      for (int g = 0; g < 4; ++g) pr[g] = red[t & 1][q][g * kUnits + uu];
+      asm volatile("" : "+v"(pr[0]), "+v"(pr[1]), "+v"(pr[2]), "+v"(pr[3]));  // four reads in flight
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const f4 pr = red[t & 1][q][g * kUnits + uu];
-        const float mm = (pr[0] + pr[1]) + (pr[2] + pr[3]);
-        act[g] = sigmoid_f((gi[g] + mm) + bs[g]);
+        const float mm = (pr[g][0] + pr[g][1]) + (pr[g][2] + pr[g][3]);
+        act[g] = sigmoid_f((XP ? mm : gi[g] + mm) + bs[g]);
       }
       const float c = act[1] * c_reg + act[0] * act[2];
       const float tc = tanh_f(c);
@@ -671,6 +673,7 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
     return true;
   };
 
+  if constexpr (XP) lds_barrier();  // block 0 of xin is written
   for (int t = 0; t < T; t += 2) {
     if (!step(t, giA, giB)) return;
     if (t + 1 < T && !step(t + 1, giB, giA)) return;
@@ -685,11 +688,13 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
 // v_mfma_f32_32x32x2_f32 tile (column = t%8 * 4 + batch slot), rows = the 64 gate rows
 // (two tiles), W_ih's rows held in registers for the whole launch.  The two half-waves
 // take the two 32-wide halves of the quarter (A and B use the same k order).  Block m+1
-// is computed during the 8 steps of block m (8 products per step), written to xin at the
-// end of the block (parity m+1, read by the cells of block m+1 after the barrier of its
-// first step), and its x operands are loaded two blocks ahead.  Block 0 is computed
-// before the first step.  The waves take part in every workgroup barrier of the
-// recurrent waves (one per step) and leave when the group aborts, as they do.
+// is computed during the first 7 steps of block m (the 64 products spread over them) and
+// written to xin before the barrier of step 8m+7 (parity m+1; recurrent wave w reads its
+// plane at the start of each step of block m+1, before that step's barrier, and the
+// last reads of block m-1, which the write replaces, came before the barrier of step
+// 8m-1).  Its x operands are loaded two blocks ahead.  Block 0 is computed and written
+// before one extra barrier ahead of the first step.  The waves take part in every
+// workgroup barrier of the recurrent waves and leave when the group aborts, as they do.
 template <int KQ>
 __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg, XinBuf* xin, int& abort_flag) {
   const int T = p.T, B = p.B, H = p.H, D = p.D, Bg = p.Bg;
@@ -725,12 +730,12 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
     }
   };
   f16v acc[2] = {f16v{}, f16v{}};
-  auto products = [&](const float (&xo)[32], int sub) {  // k-steps 4 sub .. 4 sub + 3
+  auto products = [&](const float (&xo)[32], int i0, int i1) {  // k-steps i0 .. i1-1
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4)
+    for (int i = i0; i < i1; ++i)
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
-        acc[rt] = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[rt][4 * sub + i4], xo[4 * sub + i4], acc[rt], 0, 0, 0);
+        acc[rt] = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[rt][i], xo[i], acc[rt], 0, 0, 0);
   };
   auto write_blk = [&](int m) {  // D layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column l%32
 #pragma unroll
@@ -738,7 +743,7 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = rt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        reinterpret_cast<float*>(&(*xin)[m & 1][row][l32])[w] = acc[rt][r];
+        (*xin)[m & 1][w][row][l32] = acc[rt][r];
       }
       acc[rt] = f16v{};
     }
@@ -747,11 +752,12 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
   float xa[32], xb[32];  // x operands of even / odd blocks
   load_blk(0, xa);
   load_blk(1, xb);
-#pragma unroll
-  for (int sub = 0; sub < 8; ++sub) products(xa, sub);
+  products(xa, 0, 32);
   write_blk(0);
   load_blk(2, xa);
-  // window j: the 8 steps of block j, computing block j+1 from its operand set
+  lds_barrier();  // the recurrent waves' barrier ahead of their first step
+  // window j: the 8 steps of block j, computing block j+1 from its operand set in steps
+  // 0-6 (k-steps 32 sub / 7 .. 32 (sub+1) / 7 in step sub)
   auto window = [&](int j, float (&xu)[32]) __attribute__((always_inline)) -> bool {
     const bool next = (j + 1) * kXinSteps < T;
 #pragma unroll
@@ -760,7 +766,7 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
       if (t >= T) return false;
       lds_barrier();  // the recurrent waves' barrier of this step
       if (abort_flag) return false;
-      if (next) {
+      if (next && sub < 7) {
         if constexpr (kXprojAfterPublish) {  // after the recurrent waves' publish of h_t
           const long long t0 = wall_clock64();
           while (true) {
@@ -776,12 +782,12 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
             __builtin_amdgcn_s_sleep(1);
           }
         }
-        products(xu, sub);
+        products(xu, 32 * sub / 7, 32 * (sub + 1) / 7);
+        if (sub == 6) {
+          write_blk(j + 1);
+          load_blk(j + 3, xu);
+        }
       }
-    }
-    if (next) {
-      write_blk(j + 1);
-      load_blk(j + 3, xu);
     }
     return true;
   };

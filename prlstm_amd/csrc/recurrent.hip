@@ -29,7 +29,8 @@
 
 namespace hsl {
 
-using CfgStep = GemmCfg<32, 32, 32, 1, 1, 4>;
+// Per-step products: 32x32 tiles, four waves splitting each 128-deep k-slice.
+using CfgStep = GemmCfg<32, 32, 128, 1, 1, 4>;
 
 namespace {
 
@@ -253,6 +254,60 @@ struct EpiCellBwd {
     }
   }
 };
+
+// Split-K form of the per-step cells: the step GEMM writes S fp32 partial planes
+// P[S][B][N] (EpiPartial) and one thread per (b, u) adds them in plane order and runs
+// the cell.  Used when the output has too few 32x32 tiles to fill the chip (the
+// backward product dg W_s has only B x H outputs for a 4H-long reduction).
+__global__ __launch_bounds__(256) void step_cell_fwd_kernel(const float* __restrict__ P, int S,
+                                                           const float* __restrict__ gih, const float* __restrict__ bs,
+                                                           const float* __restrict__ c_prev, float* __restrict__ h_out,
+                                                           float* __restrict__ c_out, float* __restrict__ gact,
+                                                           float* __restrict__ tanh_c, int B, int H) {
+  const size_t n = (size_t)B * H, plane = (size_t)B * 4 * H;
+  for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < n; e += (size_t)gridDim.x * blockDim.x) {
+    const int b = (int)(e / H), u = (int)(e % H);
+    const size_t col = (size_t)b * 4 * H + 4 * u;  // unit-interleaved columns 4u+g
+    f4 z = *reinterpret_cast<const f4*>(P + col);
+    for (int sp = 1; sp < S; ++sp) z += *reinterpret_cast<const f4*>(P + sp * plane + col);
+    float act[4];
+#pragma unroll
+    for (int gt = 0; gt < 4; ++gt) {
+      const int nn = gt * H + u;
+      act[gt] = sigmoid_f((gih[(size_t)b * 4 * H + nn] + z[gt]) + bs[nn]);
+    }
+    *reinterpret_cast<f4*>(gact + e * 4) = f4{act[0], act[1], act[2], act[3]};
+    const float c = act[1] * c_prev[e] + act[0] * act[2];
+    const float tc = tanh_f(c);
+    h_out[e] = act[3] * tc;
+    c_out[e] = c;
+    tanh_c[e] = tc;
+  }
+}
+
+__global__ __launch_bounds__(256) void step_cell_bwd_kernel(const float* __restrict__ P, int S,
+                                                           const float* __restrict__ dh_extra,
+                                                           const float* __restrict__ dout,
+                                                           const float* __restrict__ c_prev,
+                                                           const float* __restrict__ gact,
+                                                           const float* __restrict__ tanh_c, float* __restrict__ dc,
+                                                           float* __restrict__ dg, int B, int H) {
+  const size_t n = (size_t)B * H;
+  for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < n; e += (size_t)gridDim.x * blockDim.x) {
+    const int b = (int)(e / H), u = (int)(e % H);
+    float dh = 0.f;
+    for (int sp = 0; sp < S; ++sp) dh += P[sp * n + e];
+    if (dh_extra) dh = dh + dh_extra[e];
+    dh = dh + dout[e];
+    const f4 ga = *reinterpret_cast<const f4*>(gact + e * 4);
+    float dcv = dc[e];
+    float d[4];
+    cell_bwd(dh, dcv, c_prev[e], ga[0], ga[1], ga[2], ga[3], tanh_c[e], d);
+    dc[e] = dcv;
+#pragma unroll
+    for (int gt = 0; gt < 4; ++gt) dg[(size_t)b * 4 * H + gt * H + u] = d[gt];
+  }
+}
 
 // ---------------------------------------------------------------------------------
 // persistent path
@@ -1442,6 +1497,22 @@ inline int grid_for(size_t n) {
   return (int)b;
 }
 
+// k-splits of a per-step product with an M x N output (32x32 tiles) and depth K: enough
+// workgroups to cover the chip twice, at least two 128-deep slices per split.  Returns
+// the number of planes the launch really writes (1 = fused epilogue, no partials).
+int step_splits(int M, int N, int K, int* k_per_split) {
+  const int tiles = ((M + 31) / 32) * ((N + 31) / 32);
+  int s = 1;
+  if (tiles < 256 && K >= 512) {
+    s = (512 + tiles - 1) / tiles;
+    const int max_by_k = K / 256;
+    if (s > max_by_k) s = max_by_k;
+    if (s > 16) s = 16;
+    if (s < 1) s = 1;
+  }
+  return split_layout<CfgStep>(K, s, k_per_split);
+}
+
 int fill_words(unsigned long long* p, size_t n, unsigned long long v, hipStream_t s) {
   if (n == 0) return HSL_OK;
   hipLaunchKernelGGL(fill_u64_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, n, v);
@@ -1478,6 +1549,7 @@ struct FwdWs {
   size_t hwords;
   float* w_perm;              // [4H*H]      (per-step)
   float* bs;                  // [4H]        (per-step)
+  float* part;                // [S*B*4H]    (per-step split-K planes)
 };
 
 size_t carve_fwd(void* ws, size_t cap, int T, int B, int H, FwdWs* o) {
@@ -1492,6 +1564,9 @@ size_t carve_fwd(void* ws, size_t cap, int T, int B, int H, FwdWs* o) {
   o->hello = c.take<unsigned long long>(o->hwords);
   o->w_perm = c.take<float>((size_t)4 * H * H);
   o->bs = c.take<float>((size_t)4 * H);
+  int kps;
+  const int sp = step_splits(B, 4 * H, H, &kps);
+  o->part = c.take<float>(sp > 1 ? (size_t)sp * B * 4 * H : 0);
   return c.off;
 }
 
@@ -1502,6 +1577,7 @@ struct BwdWs {
   double* rowdot;            // [4H]
   float* dc;                 // [B*H]   (per-step)
   float* w_s;                // [4H*H]  (per-step)
+  float* part;               // [S*B*H] (per-step split-K planes)
   float* pbuf;                // [3*NG*NWMAX*4*64*PER] (persistent)
   size_t pfloats;
   unsigned long long* hello;  // [NG*NWMAX]           (persistent)
@@ -1537,6 +1613,9 @@ size_t carve_bwd(void* ws, size_t cap, int T, int B, int D, int H, BwdWs* o) {
   o->rowdot = c.take<double>((size_t)4 * H);
   o->dc = c.take<float>((size_t)B * H);
   o->w_s = c.take<float>((size_t)4 * H * H);
+  int kps;
+  const int sp = step_splits(B, H, 4 * H, &kps);
+  o->part = c.take<float>(sp > 1 ? (size_t)sp * B * H : 0);
   const int kq = pick_kq(H);
   const size_t ng = (size_t)(B + 3) / 4;
   const size_t nwmax = kq ? (size_t)(4 * kq / kUnits) : 0;
@@ -1660,6 +1739,8 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
   HSL_CHECK(copy_f32(h_save, h0, (size_t)B * H, s));
   HSL_CHECK(copy_f32(c_save, c0, (size_t)B * H, s));
   const size_t plane = (size_t)B * H, plane4 = (size_t)B * 4 * H;
+  int kps;
+  const int nsp = step_splits(B, 4 * H, H, &kps);
   const int slot = timing_begin(kTimeStepFwd, s);
   for (int t = 0; t < T; ++t) {
     GemmArgs ga{};
@@ -1672,9 +1753,18 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
     ga.ldb = H;
     ga.vec_a = aligned16(ga.A) && H % 4 == 0;
     ga.vec_b = aligned16(ga.B) && H % 4 == 0;
-    EpiCellFwd epi{w.gih + t * plane4, w.bs, c_save + t * plane, h_save + (t + 1) * plane, c_save + (t + 1) * plane,
-                   gact + t * plane4, tanh_c + t * plane, B, H};
-    HSL_CHECK((launch_gemm<CfgStep, false, true>(ga, 1, epi, s)));
+    if (nsp == 1) {
+      EpiCellFwd epi{w.gih + t * plane4, w.bs, c_save + t * plane, h_save + (t + 1) * plane,
+                     c_save + (t + 1) * plane, gact + t * plane4, tanh_c + t * plane, B, H};
+      HSL_CHECK((launch_gemm<CfgStep, false, true>(ga, 1, epi, s)));
+    } else {
+      EpiPartial epi{w.part, B, 4 * H};
+      HSL_CHECK((launch_gemm<CfgStep, false, true>(ga, nsp, epi, s)));
+      hipLaunchKernelGGL(step_cell_fwd_kernel, dim3(grid_for(plane)), dim3(256), 0, s, w.part, nsp,
+                         w.gih + t * plane4, w.bs, c_save + t * plane, h_save + (t + 1) * plane,
+                         c_save + (t + 1) * plane, gact + t * plane4, tanh_c + t * plane, B, H);
+      HSL_HIP(hipGetLastError());
+    }
   }
   timing_end(slot, s);
   note_recurrent_path(1);
@@ -1760,6 +1850,8 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
                        (float*)nullptr, (float*)nullptr, H);
     HSL_HIP(hipGetLastError());
     HSL_CHECK(copy_f32(w.dc, dc_n, plane, s));
+    int kps;
+    const int nsp = step_splits(B, H, 4 * H, &kps);
     const int slot = timing_begin(kTimeStepBwd, s);
     for (int t = T - 1; t >= 0; --t) {
       GemmArgs ga{};
@@ -1772,9 +1864,21 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
       ga.ldb = H;
       ga.vec_a = aligned16(ga.A);
       ga.vec_b = aligned16(ga.B) && H % 4 == 0;
-      EpiCellBwd epi{dout + t * plane, t == T - 1 ? dh_n : nullptr, c_save + t * plane, gact + t * plane4,
-                     tanh_c + t * plane, w.dc, w.dgates + t * plane4, B, H};
-      HSL_CHECK((launch_gemm<CfgStep, false, false>(ga, 1, epi, s)));
+      if (nsp == 1) {
+        EpiCellBwd epi{dout + t * plane, t == T - 1 ? dh_n : nullptr, c_save + t * plane, gact + t * plane4,
+                       tanh_c + t * plane, w.dc, w.dgates + t * plane4, B, H};
+        HSL_CHECK((launch_gemm<CfgStep, false, false>(ga, 1, epi, s)));
+      } else {
+        // the last step has no dgates_{t+1}: no product, zero planes summed
+        if (ga.K > 0) {
+          EpiPartial epi{w.part, B, H};
+          HSL_CHECK((launch_gemm<CfgStep, false, false>(ga, nsp, epi, s)));
+        }
+        hipLaunchKernelGGL(step_cell_bwd_kernel, dim3(grid_for(plane)), dim3(256), 0, s, w.part,
+                           ga.K > 0 ? nsp : 0, t == T - 1 ? dh_n : nullptr, dout + t * plane, c_save + t * plane,
+                           gact + t * plane4, tanh_c + t * plane, w.dc, w.dgates + t * plane4, B, H);
+        HSL_HIP(hipGetLastError());
+      }
     }
     timing_end(slot, s);
     if (dh0) {

@@ -155,6 +155,12 @@ def test_config2_nonlinear_a(dev):
     check(256, 32, 256, 512, dev, 2, a=a.tolist())
 
 
+def test_per_step_split_products(dev):
+    """Per-step path with split-K products in both directions (64 output tiles of the
+    forward product, 16 of the backward one), nonlinear a and initial states."""
+    check(10, 8, 64, 512, dev, 1, a=[0.4, 0.1, 0.3, 0.2], with_hx=True)
+
+
 def test_config3_large_hidden(dev):
     """T64 B32 D1024 H2048 (per-step path: W_hh does not fit on chip)."""
     check(64, 32, 1024, 2048, dev, 1)

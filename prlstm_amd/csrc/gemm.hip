@@ -1,17 +1,23 @@
 // hsl_gemm_f32: fp32 MFMA GEMM entry point with optional split-K.
 //
+// Products with M, N >= 64 run on the third core (gemm3_core.h): 128x256, 128x128 or
+// 128x64 tiles, whichever is the largest that still gives two workgroups per CU, and
+// 128x64 tiles with fp64 folding for the long weight-gradient reductions.  Thinner
+// products (one side below 64, e.g. the [B,H] carries) use the first core's 32x32 tile.
+//
 // Split-K writes fp32 partial tiles [splits][M][N] and a second kernel adds them in
 // fp64 (plus the bias), so long reductions (K = T*B up to 65536 for the weight
 // gradients) lose less accuracy than one fp32 running sum.
-#include "gemm2_core.h"
+#include "gemm3_core.h"
 
 namespace hsl {
 
-using CfgBig = GemmCfg<128, 128, 32, 2, 2, 1>;
-using CfgMid = GemmCfg<64, 64, 32, 2, 2, 1>;
 using CfgSmall = GemmCfg<32, 32, 32, 1, 1, 4>;
-// fp64-accumulating products with both sides >= 64 use the double-buffered core.
-using Cfg2Acc = Gemm2Cfg<64, 64, 32, true>;
+using Cfg3Wide = Gemm3Cfg<128, 256, 32, false>;
+using Cfg3Sq = Gemm3Cfg<128, 128, 32, false>;
+using Cfg3Narrow = Gemm3Cfg<128, 64, 32, false>;
+// fp64-accumulating products: fp32 MFMA partials of 4 slices (128 k) folded into fp64
+using Cfg3Acc = Gemm3Cfg<128, 64, 32, true, 4>;
 
 namespace {
 
@@ -29,69 +35,70 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
-enum class Tile { Big, Mid, Small };
+enum class Tile { Wide, Sq, Narrow, Acc, Small };
 
-Tile pick_tile(int M, int N, int acc64 = 0) {
-  const long big_tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
-  if (!acc64 && M >= 128 && N >= 128 && big_tiles >= 128) return Tile::Big;
-  const long mid_tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
-  if (M >= 64 && N >= 64 && mid_tiles >= 32) return Tile::Mid;
-  return Tile::Small;
+// Workgroups the chip runs at once with two per CU.
+constexpr long kFill = 512;
+
+long tiles_of(int M, int N, int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+
+Tile pick_tile(int M, int N, int acc64) {
+  if (M < 64 || N < 64) return Tile::Small;
+  if (acc64) return Tile::Acc;
+  if (tiles_of(M, N, 128, 256) >= kFill) return Tile::Wide;
+  if (tiles_of(M, N, 128, 128) >= kFill) return Tile::Sq;
+  return Tile::Narrow;
 }
 
-int tile_count(Tile t, int M, int N) {
-  const int b = t == Tile::Big ? 128 : t == Tile::Mid ? 64 : 32;
-  return ((M + b - 1) / b) * ((N + b - 1) / b);
-}
-
-template <class Cfg, class Epi, bool ACC64>
-int dispatch_trans(const GemmArgs& g, int ta, int tb, int splits, const Epi& epi, hipStream_t s) {
-  if (!ta && !tb) return launch_gemm<Cfg, false, false, Epi, ACC64>(g, splits, epi, s);
-  if (!ta && tb) return launch_gemm<Cfg, false, true, Epi, ACC64>(g, splits, epi, s);
-  if (ta && !tb) return launch_gemm<Cfg, true, false, Epi, ACC64>(g, splits, epi, s);
-  return launch_gemm<Cfg, true, true, Epi, ACC64>(g, splits, epi, s);
-}
-
-// fp64-accumulating products use the 64x64 (or 32x32) tiles: the fp64 registers of
-// the 128x128 tile would not fit next to its fp32 accumulators.
-template <class Epi>
-int dispatch(Tile t, const GemmArgs& g, int ta, int tb, int splits, const Epi& epi, hipStream_t s, int acc64) {
-  if (acc64) {
-    if (t == Tile::Small) return dispatch_trans<CfgSmall, Epi, true>(g, ta, tb, splits, epi, s);
-    return dispatch_trans<CfgMid, Epi, true>(g, ta, tb, splits, epi, s);
-  }
+long tile_count(Tile t, int M, int N) {
   switch (t) {
-    case Tile::Big: return dispatch_trans<CfgBig, Epi, false>(g, ta, tb, splits, epi, s);
-    case Tile::Mid: return dispatch_trans<CfgMid, Epi, false>(g, ta, tb, splits, epi, s);
-    default: return dispatch_trans<CfgSmall, Epi, false>(g, ta, tb, splits, epi, s);
+    case Tile::Wide: return tiles_of(M, N, 128, 256);
+    case Tile::Sq: return tiles_of(M, N, 128, 128);
+    case Tile::Narrow:
+    case Tile::Acc: return tiles_of(M, N, 128, 64);
+    default: return tiles_of(M, N, 32, 32);
   }
 }
 
-bool use_v2(const GemmDesc& d) { return d.acc64 && d.M >= 64 && d.N >= 64; }
-
-int dispatch_v2(const GemmDesc& d, float* partial, int splits, hipStream_t s, int* used) {
-  const int vec_a = aligned16(d.A) && d.lda % 4 == 0, vec_b = aligned16(d.B) && d.ldb % 4 == 0;
+template <class Cfg>
+int run3(const GemmDesc& d, float* partial, int splits, hipStream_t s, int* used) {
+  const int vec = aligned16(d.A) && aligned16(d.B) && d.lda % 4 == 0 && d.ldb % 4 == 0;
+  const float* bias = partial ? nullptr : d.bias;
   if (!d.trans_a && !d.trans_b)
-    return launch_gemm2<Cfg2Acc, false, false>(d.A, d.B, d.bias, d.C, partial, d.M, d.N, d.K, d.lda, d.ldb, d.ldc,
-                                               splits, vec_a, vec_b, s, used);
+    return launch_gemm3<Cfg, false, false>(d.A, d.B, bias, d.C, partial, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, splits,
+                                           vec, s, used);
   if (!d.trans_a && d.trans_b)
-    return launch_gemm2<Cfg2Acc, false, true>(d.A, d.B, d.bias, d.C, partial, d.M, d.N, d.K, d.lda, d.ldb, d.ldc,
-                                              splits, vec_a, vec_b, s, used);
+    return launch_gemm3<Cfg, false, true>(d.A, d.B, bias, d.C, partial, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, splits,
+                                          vec, s, used);
   if (d.trans_a && !d.trans_b)
-    return launch_gemm2<Cfg2Acc, true, false>(d.A, d.B, d.bias, d.C, partial, d.M, d.N, d.K, d.lda, d.ldb, d.ldc,
-                                              splits, vec_a, vec_b, s, used);
-  return launch_gemm2<Cfg2Acc, true, true>(d.A, d.B, d.bias, d.C, partial, d.M, d.N, d.K, d.lda, d.ldb, d.ldc,
-                                           splits, vec_a, vec_b, s, used);
+    return launch_gemm3<Cfg, true, false>(d.A, d.B, bias, d.C, partial, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, splits,
+                                          vec, s, used);
+  return launch_gemm3<Cfg, true, true>(d.A, d.B, bias, d.C, partial, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, splits, vec,
+                                       s, used);
+}
+
+template <class Epi>
+int run_small(const GemmArgs& g, int ta, int tb, int splits, const Epi& epi, hipStream_t s, int acc64) {
+  if (acc64) {
+    if (!ta && !tb) return launch_gemm<CfgSmall, false, false, Epi, true>(g, splits, epi, s);
+    if (!ta && tb) return launch_gemm<CfgSmall, false, true, Epi, true>(g, splits, epi, s);
+    if (ta && !tb) return launch_gemm<CfgSmall, true, false, Epi, true>(g, splits, epi, s);
+    return launch_gemm<CfgSmall, true, true, Epi, true>(g, splits, epi, s);
+  }
+  if (!ta && !tb) return launch_gemm<CfgSmall, false, false, Epi, false>(g, splits, epi, s);
+  if (!ta && tb) return launch_gemm<CfgSmall, false, true, Epi, false>(g, splits, epi, s);
+  if (ta && !tb) return launch_gemm<CfgSmall, true, false, Epi, false>(g, splits, epi, s);
+  return launch_gemm<CfgSmall, true, true, Epi, false>(g, splits, epi, s);
 }
 
 // Number of k-slices the chosen kernel really launches for a requested split count.
-int actual_splits(const GemmDesc& d, Tile t, int splits) {
+int actual_splits(Tile t, int K, int splits) {
   int kps;
-  const int K = d.K;
-  if (use_v2(d)) return gemm2_split_layout<Cfg2Acc>(K, splits, &kps);
   switch (t) {
-    case Tile::Big: return split_layout<CfgBig>(K, splits, &kps);
-    case Tile::Mid: return split_layout<CfgMid>(K, splits, &kps);
+    case Tile::Wide: return gemm3_split_layout<Cfg3Wide>(K, splits, &kps);
+    case Tile::Sq: return gemm3_split_layout<Cfg3Sq>(K, splits, &kps);
+    case Tile::Narrow: return gemm3_split_layout<Cfg3Narrow>(K, splits, &kps);
+    case Tile::Acc: return gemm3_split_layout<Cfg3Acc>(K, splits, &kps);
     default: return split_layout<CfgSmall>(K, splits, &kps);
   }
 }
@@ -110,6 +117,24 @@ GemmArgs make_args(const GemmDesc& d) {
   return g;
 }
 
+// The product into C (partial == nullptr) or into split-K planes.
+int dispatch(Tile t, const GemmDesc& d, float* partial, int splits, hipStream_t s, int* used) {
+  switch (t) {
+    case Tile::Wide: return run3<Cfg3Wide>(d, partial, splits, s, used);
+    case Tile::Sq: return run3<Cfg3Sq>(d, partial, splits, s, used);
+    case Tile::Narrow: return run3<Cfg3Narrow>(d, partial, splits, s, used);
+    case Tile::Acc: return run3<Cfg3Acc>(d, partial, splits, s, used);
+    default: break;
+  }
+  *used = actual_splits(t, d.K, partial ? splits : 1);
+  if (partial) {
+    EpiPartial epi{partial, d.M, d.N};
+    return run_small(make_args(d), d.trans_a, d.trans_b, *used, epi, s, d.acc64);
+  }
+  EpiStore epi{d.C, d.bias, d.M, d.N, d.ldc};
+  return run_small(make_args(d), d.trans_a, d.trans_b, 1, epi, s, d.acc64);
+}
+
 int check_desc(const GemmDesc& d) {
   if (d.M < 0 || d.N < 0 || d.K < 0) return fail(HSL_ERR_ARG, "gemm: negative size");
   const int a_cols = d.trans_a ? d.M : d.K, b_cols = d.trans_b ? d.K : d.N;
@@ -123,11 +148,10 @@ int check_desc(const GemmDesc& d) {
 }  // namespace
 
 int gemm_pick_splits(int M, int N, int K, int acc64) {
-  const Tile t = pick_tile(M, N, acc64);
-  const int tiles = tile_count(t, M, N);
-  if (tiles >= 512 || K < 1024) return 1;
-  int s = (1024 + tiles - 1) / tiles;     // aim for ~1024 workgroups
-  const int max_by_k = K / 512;           // keep >= 512 k per split
+  const long tiles = tile_count(pick_tile(M, N, acc64), M, N);
+  if (tiles >= kFill || K < 1024) return 1;
+  int s = (int)((2 * kFill + tiles - 1) / tiles);  // aim for ~1024 workgroups
+  const int max_by_k = K / 512;                    // keep >= 512 k per split
   if (s > max_by_k) s = max_by_k;
   if (s > 64) s = 64;
   return s < 1 ? 1 : s;
@@ -140,11 +164,7 @@ size_t gemm_ws_bytes(int M, int N, int K, int acc64) {
 
 int gemm_partials(const GemmDesc& d, float* partials, int splits, hipStream_t s, int* used) {
   HSL_CHECK(check_desc(d));
-  if (use_v2(d)) return dispatch_v2(d, partials, splits, s, used);
-  const Tile t = pick_tile(d.M, d.N, d.acc64);
-  *used = actual_splits(d, t, splits);
-  EpiPartial epi{partials, d.M, d.N};
-  return dispatch(t, make_args(d), d.trans_a, d.trans_b, *used, epi, s, d.acc64);
+  return dispatch(pick_tile(d.M, d.N, d.acc64), d, partials, splits, s, used);
 }
 
 int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s) {
@@ -152,23 +172,14 @@ int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s) {
   if (d.M == 0 || d.N == 0) return HSL_OK;
   const Tile t = pick_tile(d.M, d.N, d.acc64);
   int splits = gemm_pick_splits(d.M, d.N, d.K, d.acc64);
-  if (splits > 1) splits = actual_splits(d, t, splits);
+  if (splits > 1) splits = actual_splits(t, d.K, splits);
   const size_t need = sizeof(float) * (size_t)splits * d.M * d.N;
   if (splits > 1 && (ws == nullptr || ws_bytes < need)) splits = 1;
   float* P = static_cast<float*>(ws);
-  if (use_v2(d)) {
-    int used = 1;
-    HSL_CHECK(dispatch_v2(d, splits > 1 ? P : nullptr, splits, s, &used));
-    if (splits == 1) return HSL_OK;
-    splits = used;
-  } else if (splits == 1) {
-    EpiStore epi{d.C, d.bias, d.M, d.N, d.ldc};
-    return dispatch(t, make_args(d), d.trans_a, d.trans_b, 1, epi, s, d.acc64);
-  } else {
-    EpiPartial epi{P, d.M, d.N};
-    HSL_CHECK(dispatch(t, make_args(d), d.trans_a, d.trans_b, splits, epi, s, d.acc64));
-  }
-  return splitk_reduce(P, splits, d.bias, d.C, d.M, d.N, d.ldc, s);
+  int used = 1;
+  if (splits == 1) return dispatch(t, d, nullptr, 1, s, &used);
+  HSL_CHECK(dispatch(t, d, P, splits, s, &used));
+  return splitk_reduce(P, used, d.bias, d.C, d.M, d.N, d.ldc, s);
 }
 
 int splitk_reduce(const float* P, int splits, const float* bias, float* C, int M, int N, int ldc, hipStream_t s) {

@@ -266,15 +266,27 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
   __syncthreads();
 }
 
-// Maps blockIdx to (tile_m, tile_n, split) so that the tiles one XCD works on are
-// contiguous (workgroup i runs on XCD i % 8; neighbouring tiles share A/B rows
-// in that XCD's L2).
-__device__ __forceinline__ void tile_coords(const GemmArgs& g, int* tm, int* tn) {
-  const int total = g.tiles_m * g.tiles_n;
+// Maps blockIdx.x to a tile (tm, tn).  Workgroup i runs on XCD i % 8, so each XCD gets
+// a contiguous range of the tile sequence (when the tile count divides by 8), and the
+// sequence visits tiles in groups of 8 row panels: consecutive tiles walk down 8 rows
+// of one column before moving to the next column.  The workgroups in flight on one XCD
+// (two per CU) then share 8 A panels and 8 B panels, which stay in that XCD's L2,
+// instead of sweeping every column of B for each row panel.
+__device__ __forceinline__ void gemm_tile_order(int tiles_m, int tiles_n, int* tm, int* tn) {
+  const int total = tiles_m * tiles_n;
   int id = blockIdx.x;
   if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
-  *tm = id / g.tiles_n;
-  *tn = id % g.tiles_n;
+  constexpr int GM = 8;
+  const int group = id / (GM * tiles_n);
+  const int first = group * GM;
+  const int rows = min(GM, tiles_m - first);
+  const int in = id - group * GM * tiles_n;
+  *tm = first + in % rows;
+  *tn = in / rows;
+}
+
+__device__ __forceinline__ void tile_coords(const GemmArgs& g, int* tm, int* tn) {
+  gemm_tile_order(g.tiles_m, g.tiles_n, tm, tn);
 }
 
 template <class Cfg, bool TA, bool TB, class Epi, bool ACC64 = false>

@@ -17,6 +17,10 @@ Prints ONE JSON line:
               same workload, timed on this host's cores
   scan        configs[4] parallel scan (T=4096 B=16 H=1024) forward and
               backward kernels: algorithmic HBM bytes / launch time
+  modes       every configured shape (configs[0..4], configs[1] in both modes)
+              as one graph-replayed fwd+bwd step each; algorithmic TFLOP/s counts
+              24*T*B*H*(D+H) (recurrent) or the projection and dW_ih products
+              2*2*T*B*D*4H (parallel, x is data so no dx)
 """
 
 import argparse
@@ -163,6 +167,55 @@ def bench_scan(args):
     return res
 
 
+# configs[0..4] of BASELINE.json (configs[1] in both modes): (name, T, B, D, H, parallel, a)
+MODE_CONFIGS = [
+    ("configs[0]", 32, 16, 64, 128, False, 1e-4),
+    ("configs[1]", 128, 32, 256, 256, False, 1e-4),
+    ("configs[1]", 128, 32, 256, 256, True, 1e-4),
+    ("configs[2] a~U(0,0.5)", 256, 32, 256, 512, False, None),
+    ("configs[3]", 64, 32, 1024, 2048, False, 1e-4),
+    ("configs[4]", 4096, 16, 256, 1024, True, 0.0),
+]
+
+
+def bench_modes(args):
+    """Every configured shape in its mode(s): one graph replay of fwd+bwd per step,
+    same recipe as the headline (seed 0, module on CPU, x ~ N(0,1), loss out.sum())."""
+    from prlstm_amd import HeadStartLSTM
+    from prlstm_amd.graph import GraphedTrainStep
+    dev = torch.device("cuda", 0)
+    res = []
+    for name, t, b, d, h, par, a in MODE_CONFIGS:
+        torch.manual_seed(0)
+        m = HeadStartLSTM(d, h, a_init=0.0 if a is None else a, parallel=par)
+        if a is None:  # the configs[2] variant: a drawn right after init
+            with torch.no_grad():
+                m.a.copy_(torch.rand(4) * 0.5)
+        x = torch.randn(t, b, d)
+        m = m.to(dev)
+        step = GraphedTrainStep(m, x.to(dev))
+        for _ in range(3):
+            step.step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = max(5, args.steps // 2)
+        e0.record()
+        for _ in range(n):
+            step.step()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / n
+        # parallel: the projection and dW_ih products, 2 * (2*T*B*D*4H); recurrent: 24*T*B*H*(D+H)
+        flops = 2 * (2 * t * b * d * 4 * h) if par else 24 * t * b * h * (d + h)
+        res.append({"config": name, "mode": "parallel" if par else "recurrent", "T": t, "B": b, "D": d, "H": h,
+                    "ms_per_step": round(ms, 4), "timesteps_batch_per_s": round(t * b / ms * 1e3, 1),
+                    "algorithmic_tflops": round(flops / ms / 1e9, 2)})
+        log(f"mode {name} {'parallel' if par else 'recurrent'}: {ms:.4f} ms/step")
+        del step, m
+        torch.cuda.empty_cache()
+    return res
+
+
 def bench_cpu(args):
     """The reference torch backend restated (oracle/), fp32 on this host's cores."""
     from oracle.hsl_oracle import RefHeadStartLSTM
@@ -205,6 +258,7 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-scan", action="store_true")
+    ap.add_argument("--no-modes", action="store_true", help="skip the per-config table of both modes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -216,6 +270,7 @@ def main():
 
     ms, wall_ms, kern, path, fused = bench_gpu(args)
     scan = None if args.no_scan else bench_scan(args)
+    modes = None if args.no_modes else bench_modes(args)
     cpu = None if args.no_cpu else bench_cpu(args)
 
     step_flops = 24.0 * T * B * H * (D + H)           # algorithmic fwd+bwd FLOPs
@@ -260,6 +315,7 @@ def main():
         "kernels_ms": {k: round(v, 5) for k, v in kern.items()},
         "wall_ms_per_step": round(wall_ms, 5),
         "scan": scan,
+        "modes": modes,
         "cpu_baseline": cpu,
     }
     if cpu:

@@ -135,6 +135,17 @@ int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float*
                 float eps, float* gates, float* out, float* c_seq,
                 int T, int B, int D, int H, void* stream);
 
+/* hsl_par_fwd for a half-precision module: x [T,B,D] and w_ih [4H,D] are bf16
+ * (fmt 0) or fp16 (fmt 1); b_ih, c0 and everything written are fp32.  The input
+ * projection runs on 16-bit MFMA with fp32 accumulation: each product of two 16-bit
+ * values is exact in fp32, so gates equal the fp32 projection of the widened
+ * operands up to the order of the fp32 additions.  Replaces the same call sites as
+ * hsl_par_fwd (_parallel.py:38-74) for modules moved to bf16/fp16 (the way
+ * test_parallel.py:22-38 runs bf16). */
+int hsl_par_fwd_b16(const void* x, const float* c0, const void* w_ih, const float* b_ih,
+                    float eps, float* gates, float* out, float* c_seq,
+                    int T, int B, int D, int H, int fmt, void* stream);
+
 size_t hsl_par_bwd_ws_bytes(int T, int B, int D, int H);
 
 /* Backward of hsl_par_fwd w.r.t. x, W_ih, b_ih and c0 (W_hh, b_hh, a and h0
@@ -172,6 +183,13 @@ size_t hsl_gemm_ws_bytes(int M, int N, int K);
 int hsl_gemm_f32(const float* A, const float* Bm, const float* bias, float* C,
                  int M, int N, int K, int lda, int ldb, int ldc,
                  int trans_a, int trans_b, void* ws, size_t ws_bytes, void* stream);
+
+/* C[M,N] = A[M,K] . B[N,K]^T (+ bias[N]) with A, B bf16 (fmt 0) or fp16 (fmt 1),
+ * fp32 accumulation, C and bias fp32 (row-major, leading dimensions in elements).
+ * The 16-bit counterpart of hsl_gemm_f32's trans_b product (F.linear,
+ * _parallel.py:56) used by hsl_par_fwd_b16. */
+int hsl_gemm_b16(const void* A, const void* B, const float* bias, float* C,
+                 int M, int N, int K, int lda, int ldb, int ldc, int fmt, void* stream);
 
 #ifdef __cplusplus
 }

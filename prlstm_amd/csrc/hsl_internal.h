@@ -83,6 +83,10 @@ int gemm_partials(const GemmDesc& d, float* partials, int splits, hipStream_t s,
 // (+ bias[N] when non-null).
 int splitk_reduce(const float* P, int splits, const float* bias, float* C, int M, int N, int ldc, hipStream_t s);
 int gemm_pick_splits(int M, int N, int K, int acc64);
+// C[M][N] = A[M][K] . B[N][K]^T (+ bias[N]) with 16-bit A and B (fmt 0 bf16, 1 fp16),
+// fp32 accumulation and output (gemm_b16.hip).
+int gemm_b16_run(const void* A, const void* B, const float* bias, float* C, int M, int N, int K, int lda, int ldb,
+                 int ldc, int fmt, hipStream_t s);
 
 // ---- shared finalisation (recurrent.hip) ------------------------------------------
 // db = sum_b db_part[b][:] ; db_ih = db ; db_hh = a_g db ; da[g] = sum_{n in g} rowdot[n] + b_hh[n] db[n].

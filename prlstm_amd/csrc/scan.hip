@@ -337,6 +337,19 @@ int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float*
   return scan_fwd(gates, c0, eps, out, c_seq, T, B, H, s);
 }
 
+int hsl_par_fwd_b16(const void* x, const float* c0, const void* w_ih, const float* b_ih, float eps, float* gates,
+                    float* out, float* c_seq, int T, int B, int D, int H, int fmt, void* stream) {
+  HSL_CHECK(check_scan_dims(T, B, H));
+  if (D < 0) return fail(HSL_ERR_ARG, "negative D");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (T == 0 || B == 0 || H == 0) return HSL_OK;
+  if (!x || !w_ih || !b_ih || !gates || !out || !c_seq) return fail(HSL_ERR_ARG, "hsl_par_fwd_b16: null pointer");
+  const int slot = timing_begin(kTimeInputProj, s);
+  HSL_CHECK(gemm_b16_run(x, w_ih, b_ih, gates, T * B, 4 * H, D, D, D, 4 * H, fmt, s));
+  timing_end(slot, s);
+  return scan_fwd(gates, c0, eps, out, c_seq, T, B, H, s);
+}
+
 size_t hsl_par_bwd_ws_bytes(int T, int B, int D, int H) {
   if (T < 0 || B < 0 || D < 0 || H < 0) return 0;
   ParWs w;

@@ -178,10 +178,68 @@ class ParallelFn(torch.autograd.Function):
 _HALF = (torch.bfloat16, torch.float16)
 
 
+class ParallelHalfFn(torch.autograd.Function):
+    """Parallel mode of a bf16/fp16 module: x and W_ih stay 16-bit for the input
+    projection, which runs on 16-bit MFMA with fp32 accumulation (each product of two
+    16-bit values is exact in fp32); c0 and b_ih arrive widened, and the scan, the
+    outputs and the whole backward are fp32 (x and W_ih widened there), as in
+    ``ParallelFn``."""
+
+    @staticmethod
+    def forward(ctx, x, c0, w_ih, b_ih, eps):
+        if x.dim() != 3:
+            raise RuntimeError(f"x must be [T, B, D], got shape {tuple(x.shape)}")
+        T, B, D = x.shape
+        H = b_ih.shape[0] // 4
+        if tuple(w_ih.shape) != (4 * H, D) or (c0 is not None and tuple(c0.shape) != (B, H)):
+            raise RuntimeError("weight_ih_l0 must be [4H, D] and c0 [B, H]")
+        for name, t in (("x", x), ("weight_ih_l0", w_ih), ("bias_ih_l0", b_ih), ("c0", c0)):
+            if t is not None and (t.device.type != "cuda" or t.device != x.device):
+                raise RuntimeError(f"prlstm_amd runs on ROCm devices only: {name} is on {t.device}")
+        if w_ih.dtype != x.dtype or b_ih.dtype != torch.float32 or (c0 is not None and c0.dtype != torch.float32):
+            raise RuntimeError("ParallelHalfFn: x and W_ih share a 16-bit dtype; b_ih and c0 are float32")
+        x, c0, w_ih, b_ih = map(_c, (x, c0, w_ih, b_ih))
+        ctx.set_materialize_grads(False)
+        gates = x.new_empty(T, B, 4 * H, dtype=torch.float32)
+        out = x.new_empty(T, B, H, dtype=torch.float32)
+        c_seq = x.new_empty(T, B, H, dtype=torch.float32)
+        fmt = 0 if x.dtype == torch.bfloat16 else 1
+        P = _lib.ptr
+        _lib.call("hsl_par_fwd_b16", P(x), P(c0), P(w_ih), P(b_ih), float(eps), P(gates), P(out),
+                  P(c_seq), T, B, D, H, fmt, _lib.stream_of(x.device))
+        ctx.save_for_backward(x, c0, w_ih, gates, c_seq)
+        ctx.dims = (T, B, D, H)
+        ctx.eps = float(eps)
+        return out, out[T - 1], c_seq[T - 1]
+
+    @staticmethod
+    def backward(ctx, dout, dh_n, dc_n):
+        x, c0, w_ih, gates, c_seq = ctx.saved_tensors
+        T, B, D, H = ctx.dims
+        dout = _grad_or_zeros(dout, c_seq)
+        dh_n, dc_n = _c(dh_n), _c(dc_n)
+        need = ctx.needs_input_grad
+        x32, w32 = x.float(), w_ih.float()
+        dx = torch.empty_like(x32) if need[0] else None
+        dc0 = x32.new_empty(B, H) if need[1] else None
+        dw_ih = torch.empty_like(w32)
+        db_ih = x32.new_empty(4 * H)
+        lib = _lib.load()
+        nbytes = lib.hsl_par_bwd_ws_bytes(T, B, D, H)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+        P = _lib.ptr
+        _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(x32), P(c0), P(gates), P(c_seq),
+                  P(w32), ctx.eps, P(dx), P(dw_ih), P(db_ih), P(dc0), P(ws), nbytes, T, B, D, H,
+                  _lib.stream_of(x.device))
+        # autograd casts each gradient to its input's dtype (x and W_ih: 16-bit)
+        return dx, dc0, dw_ih, db_ih, None
+
+
 def _widen(args):
     """bf16/fp16 operands (a module moved with ``.to(dtype)``, as the reference's tests do for
-    bf16, ``test_parallel.py:22-38``) are cast to fp32 here; the kernels then compute and
-    accumulate in fp32 and the outputs are cast back.  The casts are autograd ops, so the
+    bf16, ``test_parallel.py:22-38``) are cast to fp32 here (recurrent mode; parallel mode
+    keeps x and W_ih 16-bit for its projection, ``ParallelHalfFn``); the kernels then compute
+    and accumulate in fp32 and the outputs are cast back.  The casts are autograd ops, so the
     gradients arrive in each operand's own dtype.  Returns (args, output dtype or None)."""
     dtype = args[0].dtype
     if dtype not in _HALF:
@@ -201,5 +259,8 @@ def headstartlstm_recurrent(x, h0, c0, W_ih, W_hh, b_ih, b_hh, a):
 
 def headstartlstm_parallel(x, h0, c0, W_ih, W_hh, b_ih, b_hh, a, eps=EPS):
     """Parallel-mode functional (drop-in for ``headstartlstm_parallel``, ``_parallel.py:38``)."""
+    if x.dtype in _HALF and W_ih.dtype == x.dtype:  # 16-bit projection, fp32 everywhere else
+        c0w = None if c0 is None else c0.float()
+        return _narrow(ParallelHalfFn.apply(x, c0w, W_ih, b_ih.float(), eps), x.dtype)
     args, dtype = _widen((x, h0, c0, W_ih, W_hh, b_ih, b_hh, a))
     return _narrow(ParallelFn.apply(*args, eps), dtype)

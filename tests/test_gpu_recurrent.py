@@ -186,6 +186,12 @@ def test_sgd_training_step(dev):
         assert (p.detach().cpu() - q.detach()).abs().max() < 1e-5, n
 
 
+def test_long_sequence_persistent(dev):
+    """T=2048 on the persistent kernels: the fused weight gradients then keep 256 steps
+    (1024 products) per fp32 partial plane, the longest running sums the backward makes."""
+    check(2048, 4, 32, 512, dev, 2, a=[0.3, 0.2, 0.4, 0.1])
+
+
 def test_repeated_calls_are_deterministic(dev):
     """Persistent kernels exchange data between workgroups; repeat runs must agree bit for bit."""
     torch.manual_seed(0)

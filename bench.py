@@ -167,14 +167,16 @@ def bench_scan(args):
     return res
 
 
-# configs[0..4] of BASELINE.json (configs[1] in both modes): (name, T, B, D, H, parallel, a)
+# configs[0..4] of BASELINE.json (configs[1] in both modes), and configs[4] with the
+# module in bf16 (16-bit input projection): (name, T, B, D, H, parallel, a, dtype)
 MODE_CONFIGS = [
-    ("configs[0]", 32, 16, 64, 128, False, 1e-4),
-    ("configs[1]", 128, 32, 256, 256, False, 1e-4),
-    ("configs[1]", 128, 32, 256, 256, True, 1e-4),
-    ("configs[2] a~U(0,0.5)", 256, 32, 256, 512, False, None),
-    ("configs[3]", 64, 32, 1024, 2048, False, 1e-4),
-    ("configs[4]", 4096, 16, 256, 1024, True, 0.0),
+    ("configs[0]", 32, 16, 64, 128, False, 1e-4, torch.float32),
+    ("configs[1]", 128, 32, 256, 256, False, 1e-4, torch.float32),
+    ("configs[1]", 128, 32, 256, 256, True, 1e-4, torch.float32),
+    ("configs[2] a~U(0,0.5)", 256, 32, 256, 512, False, None, torch.float32),
+    ("configs[3]", 64, 32, 1024, 2048, False, 1e-4, torch.float32),
+    ("configs[4]", 4096, 16, 256, 1024, True, 0.0, torch.float32),
+    ("configs[4] bf16 module", 4096, 16, 256, 1024, True, 0.0, torch.bfloat16),
 ]
 
 
@@ -185,14 +187,14 @@ def bench_modes(args):
     from prlstm_amd.graph import GraphedTrainStep
     dev = torch.device("cuda", 0)
     res = []
-    for name, t, b, d, h, par, a in MODE_CONFIGS:
+    for name, t, b, d, h, par, a, dt in MODE_CONFIGS:
         torch.manual_seed(0)
         m = HeadStartLSTM(d, h, a_init=0.0 if a is None else a, parallel=par)
         if a is None:  # the configs[2] variant: a drawn right after init
             with torch.no_grad():
                 m.a.copy_(torch.rand(4) * 0.5)
-        x = torch.randn(t, b, d)
-        m = m.to(dev)
+        x = torch.randn(t, b, d).to(dt)
+        m = m.to(dev, dt)
         step = GraphedTrainStep(m, x.to(dev))
         for _ in range(3):
             step.step()
@@ -207,7 +209,8 @@ def bench_modes(args):
         ms = e0.elapsed_time(e1) / n
         # parallel: the projection and dW_ih products, 2 * (2*T*B*D*4H); recurrent: 24*T*B*H*(D+H)
         flops = 2 * (2 * t * b * d * 4 * h) if par else 24 * t * b * h * (d + h)
-        res.append({"config": name, "mode": "parallel" if par else "recurrent", "T": t, "B": b, "D": d, "H": h,
+        res.append({"config": name, "mode": "parallel" if par else "recurrent", "dtype": str(dt).split(".")[-1],
+                    "T": t, "B": b, "D": d, "H": h,
                     "ms_per_step": round(ms, 4), "timesteps_batch_per_s": round(t * b / ms * 1e3, 1),
                     "algorithmic_tflops": round(flops / ms / 1e9, 2)})
         log(f"mode {name} {'parallel' if par else 'recurrent'}: {ms:.4f} ms/step")

@@ -63,6 +63,18 @@ long long hsl_set_spin_timeout_us(long long us);
  * batch group runs on one XCD, device-scope stores otherwise), 1 = always
  * device-scope stores.  Returns the previous value.  Process-wide. */
 int hsl_set_exchange_scope(int mode);
+/* Large products C = A B^T (+bias) -- the input projection x W_ih^T + b_ih
+ * (_torch.py:96, _parallel.py:56) and hsl_gemm_f32 calls of that layout with at
+ * least 256 output tiles of 256 x 256 -- run by default (on = 1) on the bf16
+ * matrix instructions with every fp32 operand split exactly into three bf16 pieces
+ * and the six largest piece products accumulated in fp32 (error that of the fp32
+ * MFMA product); on = 0 uses the fp32 MFMA instruction for every product.  With
+ * on = 1 a non-finite element of A (or one beyond the bf16 range, 3.3895e38) makes
+ * its row of C NaN and one of B its column, where the fp32 instruction would give
+ * IEEE infinities.  Returns
+ * the previous value.  Process-wide.  No counterpart in the reference (its torch
+ * backend calls torch.nn.functional.linear). */
+int hsl_set_split_products(int on);
 /* Which path the last hsl_rec_fwd / hsl_rec_bwd on this host thread used:
  * 1 = per-step, 2 = persistent. */
 int hsl_last_recurrent_path(void);

@@ -27,6 +27,7 @@ SIGNATURES = {
     "hsl_last_recurrent_path": (_I, []),
     "hsl_last_backward_fused": (_I, []),
     "hsl_set_exchange_scope": (_I, [_I]),
+    "hsl_set_split_products": (_I, [_I]),
     "hsl_poll_error": (_I, [_P, _P, _P]),
     "hsl_set_timing": (_I, [_I]),
     "hsl_timing_collect": (_I, [_I, _P, _P]),
@@ -93,6 +94,12 @@ def call(name, *args):
 def set_recurrent_path(mode):
     """0 = automatic, 1 = one launch per time step, 2 = persistent only."""
     return load().hsl_set_recurrent_path(int(mode))
+
+
+def set_split_products(on):
+    """Large ``A B^T`` products (the input projection) on split-bf16 MFMA (1, default)
+    or on the fp32 instruction (0); returns the previous setting."""
+    return load().hsl_set_split_products(1 if on else 0)
 
 
 def set_exchange_scope(mode):

@@ -15,6 +15,7 @@ thread_local int g_last_path = 0;
 std::atomic<int> g_last_fused{0};  // process-wide: autograd runs backward on its own thread
 std::atomic<int> g_path_mode{0};
 std::atomic<int> g_exchange_scope{0};
+std::atomic<int> g_split_products{1};
 std::atomic<long long> g_spin_us{2000000};
 std::mutex g_dev_mu;
 DeviceInfo g_devs[64];
@@ -78,6 +79,7 @@ void timing_end(int slot, hipStream_t s) {
 
 int recurrent_path_mode() { return g_path_mode.load(); }
 int exchange_scope_mode() { return g_exchange_scope.load(); }
+int split_products_mode() { return g_split_products.load(); }
 long long spin_timeout_ticks() { return g_spin_us.load() * 100; }  // 100 MHz clock
 void note_recurrent_path(int path) { g_last_path = path; }
 void note_backward_fused(int fused) { g_last_fused.store(fused); }
@@ -104,6 +106,8 @@ int hsl_last_recurrent_path(void) { return hsl::g_last_path; }
 int hsl_last_backward_fused(void) { return hsl::g_last_fused.load(); }
 
 int hsl_set_exchange_scope(int mode) { return hsl::g_exchange_scope.exchange(mode == 1 ? 1 : 0); }
+
+int hsl_set_split_products(int on) { return hsl::g_split_products.exchange(on ? 1 : 0); }
 
 int hsl_set_timing(int on) { return hsl::g_timing.exchange(on ? 1 : 0); }
 

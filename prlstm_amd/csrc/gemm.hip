@@ -1,5 +1,8 @@
 // hsl_gemm_f32: fp32 MFMA GEMM entry point with optional split-K.
 //
+// Large C = A B^T products (at least 256 tiles of 256 x 256, no fp64 folding) run on the
+// split-bf16 kernel of gemm_x6.hip (fp32 accuracy, 2.5x the matrix-core rate) unless
+// hsl_set_split_products(0) selects the fp32 instruction for everything.
 // Products with M, N >= 64 run on the third core (gemm3_core.h): 128x256, 128x128 or
 // 128x64 tiles, whichever is the largest that still gives two workgroups per CU, and
 // 128x64 tiles with fp64 folding for the long weight-gradient reductions.  Thinner
@@ -170,6 +173,8 @@ int gemm_partials(const GemmDesc& d, float* partials, int splits, hipStream_t s,
 int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s) {
   HSL_CHECK(check_desc(d));
   if (d.M == 0 || d.N == 0) return HSL_OK;
+  if (!d.trans_a && d.trans_b && !d.acc64 && split_products_mode() && gemm_x6_applies(d.M, d.N, d.K))
+    return gemm_x6_run(d.A, d.B, d.bias, d.C, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, s);
   const Tile t = pick_tile(d.M, d.N, d.acc64);
   int splits = gemm_pick_splits(d.M, d.N, d.K, d.acc64);
   if (splits > 1) splits = actual_splits(t, d.K, splits);

@@ -35,6 +35,7 @@ int device_info(DeviceInfo* out);
 // Process-wide options (see hsl_set_recurrent_path / hsl_set_spin_timeout_us).
 int recurrent_path_mode();
 int exchange_scope_mode();  // 1: persistent kernels always use device-scope stores
+int split_products_mode();  // 1: large A B^T products on split bf16 pieces (gemm_x6.hip)
 // Timing hooks (active only after hsl_set_timing(1)): events around one launch.
 enum TimingKind { kTimeRecFwd = 1, kTimeRecBwd = 2, kTimeScanFwd = 3, kTimeScanBwd = 4,
                   kTimeInputProj = 5, kTimeStepFwd = 6, kTimeStepBwd = 7 };
@@ -85,6 +86,9 @@ int splitk_reduce(const float* P, int splits, const float* bias, float* C, int M
 int gemm_pick_splits(int M, int N, int K, int acc64);
 // C[M][N] = A[M][K] . B[N][K]^T (+ bias[N]) with 16-bit A and B (fmt 0 bf16, 1 fp16),
 // fp32 accumulation and output (gemm_b16.hip).
+bool gemm_x6_applies(int M, int N, int K);
+int gemm_x6_run(const float* A, const float* B, const float* bias, float* C, int M, int N, int K, int lda, int ldb,
+                int ldc, hipStream_t s);
 int gemm_b16_run(const void* A, const void* B, const float* bias, float* C, int M, int N, int K, int lda, int ldb,
                  int ldc, int fmt, hipStream_t s);
 

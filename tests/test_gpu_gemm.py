@@ -69,3 +69,84 @@ def test_gemm_empty_and_unaligned(dev):
     C = _gemm(A, B, None, 37, 23, 19, 0, 0)
     ref = A.cpu().double() @ B.cpu().double()
     assert (C.cpu().double() - ref).abs().max() < 1e-4
+
+
+@pytest.fixture
+def split_products():
+    prev = _lib.set_split_products(1)
+    yield
+    _lib.set_split_products(prev)
+
+
+def _both(A, B, bias, M, N, K, lda=None, ldb=None):
+    """C = A B^T (+bias) by the split-bf16 kernel and by the fp32 MFMA kernel."""
+    dev = A.device
+    out = []
+    for on in (1, 0):
+        _lib.set_split_products(on)
+        C = torch.empty(M, N, device=dev)
+        P = _lib.ptr
+        _lib.call("hsl_gemm_f32", P(A), P(B), P(bias), P(C), M, N, K, lda or K, ldb or K, N, 0, 1,
+                  None, 0, _lib.stream_of(dev))
+        out.append(C.cpu().double())
+    _lib.set_split_products(1)
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,pad_a,pad_b", [(4096, 4096, 256, 0, 0), (4096 + 37, 4096 + 100, 207, 0, 0),
+                                               (4352, 4096, 96, 3, 1), (2048, 8192, 1024, 0, 0)])
+def test_split_products_as_accurate_as_fp32(dev, split_products, M, N, K, pad_a, pad_b):
+    """Large A B^T products (>= 256 tiles of 256x256) take the split-bf16 kernel: every
+    fp32 operand is split exactly into three bf16 pieces and the six largest piece
+    products are accumulated in fp32.  Against the fp64 product it must meet the fp32
+    bound, and its error statistics must match those of the fp32 MFMA kernel on the
+    same operands (rows sampled for the fp64 reference)."""
+    print(f"split products M={M} N={N} K={K} pad=({pad_a},{pad_b})", flush=True)
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randn(M, K + pad_a, generator=g)
+    b = torch.randn(N, K + pad_b, generator=g) * 0.1
+    bias = torch.randn(N, generator=g)
+    cx6, c32 = _both(a.to(dev), b.to(dev), bias.to(dev), M, N, K, K + pad_a, K + pad_b)
+    assert not torch.equal(cx6, c32)  # two different kernels ran
+    rows = torch.arange(0, M, 97)
+    av, bv = a[rows, :K].double(), b[:, :K].double()
+    ref = av @ bv.t() + bias.double()
+    scale = av.abs() @ bv.abs().t() + bias.double().abs()
+    ex6 = (cx6[rows] - ref).abs() / scale
+    e32 = (c32[rows] - ref).abs() / scale
+    print(f"  rel err x6 max {ex6.max():.3e} rms {ex6.pow(2).mean().sqrt():.3e}; "
+          f"fp32 max {e32.max():.3e} rms {e32.pow(2).mean().sqrt():.3e}", flush=True)
+    assert float(ex6.max()) <= 2e-6 * K ** 0.5
+    assert float(ex6.pow(2).mean().sqrt()) <= 1.25 * float(e32.pow(2).mean().sqrt()) + 1e-12
+    assert float(ex6.max()) <= 2.0 * float(e32.max()) + 1e-12
+
+
+def test_split_products_non_finite(dev, split_products):
+    """A non-finite element of A makes its row of C NaN, one of B its column (piece
+    products of an infinite piece with zero pieces are NaN); finite values beyond the
+    bf16 range count as non-finite.  Everything else is unaffected, and the fp32 path
+    (split products off) keeps the IEEE results."""
+    M, N, K = 4096, 4096, 64
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn(M, K, generator=g)
+    b = torch.rand(N, K, generator=g) + 0.5
+    a[3, 5] = float("inf")
+    a[700, 0] = -float("inf")
+    a[1200, 9] = float("nan")
+    a[2000, 1] = 3.4e38  # finite in fp32, beyond bf16
+    b[17, 2] = float("inf")
+    cx6, c32 = _both(a.to(dev), b.to(dev), None, M, N, K)
+    bad_rows = torch.tensor([3, 700, 1200, 2000])
+    for r in bad_rows.tolist():
+        assert bool(torch.isnan(cx6[r]).all()), r
+    assert bool(torch.isnan(cx6[:, 17]).all())
+    keep = torch.ones(M, dtype=torch.bool)
+    keep[bad_rows] = False
+    rest = cx6[keep][:, torch.arange(N) != 17]
+    assert bool(torch.isfinite(rest).all())
+    ref = c32[keep][:, torch.arange(N) != 17]
+    assert float(((rest - ref).abs() / (ref.abs() + 1.0)).max()) < 1e-5
+    # the fp32 instruction: IEEE infinities
+    assert bool(torch.isposinf(c32[3, :17]).all()) and bool(torch.isneginf(c32[700, :17]).all())
+    assert bool(torch.isnan(c32[1200]).all()) and bool(torch.isinf(c32[5:10, 17]).all())
+    assert torch.equal(torch.sign(c32[5:10, 17]), torch.sign(a[5:10, 2]).double())

@@ -63,12 +63,15 @@ long long hsl_set_spin_timeout_us(long long us);
  * batch group runs on one XCD, device-scope stores otherwise), 1 = always
  * device-scope stores.  Returns the previous value.  Process-wide. */
 int hsl_set_exchange_scope(int mode);
-/* Large products C = A B^T (+bias) -- the input projection x W_ih^T + b_ih
- * (_torch.py:96, _parallel.py:56) and hsl_gemm_f32 calls of that layout with at
- * least 256 output tiles of 256 x 256 -- run by default (on = 1) on the bf16
- * matrix instructions with every fp32 operand split exactly into three bf16 pieces
- * and the six largest piece products accumulated in fp32 (error that of the fp32
- * MFMA product); on = 0 uses the fp32 MFMA instruction for every product.  With
+/* Large products run by default (on = 1) on the bf16 matrix instructions with
+ * every fp32 operand split exactly into three bf16 pieces and the six largest piece
+ * products accumulated in fp32 (error that of the fp32 MFMA product):
+ *  - C = A B^T (+bias) with at least 256 output tiles of 256 x 256: the input
+ *    projection x W_ih^T + b_ih (_torch.py:96, _parallel.py:56);
+ *  - C = A^T B of at least 8 GFLOP with both sides >= 256: the weight gradients
+ *    (_torch.py:157-162), split along K into fp32 runs of at most 2048 k that are
+ *    added in fp64 (workspace permitting; otherwise the fp32 kernel runs).
+ * on = 0 uses the fp32 MFMA instruction for every product.  With
  * on = 1 a non-finite element of A (or one beyond the bf16 range, 3.3895e38) makes
  * its row of C NaN and one of B its column, where the fp32 instruction would give
  * IEEE infinities.  Returns
@@ -189,7 +192,8 @@ int hsl_scan_bwd(const float* gates, const float* c0, const float* c_seq,
  *   trans_a = 0: A is [M,lda] row-major; 1: A is [K,lda] and op(A) = A^T
  *   trans_b = 0: B is [K,ldb] row-major; 1: B is [N,ldb] and op(B) = B^T
  * Split-K (for K much larger than M*N) goes through ws; with ws_bytes = 0 the
- * product is computed without splitting.
+ * product is computed without splitting.  hsl_gemm_ws_bytes is enough for every
+ * layout (the split-bf16 A^T B kernel may use more planes than the others).
  * ------------------------------------------------------------------------- */
 size_t hsl_gemm_ws_bytes(int M, int N, int K);
 int hsl_gemm_f32(const float* A, const float* Bm, const float* bias, float* C,

@@ -1,8 +1,9 @@
 // hsl_gemm_f32: fp32 MFMA GEMM entry point with optional split-K.
 //
-// Large C = A B^T products (at least 256 tiles of 256 x 256, no fp64 folding) run on the
-// split-bf16 kernel of gemm_x6.hip (fp32 accuracy, 2.5x the matrix-core rate) unless
-// hsl_set_split_products(0) selects the fp32 instruction for everything.
+// Large C = A B^T products (at least 256 tiles of 256 x 256, no fp64 folding) and large
+// C = A^T B weight gradients (>= 8 GFLOP, split into fp32 runs of <= 2048 k added in fp64)
+// run on the split-bf16 kernel of gemm_x6.hip (fp32 accuracy, 2.5x the matrix-core rate)
+// unless hsl_set_split_products(0) selects the fp32 instruction for everything.
 // Products with M, N >= 64 run on the third core (gemm3_core.h): 128x256, 128x128 or
 // 128x64 tiles, whichever is the largest that still gives two workgroups per CU, and
 // 128x64 tiles with fp64 folding for the long weight-gradient reductions.  Thinner
@@ -11,6 +12,8 @@
 // Split-K writes fp32 partial tiles [splits][M][N] and a second kernel adds them in
 // fp64 (plus the bias), so long reductions (K = T*B up to 65536 for the weight
 // gradients) lose less accuracy than one fp32 running sum.
+#include <algorithm>
+
 #include "gemm3_core.h"
 
 namespace hsl {
@@ -165,16 +168,58 @@ size_t gemm_ws_bytes(int M, int N, int K, int acc64) {
   return s > 1 ? sizeof(float) * (size_t)s * M * N : 0;
 }
 
+namespace {
+// Split count of the split-bf16 A^T B kernel for this product when it is taken with at
+// most `max_planes` partial planes (0: not taken, because split products are off, the
+// product is small, or the planes would leave fp32 running sums longer than 2048 k).
+int x6_tn_take(const GemmDesc& d, long max_planes) {
+  if (!d.trans_a || d.trans_b || !split_products_mode()) return 0;
+  int s = gemm_x6_tn_splits(d.M, d.N, d.K);
+  if (s <= 0) return 0;
+  if (s > max_planes) s = (int)max_planes;
+  if (s < 1 || (long)s * 2048 < d.K) return 0;
+  return s;
+}
+}  // namespace
+
+size_t gemm_ws_bytes_layout(int M, int N, int K, int acc64, int trans_a, int trans_b) {
+  size_t need = gemm_ws_bytes(M, N, K, acc64);
+  if (trans_a && !trans_b && split_products_mode()) {
+    const int s = gemm_x6_tn_splits(M, N, K);
+    if (s > 1) need = std::max(need, sizeof(float) * (size_t)s * M * N);
+  }
+  return need;
+}
+
+int gemm_tn_planes(int M, int N, int K) {
+  int s = gemm_pick_splits(M, N, K, 1);
+  if (split_products_mode()) s = std::max(s, gemm_x6_tn_splits(M, N, K));
+  return s;
+}
+
 int gemm_partials(const GemmDesc& d, float* partials, int splits, hipStream_t s, int* used) {
   HSL_CHECK(check_desc(d));
-  return dispatch(pick_tile(d.M, d.N, d.acc64), d, partials, splits, s, used);
+  if (const int sx = x6_tn_take(d, splits))
+    return gemm_x6_run(d.A, d.B, nullptr, nullptr, partials, d.M, d.N, d.K, d.lda, d.ldb, d.N, 1, 0, sx, s, used);
+  return dispatch(pick_tile(d.M, d.N, d.acc64), d, partials, std::min(splits, gemm_pick_splits(d.M, d.N, d.K, d.acc64)), s,
+                  used);
 }
 
 int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s) {
   HSL_CHECK(check_desc(d));
   if (d.M == 0 || d.N == 0) return HSL_OK;
   if (!d.trans_a && d.trans_b && !d.acc64 && split_products_mode() && gemm_x6_applies(d.M, d.N, d.K))
-    return gemm_x6_run(d.A, d.B, d.bias, d.C, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, s);
+    return gemm_x6_run(d.A, d.B, d.bias, d.C, nullptr, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, 0, 1, 1, s, nullptr);
+  // planes the workspace holds (one split needs none: it writes C directly)
+  const long planes = ws ? (long)(ws_bytes / (sizeof(float) * (size_t)d.M * d.N)) : 0;
+  if (const int sx = x6_tn_take(d, planes > 1 ? planes : 1)) {
+    if (sx == 1)
+      return gemm_x6_run(d.A, d.B, d.bias, d.C, nullptr, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, 1, 0, 1, s, nullptr);
+    float* P = static_cast<float*>(ws);
+    int used = 1;
+    HSL_CHECK(gemm_x6_run(d.A, d.B, nullptr, nullptr, P, d.M, d.N, d.K, d.lda, d.ldb, d.N, 1, 0, sx, s, &used));
+    return splitk_reduce(P, used, d.bias, d.C, d.M, d.N, d.ldc, s);
+  }
   const Tile t = pick_tile(d.M, d.N, d.acc64);
   int splits = gemm_pick_splits(d.M, d.N, d.K, d.acc64);
   if (splits > 1) splits = actual_splits(t, d.K, splits);
@@ -203,7 +248,8 @@ extern "C" {
 
 size_t hsl_gemm_ws_bytes(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return hsl::gemm_ws_bytes(M, N, K, 0);
+  // enough for every layout: the split A^T B kernel may want more planes than the others
+  return hsl::gemm_ws_bytes_layout(M, N, K, 0, 1, 0);
 }
 
 int hsl_gemm_f32(const float* A, const float* Bm, const float* bias, float* C, int M, int N, int K, int lda,

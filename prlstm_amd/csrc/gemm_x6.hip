@@ -1,6 +1,11 @@
-// Large fp32 products C[M,N] = A[M,K] . B[N,K]^T (+ bias[N]) on the 16-bit matrix cores:
-// the input projection x W_ih^T + b_ih (_torch.py:96, _parallel.py:56) of parallel mode and
-// of the per-step path, and hsl_gemm_f32 calls of that layout.
+// Large fp32 products on the 16-bit matrix cores, in two layouts:
+//  * C[M,N] = A[M,K] . B[N,K]^T (+ bias[N]): the input projection x W_ih^T + b_ih
+//    (_torch.py:96, _parallel.py:56) of parallel mode and of the per-step path;
+//  * C[M,N] = A[K,M]^T . B[K,N]: the weight gradients dgates^T h and dgates^T x over
+//    K = T*B (_torch.py:157-162, and autograd's in parallel mode), split along K into fp32
+//    partial planes of at most 2048 k each that are added in fp64 (splitk_reduce, or the
+//    caller's own fp64 finalisation) -- the accuracy that the fp32 kernel gets from folding
+//    its accumulators into fp64 registers, which the 8-wave tile has no room for.
 //
 // Exact three-way split.  Each fp32 value v is written as v = v0 + v1 + v2 with bf16
 // pieces v0 = bf16(v) (round to nearest even), v1 = bf16(v - v0), v2 = v - v0 - v1.  The
@@ -34,6 +39,8 @@
 // repeat of the last slice, so the compiler can interleave the split with the products.
 // Shapes with partial tiles (or operands without 16-byte alignment) launch a second
 // instance that reads element-wise from clamped addresses and zeroes what lies outside.
+// A row-contiguous operand ([k][row]) is loaded as two k-rows of four rows per thread and
+// written transposed, each row's k-pair as one 32-bit word per piece.
 #include "gemm_core.h"
 
 namespace hsl {
@@ -44,25 +51,37 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kBT = 256;                   // tile rows and columns
 constexpr int kBK = 16;                    // k per slice
-constexpr int kThreads = 512;              // 8 waves, 2 (rows) x 4 (columns)
-constexpr int kWN = 4, kTM = 128, kTN = 64, kFM = kTM / 32, kFN = kTN / 32;
+constexpr int kThreads = 512;              // 8 waves
 constexpr int kLDK = kBK + 8;              // LDS row stride in bf16 elements (48 bytes)
-constexpr int kPiece = kBT * kLDK;         // one piece of one operand
-constexpr int kBuf = 6 * kPiece;           // pieces 0-2 of A, then pieces 0-2 of B
-constexpr int kCh = kBT * kBK / 4 / kThreads;  // 16-byte chunks per thread and operand
-constexpr size_t kLdsBytes = 2 * kBuf * sizeof(unsigned short);
-static_assert(kCh * 4 * kThreads == kBT * kBK, "even split of a slice");
-static_assert(kLdsBytes <= 160 * 1024, "LDS");
+constexpr int kTnRun = 2048;               // longest k-range of one split of an A^T B product
+
+// Tile shape: BM x BN with WM x WN waves; FOLD > 0 adds the MFMA accumulators into a
+// second fp32 accumulator every FOLD slices (so no accumulator rounding happens at the
+// magnitude of a long running sum more than once per FOLD slices).
+template <int BM_, int BN_, int WM_, int WN_, int FOLD_>
+struct X6Shape {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, FOLD = FOLD_;
+  static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  static constexpr int PA = BM * kLDK, PB = BN * kLDK;  // one piece of A / of B
+  static constexpr int BUF = 3 * (PA + PB);             // pieces 0-2 of A, then of B
+  static constexpr size_t LDS = 2 * BUF * sizeof(unsigned short);
+  static_assert(WM * WN * 64 == kThreads && TM % 32 == 0 && TN % 32 == 0, "wave layout");
+  static_assert(LDS <= 160 * 1024, "LDS");
+};
+// x W^T: 256 x 256 tiles, 8 waves of 128 x 64
+using ShapeProj = X6Shape<256, 256, 2, 4, 0>;
+// A^T B: 256 x 128 tiles, 8 waves of 64 x 64, folded every 4 slices (64 k)
+using ShapeWgrad = X6Shape<256, 128, 4, 2, 4>;
 
 struct X6Args {
   const float* A;
   const float* B;
-  const float* bias;
-  float* C;
+  const float* bias;  // [N] or null (direct output only)
+  float* out;         // C (ldc) or split-K partial planes [split][M][N]
   int M, N, K, lda, ldb, ldc;
-  int vec;  // 16-byte loads legal (aligned bases, lda % 4 == 0, ldb % 4 == 0)
+  int kps;            // k per split (a multiple of kBK)
+  int partial;
   int tiles_m, tiles_n;
 };
 
@@ -73,15 +92,17 @@ __device__ __forceinline__ unsigned bf16_pair(float a, float b) {  // round to n
 __device__ __forceinline__ float low_half(unsigned u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float high_half(unsigned u) { return __uint_as_float(u & 0xFFFF0000u); }
 
-// The three bf16 pieces of four consecutive values (two packed pairs each).
-__device__ __forceinline__ void split4(f4 v, u32x2 (&p)[3]) {
-  const unsigned h0 = bf16_pair(v[0], v[1]), h1 = bf16_pair(v[2], v[3]);
-  const float r0 = v[0] - low_half(h0), r1 = v[1] - high_half(h0), r2 = v[2] - low_half(h1), r3 = v[3] - high_half(h1);
-  const unsigned m0 = bf16_pair(r0, r1), m1 = bf16_pair(r2, r3);
-  const float s0 = r0 - low_half(m0), s1 = r1 - high_half(m0), s2 = r2 - low_half(m1), s3 = r3 - high_half(m1);
-  p[0] = u32x2{h0, h1};
-  p[1] = u32x2{m0, m1};
-  p[2] = u32x2{bf16_pair(s0, s1), bf16_pair(s2, s3)};
+// The three bf16 pieces of two values, each piece a packed pair (a in the low half).
+__device__ __forceinline__ void split2(float a, float b, unsigned (&p)[3]) {
+  p[0] = bf16_pair(a, b);
+  const float ra = a - low_half(p[0]), rb = b - high_half(p[0]);
+  p[1] = bf16_pair(ra, rb);
+  p[2] = bf16_pair(ra - low_half(p[1]), rb - high_half(p[1]));
+}
+
+// The value of the neighbouring lane (lane ^ 1), by DPP quad permutation [1, 0, 3, 2].
+__device__ __forceinline__ float swap_pair_lane(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
 }
 
 __device__ __forceinline__ f16v mfma_bf16(u32x4 a, u32x4 b, f16v c) {
@@ -93,183 +114,310 @@ __device__ __forceinline__ f16v mfma_bf16(u32x4 a, u32x4 b, f16v c) {
 constexpr int kPa[6] = {0, 0, 1, 0, 1, 2};
 constexpr int kPb[6] = {0, 1, 0, 2, 1, 0};
 
-// One operand's chunks: chunk j of this thread is row c / 4, k-quad c % 4 of the slice
-// (c = tid + 512 j).
-template <bool FULL>
+// One operand's share of a ROWS x 16-k slice: L = ROWS / 128 16-byte loads per thread.
+//  KC (k contiguous, [row][k]): load j of thread t is row c / 4, k-quad c % 4 of the
+//      slice (c = t + 512 j); the split writes 8 bytes per piece.
+//  !KC (row contiguous, [k][row]), ROWS = 256: thread t loads rows 4 (t / 8) .. +3 at
+//      k-rows 2 (t % 8) and +1 and pairs the two k of each row (4 bytes per piece and row).
+//  !KC, ROWS = 128: thread t loads rows 4 (t / 16) .. +3 at k-row t % 16; lanes t and t^1
+//      swap half their values, so the even lane writes rows 0-1 and the odd lane rows 2-3,
+//      each as (k even, k odd) pairs.
+// `kend` bounds k (the end of this workgroup's split): masked loads zero k >= kend and
+// rows >= rows, reading clamped addresses.
+template <bool FULL, bool KC, int ROWS>
 struct X6Operand {
+  static constexpr int L = ROWS * kBK / 4 / kThreads;
+  static_assert(L == 1 || L == 2, "128 or 256 rows");
+  static constexpr int kWrites = KC ? 3 * L : (L == 2 ? 12 : 6);  // LDS writes per store
+  static constexpr int kLoads = L;
   const float* base;
-  int ld, rows, K;
-  int r[kCh], kq[kCh];
-  __device__ __forceinline__ void init(const float* b, int ld_, int r0, int rows_, int K_) {
+  int ld, rows, kend;
+  int r[L], k[L];  // KC: row and k of load j; !KC: r[0] = first row, k[0] = first k
+  int so[L];       // LDS element offsets within one piece
+  f4 v[2];
+  __device__ __forceinline__ void init(const float* b, int ld_, int r0, int rows_, int kbeg, int kend_) {
     base = b;
     ld = ld_;
     rows = rows_;
-    K = K_;
+    kend = kend_;
+    const int t = threadIdx.x;
+    if constexpr (KC) {
 #pragma unroll
-    for (int j = 0; j < kCh; ++j) {
-      const int c = threadIdx.x + kThreads * j;
-      r[j] = r0 + c / (kBK / 4);
-      kq[j] = (c % (kBK / 4)) * 4;
+      for (int j = 0; j < L; ++j) {
+        const int c = t + kThreads * j;
+        r[j] = r0 + c / (kBK / 4);
+        k[j] = kbeg + (c % (kBK / 4)) * 4;
+        so[j] = (c / (kBK / 4)) * kLDK + (c % (kBK / 4)) * 4;
+      }
+    } else if constexpr (L == 2) {
+      r[0] = r0 + 4 * (t / 8);
+      k[0] = kbeg + 2 * (t % 8);
+      so[0] = 4 * (t / 8) * kLDK + 2 * (t % 8);
+    } else {
+      const int odd = t & 1;
+      r[0] = r0 + 4 * (t / 16);
+      k[0] = kbeg + t % 16;
+      so[0] = (4 * (t / 16) + 2 * odd) * kLDK + (t % 16) - odd;
     }
   }
-  __device__ __forceinline__ void load(f4 (&v)[kCh], int slice) const {
+  __device__ __forceinline__ f4 load_rows(int kk) const {  // !KC: 4 rows at k-row kk
+    if constexpr (FULL) {
+      return *reinterpret_cast<const f4*>(base + (size_t)kk * ld + r[0]);
+    } else {
+      f4 x;
+      const bool kok = kk < kend;
+      const float* kp = base + (size_t)(kok ? kk : kend - 1) * ld;  // a k-row that exists
 #pragma unroll
-    for (int j = 0; j < kCh; ++j) {
-      const int k = slice * kBK + kq[j];
-      if constexpr (FULL) {
-        v[j] = *reinterpret_cast<const f4*>(base + (size_t)r[j] * ld + k);
-      } else {
-        const bool rok = r[j] < rows;
-        const float* rp = base + (size_t)(rok ? r[j] : rows - 1) * ld;  // a row that exists
+      for (int i = 0; i < 4; ++i) {
+        const int rr = r[0] + i;
+        const float e = kp[rr < rows ? rr : rows - 1];
+        x[i] = (kok && rr < rows) ? e : 0.f;
+      }
+      return x;
+    }
+  }
+  __device__ __forceinline__ void load(int slice) {
+    const int ks = slice * kBK;
+    if constexpr (KC) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int kk = k + e;
-          const float x = rp[kk < K ? kk : K - 1];
-          v[j][e] = (rok && kk < K) ? x : 0.f;
+      for (int j = 0; j < L; ++j) {
+        const int kk0 = k[j] + ks;
+        if constexpr (FULL) {
+          v[j] = *reinterpret_cast<const f4*>(base + (size_t)r[j] * ld + kk0);
+        } else {
+          const bool rok = r[j] < rows;
+          const float* rp = base + (size_t)(rok ? r[j] : rows - 1) * ld;  // a row that exists
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int kk = kk0 + e;
+            const float x = rp[kk < kend ? kk : kend - 1];
+            v[j][e] = (rok && kk < kend) ? x : 0.f;
+          }
         }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < L; ++e) v[e] = load_rows(k[0] + ks + e);
+    }
+  }
+  // the three pieces into LDS: piece q of this operand starts at p0 + q * ROWS * kLDK
+  __device__ __forceinline__ void store(unsigned short* p0) const {
+    constexpr int P = ROWS * kLDK;
+    if constexpr (KC) {
+#pragma unroll
+      for (int j = 0; j < L; ++j) {
+        unsigned lo[3], hi[3];
+        split2(v[j][0], v[j][1], lo);
+        split2(v[j][2], v[j][3], hi);
+#pragma unroll
+        for (int q = 0; q < 3; ++q) *reinterpret_cast<u32x2*>(p0 + q * P + so[j]) = u32x2{lo[q], hi[q]};
+      }
+    } else if constexpr (L == 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        unsigned pc[3];
+        split2(v[0][i], v[1][i], pc);
+#pragma unroll
+        for (int q = 0; q < 3; ++q) *reinterpret_cast<unsigned*>(p0 + q * P + so[0] + i * kLDK) = pc[q];
+      }
+    } else {
+      const bool odd = threadIdx.x & 1;
+      // even lane (k even) keeps rows 0-1 and receives the odd lane's rows 0-1; the odd
+      // lane keeps rows 2-3 and receives the even lane's rows 2-3
+      const float x0 = swap_pair_lane(odd ? v[0][0] : v[0][2]);
+      const float x1 = swap_pair_lane(odd ? v[0][1] : v[0][3]);
+      const float a0 = odd ? x0 : v[0][0], b0 = odd ? v[0][2] : x0;
+      const float a1 = odd ? x1 : v[0][1], b1 = odd ? v[0][3] : x1;
+      unsigned p0c[3], p1c[3];
+      split2(a0, b0, p0c);
+      split2(a1, b1, p1c);
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        *reinterpret_cast<unsigned*>(p0 + q * P + so[0]) = p0c[q];
+        *reinterpret_cast<unsigned*>(p0 + q * P + so[0] + kLDK) = p1c[q];
       }
     }
   }
 };
 
-template <bool FULL>
+template <class S, bool FULL, bool AKC, bool BKC>
 __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigned short* sm) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave / kWN, wn = wave % kWN;
+  const int wm = wave / S::WN, wn = wave % S::WN;
   const int half = lane >> 5, r32 = lane & 31;
-  X6Operand<FULL> oa, ob;
-  oa.init(g.A, g.lda, m0, g.M, g.K);
-  ob.init(g.B, g.ldb, n0, g.N, g.K);
-  int so[kCh];  // LDS element offset of chunk j within one piece
-#pragma unroll
-  for (int j = 0; j < kCh; ++j) {
-    const int c = threadIdx.x + kThreads * j;
-    so[j] = (c / (kBK / 4)) * kLDK + (c % (kBK / 4)) * 4;
-  }
-  f4 ga[kCh], gb[kCh];
+  const int kbeg = blockIdx.z * g.kps;
+  const int kend = min(g.K, kbeg + g.kps);
+  X6Operand<FULL, AKC, S::BM> oa;
+  X6Operand<FULL, BKC, S::BN> ob;
+  oa.init(g.A, g.lda, m0, g.M, kbeg, kend);
+  ob.init(g.B, g.ldb, n0, g.N, kbeg, kend);
   auto store = [&](int buf) __attribute__((always_inline)) {
-    unsigned short* base = sm + buf * kBuf;
-#pragma unroll
-    for (int j = 0; j < kCh; ++j) {
-      u32x2 pa[3], pb[3];
-      split4(ga[j], pa);
-      split4(gb[j], pb);
-#pragma unroll
-      for (int q = 0; q < 3; ++q) {
-        *reinterpret_cast<u32x2*>(base + q * kPiece + so[j]) = pa[q];
-        *reinterpret_cast<u32x2*>(base + (3 + q) * kPiece + so[j]) = pb[q];
-      }
-    }
+    oa.store(sm + buf * S::BUF);
+    ob.store(sm + buf * S::BUF + 3 * S::PA);
   };
-  f16v acc[kFM][kFN];
+  f16v acc[S::FM][S::FN];
+  f16v tot[S::FOLD ? S::FM : 1][S::FOLD ? S::FN : 1];
 #pragma unroll
-  for (int i = 0; i < kFM; ++i)
+  for (int i = 0; i < S::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < kFN; ++j) acc[i][j] = f16v{};
+    for (int j = 0; j < S::FN; ++j) {
+      acc[i][j] = f16v{};
+      if constexpr (S::FOLD) tot[i][j] = f16v{};
+    }
 
-  const int nk = (g.K + kBK - 1) / kBK;
-  oa.load(ga, 0);
-  ob.load(gb, 0);
+  const int nk = (kend - kbeg + kBK - 1) / kBK;
+  oa.load(0);
+  ob.load(0);
   store(0);
-  oa.load(ga, min(1, nk - 1));
-  ob.load(gb, min(1, nk - 1));
+  oa.load(min(1, nk - 1));
+  ob.load(min(1, nk - 1));
   __syncthreads();
-  const int arow = (wm * kTM + r32) * kLDK + 8 * half, brow = (wn * kTN + r32) * kLDK + 8 * half;
+  const int arow = (wm * S::TM + r32) * kLDK + 8 * half, brow = (wn * S::TN + r32) * kLDK + 8 * half;
   for (int it = 0; it < nk; ++it) {
-    const unsigned short* base = sm + (it & 1) * kBuf;
-    u32x4 fa[3][kFM], fb[3][kFN];
+    const unsigned short* base = sm + (it & 1) * S::BUF;
+    u32x4 fa[3][S::FM], fb[3][S::FN];
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
 #pragma unroll
-      for (int i = 0; i < kFM; ++i)
-        fa[q][i] = *reinterpret_cast<const u32x4*>(base + q * kPiece + arow + 32 * i * kLDK);
+      for (int i = 0; i < S::FM; ++i)
+        fa[q][i] = *reinterpret_cast<const u32x4*>(base + q * S::PA + arow + 32 * i * kLDK);
 #pragma unroll
-      for (int j = 0; j < kFN; ++j)
-        fb[q][j] = *reinterpret_cast<const u32x4*>(base + (3 + q) * kPiece + brow + 32 * j * kLDK);
+      for (int j = 0; j < S::FN; ++j)
+        fb[q][j] = *reinterpret_cast<const u32x4*>(base + 3 * S::PA + q * S::PB + brow + 32 * j * kLDK);
     }
     // slice it+1 into the other buffer (its last reads were before the previous barrier)
     store((it & 1) ^ 1);
     const int nxt = min(it + 2, nk - 1);
-    oa.load(ga, nxt);
-    ob.load(gb, nxt);
+    oa.load(nxt);
+    ob.load(nxt);
 #pragma unroll
     for (int pp = 0; pp < 6; ++pp)
 #pragma unroll
-      for (int i = 0; i < kFM; ++i)
+      for (int i = 0; i < S::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < kFN; ++j) acc[i][j] = mfma_bf16(fa[kPa[pp]][i], fb[kPb[pp]][j], acc[i][j]);
+        for (int j = 0; j < S::FN; ++j) acc[i][j] = mfma_bf16(fa[kPa[pp]][i], fb[kPb[pp]][j], acc[i][j]);
     if constexpr (FULL) {
-      // fragment reads first, then the 48 products with the split and the LDS writes
-      // spread between them, then the next slice's loads
-      constexpr int kMfma = 6 * kFM * kFN, kWrites = 6 * kCh, kValu = 2 * 28 * kCh;
-      __builtin_amdgcn_sched_group_barrier(0x100, 3 * (kFM + kFN), 0);
+      // fragment reads first, then the products with the split and the LDS writes spread
+      // between them, then the next slice's loads
+      constexpr int kMfma = 6 * S::FM * S::FN;
+      constexpr int kWrites = X6Operand<FULL, AKC, S::BM>::kWrites + X6Operand<FULL, BKC, S::BN>::kWrites;
+      constexpr int kLoads = X6Operand<FULL, AKC, S::BM>::kLoads + X6Operand<FULL, BKC, S::BN>::kLoads;
+      constexpr int kValu = 28 * kLoads;
+      __builtin_amdgcn_sched_group_barrier(0x100, 3 * (S::FM + S::FN), 0);
 #pragma unroll
       for (int w = 0; w < kWrites; ++w) {
-        __builtin_amdgcn_sched_group_barrier(0x008, kMfma / kWrites, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, kValu / kWrites, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, (kMfma + kWrites - 1) / kWrites, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, (kValu + kWrites - 1) / kWrites, 0);
         __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x020, 2 * kCh, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, kLoads, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
     }
     __syncthreads();
+    if constexpr (S::FOLD) {
+      if ((it + 1) % S::FOLD == 0 || it + 1 == nk) {
+#pragma unroll
+        for (int i = 0; i < S::FM; ++i)
+#pragma unroll
+          for (int j = 0; j < S::FN; ++j) {
+            tot[i][j] += acc[i][j];
+            acc[i][j] = f16v{};
+          }
+      }
+    }
   }
 
+  float* outp = g.partial ? g.out + (size_t)blockIdx.z * g.M * g.N : g.out;
+  const int ldo = g.partial ? g.N : g.ldc;
 #pragma unroll
-  for (int i = 0; i < kFM; ++i)
+  for (int i = 0; i < S::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < kFN; ++j) {
-      const int n = n0 + wn * kTN + j * 32 + r32;
+    for (int j = 0; j < S::FN; ++j) {
+      const int n = n0 + wn * S::TN + j * 32 + r32;
       if (!FULL && n >= g.N) continue;
-      const float bval = g.bias ? g.bias[n] : 0.f;
+      const float bval = (!g.partial && g.bias) ? g.bias[n] : 0.f;
+      const f16v& res = S::FOLD ? tot[S::FOLD ? i : 0][S::FOLD ? j : 0] : acc[i][j];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * kTM + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        if (FULL || m < g.M) g.C[(size_t)m * g.ldc + n] = acc[i][j][r] + bval;
+        const int m = m0 + wm * S::TM + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (FULL || m < g.M) outp[(size_t)m * ldo + n] = res[r] + bval;
       }
     }
 }
 
-// FULL: every tile lies inside the matrices (M, N multiples of 256, K of 16, aligned
-// operands); chosen per launch, so the unmasked kernel carries no edge code.
-template <bool FULL>
+// FULL: every tile lies inside the matrices and every split is a whole number of slices
+// (M, N multiples of the tile, K and the split length of 16, aligned operands); chosen
+// per launch, so the unmasked kernel carries no edge code.  AKC / BKC: operand k-contiguous.
+template <class S, bool FULL, bool AKC, bool BKC>
 __global__ __launch_bounds__(kThreads) void gemm_x6_kernel(X6Args g) {
   extern __shared__ unsigned short x6_smem[];
   int tm, tn;
   gemm_tile_order(g.tiles_m, g.tiles_n, &tm, &tn);
-  x6_tile<FULL>(g, tm * kBT, tn * kBT, x6_smem);
+  x6_tile<S, FULL, AKC, BKC>(g, tm * S::BM, tn * S::BN, x6_smem);
+}
+
+template <class S, bool AKC, bool BKC>
+void x6_launch(X6Args g, bool vec, int splits, hipStream_t s) {
+  g.tiles_m = (g.M + S::BM - 1) / S::BM;
+  g.tiles_n = (g.N + S::BN - 1) / S::BN;
+  const bool full = vec && g.M % S::BM == 0 && g.N % S::BN == 0 && g.K % kBK == 0 && g.kps % kBK == 0;
+  const dim3 grid(g.tiles_m * g.tiles_n, 1, splits);
+  if (full)
+    hipLaunchKernelGGL((gemm_x6_kernel<S, true, AKC, BKC>), grid, dim3(kThreads), S::LDS, s, g);
+  else
+    hipLaunchKernelGGL((gemm_x6_kernel<S, false, AKC, BKC>), grid, dim3(kThreads), S::LDS, s, g);
 }
 
 }  // namespace
 
 bool gemm_x6_applies(int M, int N, int K) {
   // one 256 x 256 tile per CU at least, and enough k to amortise the tile's setup
-  const long tiles = (long)((M + kBT - 1) / kBT) * ((N + kBT - 1) / kBT);
+  const long tiles = (long)((M + ShapeProj::BM - 1) / ShapeProj::BM) * ((N + ShapeProj::BN - 1) / ShapeProj::BN);
   return tiles >= 256 && K >= 32;
 }
 
-int gemm_x6_run(const float* A, const float* B, const float* bias, float* C, int M, int N, int K, int lda, int ldb,
-                int ldc, hipStream_t s) {
+int gemm_x6_tn_splits(int M, int N, int K) {
+  // C = A^T B (weight gradients, K = T*B): at least one tile each way and >= 8 GFLOP.
+  // Splits fill the chip (one workgroup per CU) and keep every split to at most kTnRun k,
+  // summed inside the kernel as fp32 runs of 64 k (FOLD); the planes are added in fp64.
+  using S = ShapeWgrad;
+  if (M < S::BM || N < S::BN || K < 2 * kBK || 2.0 * M * N * K < 8e9) return 0;
+  const long tiles = (long)((M + S::BM - 1) / S::BM) * ((N + S::BN - 1) / S::BN);
+  long s = (256 + tiles - 1) / tiles;
+  const long by_run = (K + kTnRun - 1) / kTnRun;
+  if (by_run > s) s = by_run;
+  if (s > K / kBK) s = K / kBK;
+  if (s > 64) s = 64;
+  return s < 1 ? 1 : (int)s;
+}
+
+int gemm_x6_run(const float* A, const float* B, const float* bias, float* C, float* partial, int M, int N, int K,
+                int lda, int ldb, int ldc, int trans_a, int trans_b, int splits, hipStream_t s, int* used) {
   if (M <= 0 || N <= 0 || K <= 0) return fail(HSL_ERR_ARG, "gemm_x6: empty product");
+  if (trans_b == trans_a) return fail(HSL_ERR_ARG, "gemm_x6: layout not supported");
+  if (splits < 1 || (splits > 1 && !partial)) splits = 1;
   X6Args g{};
   g.A = A;
   g.B = B;
-  g.bias = bias;
-  g.C = C;
+  g.bias = partial ? nullptr : bias;
+  g.out = partial ? partial : C;
+  g.partial = partial ? 1 : 0;
   g.M = M;
   g.N = N;
   g.K = K;
   g.lda = lda;
   g.ldb = ldb;
   g.ldc = ldc;
-  g.vec = aligned16(A) && aligned16(B) && lda % 4 == 0 && ldb % 4 == 0;
-  g.tiles_m = (M + kBT - 1) / kBT;
-  g.tiles_n = (N + kBT - 1) / kBT;
-  const bool full = g.vec && M % kBT == 0 && N % kBT == 0 && K % kBK == 0;
-  if (full)
-    hipLaunchKernelGGL(gemm_x6_kernel<true>, dim3(g.tiles_m * g.tiles_n), dim3(kThreads), kLdsBytes, s, g);
+  int kps = (K + splits - 1) / splits;
+  kps = (kps + kBK - 1) / kBK * kBK;
+  g.kps = kps;
+  const int n = (K + kps - 1) / kps;
+  if (used) *used = n;
+  const bool vec = aligned16(A) && aligned16(B) && lda % 4 == 0 && ldb % 4 == 0;
+  if (!trans_a && trans_b)
+    x6_launch<ShapeProj, true, true>(g, vec, n, s);  // x W^T: both operands k-contiguous
   else
-    hipLaunchKernelGGL(gemm_x6_kernel<false>, dim3(g.tiles_m * g.tiles_n), dim3(kThreads), kLdsBytes, s, g);
+    x6_launch<ShapeWgrad, false, false>(g, vec, n, s);  // A^T B: both row-contiguous
   HSL_HIP(hipGetLastError());
   return HSL_OK;
 }

@@ -73,6 +73,7 @@ struct GemmDesc {
   int trans_a, trans_b;
   int acc64;  // 1: fp64 accumulation across BK-slices (long K reductions)
 };
+size_t gemm_ws_bytes_layout(int M, int N, int K, int acc64, int trans_a, int trans_b);
 size_t gemm_ws_bytes(int M, int N, int K, int acc64);
 // Full product with optional split-K through ws (ws may be null when ws_bytes==0).
 int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s);
@@ -80,15 +81,20 @@ int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s);
 // planes); *used receives the number of planes written (<= splits).  Used by the
 // fused epilogues of the weight gradients.
 int gemm_partials(const GemmDesc& d, float* partials, int splits, hipStream_t s, int* used);
+// Partial planes to provide for an A^T B product given to gemm_partials (fp32 or split-bf16).
+int gemm_tn_planes(int M, int N, int K);
 // C[M][N] (row stride ldc) = sum over the `splits` fp32 planes P[z][M][N], added in fp64
 // (+ bias[N] when non-null).
 int splitk_reduce(const float* P, int splits, const float* bias, float* C, int M, int N, int ldc, hipStream_t s);
 int gemm_pick_splits(int M, int N, int K, int acc64);
 // C[M][N] = A[M][K] . B[N][K]^T (+ bias[N]) with 16-bit A and B (fmt 0 bf16, 1 fp16),
 // fp32 accumulation and output (gemm_b16.hip).
-bool gemm_x6_applies(int M, int N, int K);
-int gemm_x6_run(const float* A, const float* B, const float* bias, float* C, int M, int N, int K, int lda, int ldb,
-                int ldc, hipStream_t s);
+bool gemm_x6_applies(int M, int N, int K);  // C = A B^T products (input projection)
+int gemm_x6_tn_splits(int M, int N, int K);  // C = A^T B: split count, 0 = not taken
+// Split-bf16 product (gemm_x6.hip): trans_a = 0, trans_b = 1 or trans_a = 1, trans_b = 0;
+// with partial != nullptr the k-splits go to planes [used][M][N] (no bias).
+int gemm_x6_run(const float* A, const float* B, const float* bias, float* C, float* partial, int M, int N, int K,
+                int lda, int ldb, int ldc, int trans_a, int trans_b, int splits, hipStream_t s, int* used);
 int gemm_b16_run(const void* A, const void* B, const float* bias, float* C, int M, int N, int K, int lda, int ldb,
                  int ldc, int fmt, hipStream_t s);
 

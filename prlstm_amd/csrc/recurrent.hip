@@ -22,6 +22,7 @@
 // v_mfma_f32_4x4x1_16b_f32 layout (verified on gfx950): A from lane 4b+i is
 // A_b[i][0], B from lane 4b+j is B_b[0][j], result lane 4b+j, reg i holds D_b[i][j].
 // With cbsz=4, abid=0 every block uses block 0's A (lanes 0-3).
+#include <algorithm>
 #include <cstdlib>
 #include <type_traits>
 
@@ -1588,9 +1589,9 @@ struct BwdWs {
 
 size_t gemm_region_bytes(int T, int B, int D, int H) {
   const int TB = T * B;
-  const int s4 = gemm_pick_splits(4 * H, H, TB, 1);
+  const int s4 = gemm_tn_planes(4 * H, H, TB);
   size_t need = sizeof(float) * (size_t)s4 * 4 * H * H;  // dW_hh partials (always staged)
-  const size_t g5 = gemm_ws_bytes(4 * H, D, TB, 1);
+  const size_t g5 = gemm_ws_bytes_layout(4 * H, D, TB, 1, 1, 0);
   const size_t g6 = gemm_ws_bytes(TB, D, 4 * H, 1);
   if (g5 > need) need = g5;
   if (g6 > need) need = g6;
@@ -1896,7 +1897,10 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
   int splits = nsplit;
   if (!fused) {
     GemmDesc g4{w.dgates, h_save, nullptr, w.gemm, 4 * H, H, TB, 4 * H, H, H, 1, 0, 1};
-    HSL_CHECK(gemm_partials(g4, w.gemm, gemm_pick_splits(4 * H, H, TB, 1), s, &splits));
+    // as many planes as asked for and as the region holds (the mode may have changed
+    // since the workspace was sized)
+    const int fit = (int)std::min<size_t>(w.gemm_bytes / (sizeof(float) * (size_t)4 * H * H), 1 << 20);
+    HSL_CHECK(gemm_partials(g4, w.gemm, std::max(1, std::min(gemm_tn_planes(4 * H, H, TB), fit)), s, &splits));
   }
   {  // dW_hh (and the fused dW_ih planes in extra blocks of the same launch)
     const size_t xn = fused_ih ? (size_t)4 * H * D : 0;

@@ -291,7 +291,7 @@ size_t carve_par(void* ws, size_t cap, int T, int B, int D, int H, ParWs* o) {
   Carver c(ws, cap);
   o->dgates = c.take<float>((size_t)T * B * 4 * H);
   o->db_part = c.take<double>((size_t)B * 4 * H);
-  size_t g = gemm_ws_bytes(4 * H, D, T * B, 1);
+  size_t g = gemm_ws_bytes_layout(4 * H, D, T * B, 1, 1, 0);
   const size_t g6 = gemm_ws_bytes(T * B, D, 4 * H, 1);
   if (g6 > g) g = g6;
   o->gemm_bytes = g;

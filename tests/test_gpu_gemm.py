@@ -78,16 +78,19 @@ def split_products():
     _lib.set_split_products(prev)
 
 
-def _both(A, B, bias, M, N, K, lda=None, ldb=None):
-    """C = A B^T (+bias) by the split-bf16 kernel and by the fp32 MFMA kernel."""
+def _both(A, B, bias, M, N, K, lda=None, ldb=None, ta=0, tb=1):
+    """C = op(A) op(B) (+bias) by the split-bf16 kernel and by the fp32 MFMA kernel
+    (A B^T by default; ta=1, tb=0 for A^T B, with the workspace hsl_gemm_ws_bytes asks)."""
     dev = A.device
     out = []
+    nbytes = _lib.load().hsl_gemm_ws_bytes(M, N, K)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     for on in (1, 0):
         _lib.set_split_products(on)
         C = torch.empty(M, N, device=dev)
         P = _lib.ptr
-        _lib.call("hsl_gemm_f32", P(A), P(B), P(bias), P(C), M, N, K, lda or K, ldb or K, N, 0, 1,
-                  None, 0, _lib.stream_of(dev))
+        _lib.call("hsl_gemm_f32", P(A), P(B), P(bias), P(C), M, N, K, lda or A.shape[1], ldb or B.shape[1], N,
+                  ta, tb, P(ws), nbytes, _lib.stream_of(dev))
         out.append(C.cpu().double())
     _lib.set_split_products(1)
     return out
@@ -150,3 +153,27 @@ def test_split_products_non_finite(dev, split_products):
     assert bool(torch.isposinf(c32[3, :17]).all()) and bool(torch.isneginf(c32[700, :17]).all())
     assert bool(torch.isnan(c32[1200]).all()) and bool(torch.isinf(c32[5:10, 17]).all())
     assert torch.equal(torch.sign(c32[5:10, 17]), torch.sign(a[5:10, 2]).double())
+
+
+@pytest.mark.parametrize("M,N,K,pad", [(4096, 256, 65536, 0), (2048, 512, 8192, 0), (1000, 300, 20000, 3)])
+def test_split_products_weight_gradient_layout(dev, split_products, M, N, K, pad):
+    """C = A^T B over a long K (the weight gradients dgates^T x, K = T*B): the split-bf16
+    kernel runs it as fp32 runs of at most 2048 k added in fp64; against the fp64 product
+    it must meet the fp32 bound and match the fp32 kernel's error (rows sampled)."""
+    print(f"split products A^T B M={M} N={N} K={K} pad={pad}", flush=True)
+    g = torch.Generator().manual_seed(M + 3 * N + K)
+    a = torch.randn(K, M + pad, generator=g) * 0.05   # dgates-like [K, M]
+    b = torch.randn(K, N + pad, generator=g)          # x-like [K, N]
+    cx6, c32 = _both(a.to(dev), b.to(dev), None, M, N, K, ta=1, tb=0)
+    assert not torch.equal(cx6, c32)
+    rows = torch.arange(0, M, 41)
+    av, bv = a[:, rows].double(), b[:, :N].double()
+    ref = av.t() @ bv
+    scale = av.abs().t() @ bv.abs()
+    ex6 = (cx6[rows] - ref).abs() / scale
+    e32 = (c32[rows] - ref).abs() / scale
+    print(f"  rel err x6 max {ex6.max():.3e} rms {ex6.pow(2).mean().sqrt():.3e}; "
+          f"fp32 max {e32.max():.3e} rms {e32.pow(2).mean().sqrt():.3e}", flush=True)
+    assert float(ex6.max()) <= 2e-6 * K ** 0.5
+    assert float(ex6.pow(2).mean().sqrt()) <= 1.25 * float(e32.pow(2).mean().sqrt()) + 1e-12
+    assert float(ex6.max()) <= 2.0 * float(e32.max()) + 1e-12

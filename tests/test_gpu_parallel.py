@@ -13,7 +13,7 @@ gate pre-activations, and the input projection on a random subset of rows.
 import pytest
 import torch
 
-from conftest import assert_close64, lim_ratio
+from conftest import assert_close64, assert_parity, lim_ratio
 from oracle import hsl_oracle as O
 import prlstm_amd
 from prlstm_amd import _lib
@@ -206,8 +206,8 @@ def test_config4_full_size_subsets(dev):
 
 
 def test_config4_module_step_runs_and_grads_are_finite(dev):
-    """Full configs[4] training step through the module (fwd+bwd), finiteness and
-    the dW_ih = dgates^T x identity on a few rows are checked."""
+    """Full configs[4] training step through the module (fwd+bwd): every output and
+    gradient is finite (the values are checked by the tests above and below)."""
     T, B, D, H = 4096, 16, 256, 1024
     torch.manual_seed(0)
     m = prlstm_amd.HeadStartLSTM(D, H, a_init=0.0, parallel=True).to(dev)
@@ -217,3 +217,49 @@ def test_config4_module_step_runs_and_grads_are_finite(dev):
     for t in (out, m.weight_ih_l0.grad, m.bias_ih_l0.grad, x.grad):
         assert torch.isfinite(t).all()
     assert m.weight_hh_l0.grad is None
+
+
+def test_config4_weight_gradient_full_size(dev):
+    """configs[4] dW_ih = dgates^T x over K = T*B = 65536 (hsl_par_bwd), on sampled rows of
+    the same dgates (from hsl_scan_bwd) and x.  fp32 arithmetic cannot meet rtol 1e-4 /
+    atol 1e-5 of the exact sum on its own at this K (the CPU's fp32 product of the same
+    operands is itself outside it), so the bar is the parity policy of the recurrent
+    tests: within tolerance of the CPU fp32 product, or at least as close to the fp64
+    product as the CPU is."""
+    T, B, D, H = 4096, 16, 256, 1024
+    print(f"parallel configs[4] dW_ih T={T} B={B} D={D} H={H}", flush=True)
+    torch.manual_seed(0)
+    ref = O.RefHeadStartLSTM(D, H, a_init=0.0)
+    x = torch.randn(T, B, D)
+    xd = x.to(dev)
+    c0 = torch.zeros(B, H, device=dev)
+    w_ih = ref.weight_ih_l0.detach().to(dev)
+    b_ih = ref.bias_ih_l0.detach().to(dev)
+    gates, out, c_seq = _par_fwd(xd, c0, w_ih, b_ih, T, B, D, H)
+    g = torch.Generator().manual_seed(2)
+    dout = torch.randn(T, B, H, generator=g).to(dev)
+    dh_n = torch.zeros(B, H, device=dev)
+    dc_n = torch.zeros(B, H, device=dev)
+    P, s = _lib.ptr, _lib.stream_of(dev)
+    dgates = torch.empty(T, B, 4 * H, device=dev)
+    db_part = torch.empty(B, 4 * H, dtype=torch.float64, device=dev)
+    _lib.call("hsl_scan_bwd", P(gates), P(c0), P(c_seq), P(dout), P(dh_n), P(dc_n), 1e-6,
+              P(dgates), P(db_part), None, T, B, H, s)
+    nbytes = _lib.load().hsl_par_bwd_ws_bytes(T, B, D, H)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    dw = torch.empty(4 * H, D, device=dev)
+    db = torch.empty(4 * H, device=dev)
+    _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(xd), P(c0), P(gates), P(c_seq), P(w_ih), 1e-6,
+              None, P(dw), P(db), None, P(ws), nbytes, T, B, D, H, s)
+    torch.cuda.synchronize()
+    rows = torch.arange(0, 4 * H, 29)
+    dg = dgates.view(T * B, 4 * H)[:, rows.to(dev)].cpu()
+    xs = x.view(T * B, D)
+    want = dg.double().t() @ xs.double()
+    cpu32 = dg.t() @ xs
+    got = dw[rows.to(dev)].cpu()
+    print(f"  dW_ih rows {len(rows)}: gpu {lim_ratio(got, want, RTOL, ATOL):.3g}x, "
+          f"cpu fp32 {lim_ratio(cpu32, want, RTOL, ATOL):.3g}x of the tolerance vs fp64", flush=True)
+    assert_parity("dW_ih", got, cpu32, want, RTOL, ATOL)
+    want_db = dg.double().sum(0)
+    assert lim_ratio(db[rows.to(dev)].cpu().double(), want_db, RTOL, ATOL) <= 1.0

@@ -68,9 +68,10 @@ int hsl_set_exchange_scope(int mode);
  * products accumulated in fp32 (error that of the fp32 MFMA product):
  *  - C = A B^T (+bias) with at least 256 output tiles of 256 x 256: the input
  *    projection x W_ih^T + b_ih (_torch.py:96, _parallel.py:56);
- *  - C = A^T B of at least 8 GFLOP with both sides >= 256: the weight gradients
- *    (_torch.py:157-162), split along K into fp32 runs of at most 2048 k that are
- *    added in fp64 (workspace permitting; otherwise the fp32 kernel runs).
+ *  - C = A^T B and C = A B of at least 8 GFLOP with M >= 256, N >= 128: the weight
+ *    gradients and dx (_torch.py:157-162), as fp32 runs of 64 k folded into a second
+ *    fp32 sum, split along K into planes of at most 2048 k added in fp64 (workspace
+ *    permitting; otherwise the fp32 kernel runs).
  * on = 0 uses the fp32 MFMA instruction for every product.  With
  * on = 1 a non-finite element of A (or one beyond the bf16 range, 3.3895e38) makes
  * its row of C NaN and one of B its column, where the fp32 instruction would give

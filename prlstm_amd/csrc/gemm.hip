@@ -1,7 +1,8 @@
 // hsl_gemm_f32: fp32 MFMA GEMM entry point with optional split-K.
 //
 // Large C = A B^T products (at least 256 tiles of 256 x 256, no fp64 folding) and large
-// C = A^T B weight gradients (>= 8 GFLOP, split into fp32 runs of <= 2048 k added in fp64)
+// C = A^T B / A B products (weight gradients and dx, >= 8 GFLOP, split into fp32 runs of
+// <= 2048 k added in fp64)
 // run on the split-bf16 kernel of gemm_x6.hip (fp32 accuracy, 2.5x the matrix-core rate)
 // unless hsl_set_split_products(0) selects the fp32 instruction for everything.
 // Products with M, N >= 64 run on the third core (gemm3_core.h): 128x256, 128x128 or
@@ -169,11 +170,11 @@ size_t gemm_ws_bytes(int M, int N, int K, int acc64) {
 }
 
 namespace {
-// Split count of the split-bf16 A^T B kernel for this product when it is taken with at
+// Split count of the split-bf16 A^T B / A B kernel for this product when it is taken with at
 // most `max_planes` partial planes (0: not taken, because split products are off, the
 // product is small, or the planes would leave fp32 running sums longer than 2048 k).
 int x6_tn_take(const GemmDesc& d, long max_planes) {
-  if (!d.trans_a || d.trans_b || !split_products_mode()) return 0;
+  if (d.trans_b || !split_products_mode()) return 0;  // A^T B or A B
   int s = gemm_x6_tn_splits(d.M, d.N, d.K);
   if (s <= 0) return 0;
   if (s > max_planes) s = (int)max_planes;
@@ -184,7 +185,7 @@ int x6_tn_take(const GemmDesc& d, long max_planes) {
 
 size_t gemm_ws_bytes_layout(int M, int N, int K, int acc64, int trans_a, int trans_b) {
   size_t need = gemm_ws_bytes(M, N, K, acc64);
-  if (trans_a && !trans_b && split_products_mode()) {
+  if (!trans_b && split_products_mode()) {
     const int s = gemm_x6_tn_splits(M, N, K);
     if (s > 1) need = std::max(need, sizeof(float) * (size_t)s * M * N);
   }
@@ -200,7 +201,8 @@ int gemm_tn_planes(int M, int N, int K) {
 int gemm_partials(const GemmDesc& d, float* partials, int splits, hipStream_t s, int* used) {
   HSL_CHECK(check_desc(d));
   if (const int sx = x6_tn_take(d, splits))
-    return gemm_x6_run(d.A, d.B, nullptr, nullptr, partials, d.M, d.N, d.K, d.lda, d.ldb, d.N, 1, 0, sx, s, used);
+    return gemm_x6_run(d.A, d.B, nullptr, nullptr, partials, d.M, d.N, d.K, d.lda, d.ldb, d.N, d.trans_a, 0, sx, s,
+                       used);
   return dispatch(pick_tile(d.M, d.N, d.acc64), d, partials, std::min(splits, gemm_pick_splits(d.M, d.N, d.K, d.acc64)), s,
                   used);
 }
@@ -214,10 +216,11 @@ int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s) {
   const long planes = ws ? (long)(ws_bytes / (sizeof(float) * (size_t)d.M * d.N)) : 0;
   if (const int sx = x6_tn_take(d, planes > 1 ? planes : 1)) {
     if (sx == 1)
-      return gemm_x6_run(d.A, d.B, d.bias, d.C, nullptr, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, 1, 0, 1, s, nullptr);
+      return gemm_x6_run(d.A, d.B, d.bias, d.C, nullptr, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, d.trans_a, 0, 1, s,
+                         nullptr);
     float* P = static_cast<float*>(ws);
     int used = 1;
-    HSL_CHECK(gemm_x6_run(d.A, d.B, nullptr, nullptr, P, d.M, d.N, d.K, d.lda, d.ldb, d.N, 1, 0, sx, s, &used));
+    HSL_CHECK(gemm_x6_run(d.A, d.B, nullptr, nullptr, P, d.M, d.N, d.K, d.lda, d.ldb, d.N, d.trans_a, 0, sx, s, &used));
     return splitk_reduce(P, used, d.bias, d.C, d.M, d.N, d.ldc, s);
   }
   const Tile t = pick_tile(d.M, d.N, d.acc64);

@@ -2,10 +2,12 @@
 //  * C[M,N] = A[M,K] . B[N,K]^T (+ bias[N]): the input projection x W_ih^T + b_ih
 //    (_torch.py:96, _parallel.py:56) of parallel mode and of the per-step path;
 //  * C[M,N] = A[K,M]^T . B[K,N]: the weight gradients dgates^T h and dgates^T x over
-//    K = T*B (_torch.py:157-162, and autograd's in parallel mode), split along K into fp32
-//    partial planes of at most 2048 k each that are added in fp64 (splitk_reduce, or the
-//    caller's own fp64 finalisation) -- the accuracy that the fp32 kernel gets from folding
-//    its accumulators into fp64 registers, which the 8-wave tile has no room for.
+//    K = T*B (_torch.py:157-162, and autograd's in parallel mode), and C[M,N] = A[M,K] .
+//    B[K,N]: dx = dgates W_ih (K = 4H); both summed as fp32 runs of 64 k folded into a
+//    second fp32 accumulator, split along K into planes of at most 2048 k each that are
+//    added in fp64 (splitk_reduce, or the caller's own fp64 finalisation) -- the accuracy
+//    that the fp32 kernel gets from folding its accumulators into fp64 registers, which the
+//    8-wave tile has no room for.
 //
 // Exact three-way split.  Each fp32 value v is written as v = v0 + v1 + v2 with bf16
 // pieces v0 = bf16(v) (round to nearest even), v1 = bf16(v - v0), v2 = v - v0 - v1.  The
@@ -377,7 +379,8 @@ bool gemm_x6_applies(int M, int N, int K) {
 }
 
 int gemm_x6_tn_splits(int M, int N, int K) {
-  // C = A^T B (weight gradients, K = T*B): at least one tile each way and >= 8 GFLOP.
+  // C = A^T B (weight gradients, K = T*B) or C = A B (dx = dgates W_ih, K = 4H): at least
+  // one tile each way and >= 8 GFLOP.
   // Splits fill the chip (one workgroup per CU) and keep every split to at most kTnRun k,
   // summed inside the kernel as fp32 runs of 64 k (FOLD); the planes are added in fp64.
   using S = ShapeWgrad;
@@ -394,7 +397,7 @@ int gemm_x6_tn_splits(int M, int N, int K) {
 int gemm_x6_run(const float* A, const float* B, const float* bias, float* C, float* partial, int M, int N, int K,
                 int lda, int ldb, int ldc, int trans_a, int trans_b, int splits, hipStream_t s, int* used) {
   if (M <= 0 || N <= 0 || K <= 0) return fail(HSL_ERR_ARG, "gemm_x6: empty product");
-  if (trans_b == trans_a) return fail(HSL_ERR_ARG, "gemm_x6: layout not supported");
+  if (trans_a && trans_b) return fail(HSL_ERR_ARG, "gemm_x6: layout not supported");
   if (splits < 1 || (splits > 1 && !partial)) splits = 1;
   X6Args g{};
   g.A = A;
@@ -416,8 +419,10 @@ int gemm_x6_run(const float* A, const float* B, const float* bias, float* C, flo
   const bool vec = aligned16(A) && aligned16(B) && lda % 4 == 0 && ldb % 4 == 0;
   if (!trans_a && trans_b)
     x6_launch<ShapeProj, true, true>(g, vec, n, s);  // x W^T: both operands k-contiguous
-  else
+  else if (trans_a)
     x6_launch<ShapeWgrad, false, false>(g, vec, n, s);  // A^T B: both row-contiguous
+  else
+    x6_launch<ShapeWgrad, true, false>(g, vec, n, s);  // A B (dx = dgates W_ih): B row-contiguous
   HSL_HIP(hipGetLastError());
   return HSL_OK;
 }

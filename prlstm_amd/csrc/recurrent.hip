@@ -1592,7 +1592,7 @@ size_t gemm_region_bytes(int T, int B, int D, int H) {
   const int s4 = gemm_tn_planes(4 * H, H, TB);
   size_t need = sizeof(float) * (size_t)s4 * 4 * H * H;  // dW_hh partials (always staged)
   const size_t g5 = gemm_ws_bytes_layout(4 * H, D, TB, 1, 1, 0);
-  const size_t g6 = gemm_ws_bytes(TB, D, 4 * H, 1);
+  const size_t g6 = gemm_ws_bytes_layout(TB, D, 4 * H, 1, 0, 0);
   if (g5 > need) need = g5;
   if (g6 > need) need = g6;
   const size_t g7 = gemm_ws_bytes(B, H, 4 * H, 1);

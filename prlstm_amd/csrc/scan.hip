@@ -292,7 +292,7 @@ size_t carve_par(void* ws, size_t cap, int T, int B, int D, int H, ParWs* o) {
   o->dgates = c.take<float>((size_t)T * B * 4 * H);
   o->db_part = c.take<double>((size_t)B * 4 * H);
   size_t g = gemm_ws_bytes_layout(4 * H, D, T * B, 1, 1, 0);
-  const size_t g6 = gemm_ws_bytes(T * B, D, 4 * H, 1);
+  const size_t g6 = gemm_ws_bytes_layout(T * B, D, 4 * H, 1, 0, 0);
   if (g6 > g) g = g6;
   o->gemm_bytes = g;
   o->gemm = c.take<float>(g / sizeof(float) + 1);

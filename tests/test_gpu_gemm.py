@@ -155,21 +155,28 @@ def test_split_products_non_finite(dev, split_products):
     assert torch.equal(torch.sign(c32[5:10, 17]), torch.sign(a[5:10, 2]).double())
 
 
-@pytest.mark.parametrize("M,N,K,pad", [(4096, 256, 65536, 0), (2048, 512, 8192, 0), (1000, 300, 20000, 3)])
-def test_split_products_weight_gradient_layout(dev, split_products, M, N, K, pad):
-    """C = A^T B over a long K (the weight gradients dgates^T x, K = T*B): the split-bf16
-    kernel runs it as fp32 runs of at most 2048 k added in fp64; against the fp64 product
-    it must meet the fp32 bound and match the fp32 kernel's error (rows sampled)."""
-    print(f"split products A^T B M={M} N={N} K={K} pad={pad}", flush=True)
-    g = torch.Generator().manual_seed(M + 3 * N + K)
-    a = torch.randn(K, M + pad, generator=g) * 0.05   # dgates-like [K, M]
-    b = torch.randn(K, N + pad, generator=g)          # x-like [K, N]
-    cx6, c32 = _both(a.to(dev), b.to(dev), None, M, N, K, ta=1, tb=0)
+@pytest.mark.parametrize("M,N,K,pad,ta", [(4096, 256, 65536, 0, 1), (2048, 512, 8192, 0, 1), (1000, 300, 20000, 3, 1),
+                                          (65536, 256, 4096, 0, 0), (2048, 1024, 8192, 0, 0), (3000, 300, 5000, 1, 0)])
+def test_split_products_weight_gradient_layout(dev, split_products, M, N, K, pad, ta):
+    """C = A^T B over a long K (the weight gradients dgates^T x, K = T*B) and C = A B
+    (dx = dgates W_ih, K = 4H): the split-bf16 kernel sums fp32 runs of 64 k into a second
+    fp32 accumulator and splits K into planes of at most 2048 k added in fp64; against the
+    fp64 product it must meet the fp32 bound and match the fp32 kernel's error (rows
+    sampled)."""
+    print(f"split products {'A^T B' if ta else 'A B'} M={M} N={N} K={K} pad={pad}", flush=True)
+    g = torch.Generator().manual_seed(M + 3 * N + K + ta)
+    if ta:
+        a = torch.randn(K, M + pad, generator=g) * 0.05   # dgates-like [K, M]
+    else:
+        a = torch.randn(M, K + pad, generator=g) * 0.05   # dgates-like [M, K]
+    b = torch.randn(K, N + pad, generator=g)              # [K, N]
+    cx6, c32 = _both(a.to(dev), b.to(dev), None, M, N, K, ta=ta, tb=0)
     assert not torch.equal(cx6, c32)
-    rows = torch.arange(0, M, 41)
-    av, bv = a[:, rows].double(), b[:, :N].double()
-    ref = av.t() @ bv
-    scale = av.abs().t() @ bv.abs()
+    rows = torch.arange(0, M, max(1, M // 100))
+    av = (a[:, rows].t() if ta else a[rows, :K]).double()
+    bv = b[:, :N].double()
+    ref = av @ bv
+    scale = av.abs() @ bv.abs()
     ex6 = (cx6[rows] - ref).abs() / scale
     e32 = (c32[rows] - ref).abs() / scale
     print(f"  rel err x6 max {ex6.max():.3e} rms {ex6.pow(2).mean().sqrt():.3e}; "

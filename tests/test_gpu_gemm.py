@@ -184,3 +184,47 @@ def test_split_products_weight_gradient_layout(dev, split_products, M, N, K, pad
     assert float(ex6.max()) <= 2e-6 * K ** 0.5
     assert float(ex6.pow(2).mean().sqrt()) <= 1.25 * float(e32.pow(2).mean().sqrt()) + 1e-12
     assert float(ex6.max()) <= 2.0 * float(e32.max()) + 1e-12
+
+
+@pytest.mark.parametrize("layout", ["abt", "atb", "ab"])
+@pytest.mark.parametrize("three_piece", ["a", "b"])
+def test_split_products_exact_on_representable_sums(dev, split_products, layout, three_piece):
+    """Pins the piece bookkeeping of the split-bf16 kernels by exact arithmetic.  One
+    operand holds values m * 2^-16 with |m| < 2^18 (three non-zero bf16 pieces in
+    general), the other +-1 (one piece), and only 32 k-values are non-zero.  Every piece
+    product that is kept then enters exactly, every partial sum is a multiple of 2^-16
+    below 2^7 in magnitude, which fp32 represents exactly, so the result must equal the
+    exact sum bit for bit: a wrong, swapped or missing piece changes it.  The long-K
+    layouts (A^T B, A B) run over K = 8192 (their size rule) with the 32 non-zero k in one
+    band, which also exercises their k-splits and the fp64 sum of the planes."""
+    g = torch.Generator().manual_seed(len(layout) * 7 + (three_piece == "a"))
+
+    def fine(*shape):
+        return torch.randint(-(1 << 18) + 1, 1 << 18, shape, generator=g).double() * 2.0 ** -16
+
+    def sign(*shape):
+        return torch.randint(0, 2, shape, generator=g).double() * 2 - 1
+
+    def pair(shape_a, shape_b):
+        return (fine(*shape_a), sign(*shape_b)) if three_piece == "a" else (sign(*shape_a), fine(*shape_b))
+
+    if layout == "abt":  # C = A B^T, A [M,K], B [N,K]
+        M, N, K = 4096, 4096, 32
+        a, b = pair((M, K), (N, K))
+        exact, ta = a @ b.t(), 0
+    else:
+        M, N, K = 4096, 256, 8192
+        band = torch.zeros(K, dtype=torch.double)
+        band[1024:1056] = 1.0
+        if layout == "atb":  # C = A^T B, A [K,M], B [K,N]
+            a, b = pair((K, M), (K, N))
+            a, b = a * band[:, None], b * band[:, None]
+            exact, ta = a.t() @ b, 1
+        else:  # C = A B, A [M,K], B [K,N]
+            a, b = pair((M, K), (K, N))
+            a, b = a * band[None, :], b * band[:, None]
+            exact, ta = a @ b, 0
+    print(f"exact sums layout={layout} three-piece operand={three_piece} M={M} N={N} K={K}", flush=True)
+    cx6, c32 = _both(a.float().to(dev), b.float().to(dev), None, M, N, K, ta=ta, tb=int(layout == "abt"))
+    assert torch.equal(cx6, exact)
+    assert torch.equal(c32, exact)

@@ -354,7 +354,18 @@ template <class S, bool FULL, bool AKC, bool BKC>
 __global__ __launch_bounds__(kThreads) void gemm_x6_kernel(X6Args g) {
   extern __shared__ unsigned short x6_smem[];
   int tm, tn;
-  gemm_tile_order(g.tiles_m, g.tiles_n, &tm, &tn);
+  if constexpr (S::FOLD) {
+    // long-K products: each XCD (workgroup i runs on XCD i % 8) takes a contiguous range of
+    // the tiles in row-major order, so the column tiles that share a panel of the long
+    // operand A run side by side on one XCD and read it from its L2 once
+    const int total = g.tiles_m * g.tiles_n;
+    int id = blockIdx.x;
+    if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+    tm = id / g.tiles_n;
+    tn = id % g.tiles_n;
+  } else {
+    gemm_tile_order(g.tiles_m, g.tiles_n, &tm, &tn);
+  }
   x6_tile<S, FULL, AKC, BKC>(g, tm * S::BM, tn * S::BN, x6_smem);
 }
 

@@ -173,9 +173,9 @@ namespace {
 // Split count of the split-bf16 A^T B / A B kernel for this product when it is taken with at
 // most `max_planes` partial planes (0: not taken, because split products are off, the
 // product is small, or the planes would leave fp32 running sums longer than 2048 k).
-int x6_tn_take(const GemmDesc& d, long max_planes) {
+int x6_longk_take(const GemmDesc& d, long max_planes) {
   if (d.trans_b || !split_products_mode()) return 0;  // A^T B or A B
-  int s = gemm_x6_tn_splits(d.M, d.N, d.K);
+  int s = gemm_x6_longk_splits(d.M, d.N, d.K);
   if (s <= 0) return 0;
   if (s > max_planes) s = (int)max_planes;
   if (s < 1 || (long)s * 2048 < d.K) return 0;
@@ -186,7 +186,7 @@ int x6_tn_take(const GemmDesc& d, long max_planes) {
 size_t gemm_ws_bytes_layout(int M, int N, int K, int acc64, int trans_a, int trans_b) {
   size_t need = gemm_ws_bytes(M, N, K, acc64);
   if (!trans_b && split_products_mode()) {
-    const int s = gemm_x6_tn_splits(M, N, K);
+    const int s = gemm_x6_longk_splits(M, N, K);
     if (s > 1) need = std::max(need, sizeof(float) * (size_t)s * M * N);
   }
   return need;
@@ -194,13 +194,13 @@ size_t gemm_ws_bytes_layout(int M, int N, int K, int acc64, int trans_a, int tra
 
 int gemm_tn_planes(int M, int N, int K) {
   int s = gemm_pick_splits(M, N, K, 1);
-  if (split_products_mode()) s = std::max(s, gemm_x6_tn_splits(M, N, K));
+  if (split_products_mode()) s = std::max(s, gemm_x6_longk_splits(M, N, K));
   return s;
 }
 
 int gemm_partials(const GemmDesc& d, float* partials, int splits, hipStream_t s, int* used) {
   HSL_CHECK(check_desc(d));
-  if (const int sx = x6_tn_take(d, splits))
+  if (const int sx = x6_longk_take(d, splits))
     return gemm_x6_run(d.A, d.B, nullptr, nullptr, partials, d.M, d.N, d.K, d.lda, d.ldb, d.N, d.trans_a, 0, sx, s,
                        used);
   return dispatch(pick_tile(d.M, d.N, d.acc64), d, partials, std::min(splits, gemm_pick_splits(d.M, d.N, d.K, d.acc64)), s,
@@ -214,7 +214,7 @@ int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s) {
     return gemm_x6_run(d.A, d.B, d.bias, d.C, nullptr, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, 0, 1, 1, s, nullptr);
   // planes the workspace holds (one split needs none: it writes C directly)
   const long planes = ws ? (long)(ws_bytes / (sizeof(float) * (size_t)d.M * d.N)) : 0;
-  if (const int sx = x6_tn_take(d, planes > 1 ? planes : 1)) {
+  if (const int sx = x6_longk_take(d, planes > 1 ? planes : 1)) {
     if (sx == 1)
       return gemm_x6_run(d.A, d.B, d.bias, d.C, nullptr, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, d.trans_a, 0, 1, s,
                          nullptr);

@@ -56,7 +56,7 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kBK = 16;                    // k per slice
 constexpr int kThreads = 512;              // 8 waves
 constexpr int kLDK = kBK + 8;              // LDS row stride in bf16 elements (48 bytes)
-constexpr int kTnRun = 2048;               // longest k-range of one split of an A^T B product
+constexpr int kLongKRun = 2048;            // longest k-range of one split of an A^T B / A B product
 
 // Tile shape: BM x BN with WM x WN waves; FOLD > 0 adds the MFMA accumulators into a
 // second fp32 accumulator every FOLD slices (so no accumulator rounding happens at the
@@ -389,16 +389,16 @@ bool gemm_x6_applies(int M, int N, int K) {
   return tiles >= 256 && K >= 32;
 }
 
-int gemm_x6_tn_splits(int M, int N, int K) {
+int gemm_x6_longk_splits(int M, int N, int K) {
   // C = A^T B (weight gradients, K = T*B) or C = A B (dx = dgates W_ih, K = 4H): at least
   // one tile each way and >= 8 GFLOP.
-  // Splits fill the chip (one workgroup per CU) and keep every split to at most kTnRun k,
+  // Splits fill the chip (one workgroup per CU) and keep every split to at most kLongKRun k,
   // summed inside the kernel as fp32 runs of 64 k (FOLD); the planes are added in fp64.
   using S = ShapeWgrad;
   if (M < S::BM || N < S::BN || K < 2 * kBK || 2.0 * M * N * K < 8e9) return 0;
   const long tiles = (long)((M + S::BM - 1) / S::BM) * ((N + S::BN - 1) / S::BN);
   long s = (256 + tiles - 1) / tiles;
-  const long by_run = (K + kTnRun - 1) / kTnRun;
+  const long by_run = (K + kLongKRun - 1) / kLongKRun;
   if (by_run > s) s = by_run;
   if (s > K / kBK) s = K / kBK;
   if (s > 64) s = 64;

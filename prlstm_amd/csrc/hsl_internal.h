@@ -90,7 +90,7 @@ int gemm_pick_splits(int M, int N, int K, int acc64);
 // C[M][N] = A[M][K] . B[N][K]^T (+ bias[N]) with 16-bit A and B (fmt 0 bf16, 1 fp16),
 // fp32 accumulation and output (gemm_b16.hip).
 bool gemm_x6_applies(int M, int N, int K);  // C = A B^T products (input projection)
-int gemm_x6_tn_splits(int M, int N, int K);  // C = A^T B or A B: split count, 0 = not taken
+int gemm_x6_longk_splits(int M, int N, int K);  // C = A^T B or A B: split count, 0 = not taken
 // Split-bf16 product (gemm_x6.hip): any layout but trans_a = trans_b = 1;
 // with partial != nullptr the k-splits go to planes [used][M][N] (no bias).
 int gemm_x6_run(const float* A, const float* B, const float* bias, float* C, float* partial, int M, int N, int K,

@@ -37,7 +37,8 @@
 // while slice s multiplies; the registers of slice s+1 are split into the three bf16
 // pieces and written to the other LDS buffer ([piece][row][k], 48-byte rows, conflict-free
 // 128-bit fragment reads) in between this slice's 48 products (scheduling groups), then
-// one barrier.  The loop body has no branches: the last slices store and request a
+// one barrier.  The output is written with non-temporal stores (it is read back only by
+// later kernels), which keeps the operand panels in L2.  The loop body has no branches: the last slices store and request a
 // repeat of the last slice, so the compiler can interleave the split with the products.
 // Shapes with partial tiles (or operands without 16-byte alignment) launch a second
 // instance that reads element-wise from clamped addresses and zeroes what lies outside.
@@ -342,7 +343,7 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * S::TM + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        if (FULL || m < g.M) outp[(size_t)m * ldo + n] = res[r] + bval;
+        if (FULL || m < g.M) __builtin_nontemporal_store(res[r] + bval, outp + (size_t)m * ldo + n);
       }
     }
 }

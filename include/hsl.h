@@ -174,6 +174,21 @@ int hsl_par_bwd(const float* dout, const float* dh_n, const float* dc_n,
                 float* dx, float* dw_ih, float* db_ih, float* dc0,
                 void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream);
 
+/* hsl_par_bwd for a bf16 (fmt 0) or fp16 (fmt 1) module: x and w_ih are 16-bit,
+ * everything else as in hsl_par_bwd (fp32 gradients).  The results equal
+ * hsl_par_bwd's on the widened x and w_ih bit for bit.  A bf16 x / w_ih is read by
+ * the split-product kernel as it is (one bf16 piece, three products per k-step
+ * instead of six); otherwise (fp16, or products too small for that kernel) it is
+ * widened into the workspace first.  Backward of the reference's parallel path for
+ * a module moved to bf16/fp16 (_parallel.py:38-74, run that way by
+ * test_parallel.py:22-38). */
+size_t hsl_par_bwd_b16_ws_bytes(int T, int B, int D, int H);
+int hsl_par_bwd_b16(const float* dout, const float* dh_n, const float* dc_n,
+                    const void* x, const float* c0, const float* gates, const float* c_seq,
+                    const void* w_ih, float eps,
+                    float* dx, float* dw_ih, float* db_ih, float* dc0,
+                    void* ws, size_t ws_bytes, int T, int B, int D, int H, int fmt, void* stream);
+
 /* The scan kernels on their own (used by hsl_par_fwd / hsl_par_bwd).
  * hsl_scan_fwd: gates [T,B,4H] pre-activations -> out, c_seq [T,B,H].
  * hsl_scan_bwd: -> dgates [T,B,4H] (pre-activation gradients) and, when

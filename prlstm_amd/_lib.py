@@ -39,6 +39,8 @@ SIGNATURES = {
     "hsl_par_fwd_b16": (_I, [_P, _P, _P, _P, _F, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "hsl_par_bwd_ws_bytes": (_Z, [_I, _I, _I, _I]),
     "hsl_par_bwd": (_I, [_P] * 8 + [_F, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _P]),
+    "hsl_par_bwd_b16_ws_bytes": (_Z, [_I, _I, _I, _I]),
+    "hsl_par_bwd_b16": (_I, [_P] * 8 + [_F, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _P]),
     "hsl_scan_fwd": (_I, [_P, _P, _F, _P, _P, _I, _I, _I, _P]),
     "hsl_scan_bwd": (_I, [_P] * 6 + [_F, _P, _P, _P, _I, _I, _I, _P]),
     "hsl_gemm_ws_bytes": (_Z, [_I, _I, _I]),

@@ -235,6 +235,49 @@ int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s) {
   return splitk_reduce(P, used, d.bias, d.C, d.M, d.N, d.ldc, s);
 }
 
+namespace {
+__global__ __launch_bounds__(256) void widen16_kernel(const unsigned short* __restrict__ src, float* __restrict__ dst,
+                                                      size_t n, int fmt) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const unsigned short v = src[i];
+    dst[i] = fmt == 0 ? __uint_as_float((unsigned)v << 16) : (float)__builtin_bit_cast(_Float16, v);
+  }
+}
+}  // namespace
+
+int widen16(const void* src, float* dst, size_t n, int fmt, hipStream_t s) {
+  if (n == 0) return HSL_OK;
+  int blocks = (int)std::min<size_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(widen16_kernel, dim3(blocks), dim3(256), 0, s, static_cast<const unsigned short*>(src), dst, n,
+                     fmt);
+  HSL_HIP(hipGetLastError());
+  return HSL_OK;
+}
+
+int gemm_run_b16(const GemmDesc& d, int fmt, float* widen, void* ws, size_t ws_bytes, hipStream_t s) {
+  HSL_CHECK(check_desc(d));
+  if (d.trans_b) return fail(HSL_ERR_ARG, "gemm_run_b16: B must be [K][N]");
+  if (d.M == 0 || d.N == 0) return HSL_OK;
+  if (fmt == 0) {  // a bf16 value is one bf16 piece: the split kernel reads it as it is
+    const long planes = ws ? (long)(ws_bytes / (sizeof(float) * (size_t)d.M * d.N)) : 0;
+    if (const int sx = x6_longk_take(d, planes > 1 ? planes : 1)) {
+      if (sx == 1)
+        return gemm_x6_run(d.A, d.B, d.bias, d.C, nullptr, d.M, d.N, d.K, d.lda, d.ldb, d.ldc, d.trans_a, 0, 1, s,
+                           nullptr, 1);
+      float* P = static_cast<float*>(ws);
+      int used = 1;
+      HSL_CHECK(gemm_x6_run(d.A, d.B, nullptr, nullptr, P, d.M, d.N, d.K, d.lda, d.ldb, d.N, d.trans_a, 0, sx, s,
+                            &used, 1));
+      return splitk_reduce(P, used, d.bias, d.C, d.M, d.N, d.ldc, s);
+    }
+  }
+  // otherwise the fp32 product of the widened B (same leading dimension)
+  HSL_CHECK(widen16(d.B, widen, (size_t)d.K * d.ldb, fmt, s));
+  GemmDesc w = d;
+  w.B = widen;
+  return gemm_run(w, ws, ws_bytes, s);
+}
+
 int splitk_reduce(const float* P, int splits, const float* bias, float* C, int M, int N, int ldc, hipStream_t s) {
   const size_t total = (size_t)M * N;
   if (total == 0) return HSL_OK;

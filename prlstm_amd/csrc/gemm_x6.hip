@@ -44,6 +44,8 @@
 // instance that reads element-wise from clamped addresses and zeroes what lies outside.
 // A row-contiguous operand ([k][row]) is loaded as two k-rows of four rows per thread and
 // written transposed, each row's k-pair as one 32-bit word per piece.
+#include <type_traits>
+
 #include "gemm_core.h"
 
 namespace hsl {
@@ -243,15 +245,69 @@ struct X6Operand {
   }
 };
 
-template <class S, bool FULL, bool AKC, bool BKC>
+// A bf16 B operand ([k][row], 128 rows; a half-precision module's x or W_ih): a bf16
+// value is its own single piece, so only piece 0 is staged and the products with B's
+// pieces 1 and 2 (zero for such values) are not issued.  Thread t loads rows
+// 4 (t / 16) .. +3 at k-row t % 16 (8 bytes); lanes t and t^1 swap two of those rows, so
+// the even lane writes rows 0-1 and the odd lane rows 2-3, each as a (k even, k odd) pair.
+template <bool FULL>
+struct X6OperandB16 {
+  static constexpr int kWrites = 2, kLoads = 1;
+  const unsigned short* base;
+  int ld, rows, kend;
+  int r0q, k0;  // first row of the thread's quad, its k-row offset
+  int so;
+  u32x2 v;      // rows 0-1 and rows 2-3 of the quad, two bf16 each
+  __device__ __forceinline__ void init(const float* b, int ld_, int r0, int rows_, int kbeg, int kend_) {
+    base = reinterpret_cast<const unsigned short*>(b);
+    ld = ld_;
+    rows = rows_;
+    kend = kend_;
+    const int t = threadIdx.x, odd = t & 1;
+    r0q = r0 + 4 * (t / 16);
+    k0 = kbeg + t % 16;
+    so = (4 * (t / 16) + 2 * odd) * kLDK + (t % 16) - odd;
+  }
+  __device__ __forceinline__ void load(int slice) {
+    const int kk = k0 + slice * kBK;
+    if constexpr (FULL) {
+      v = *reinterpret_cast<const u32x2*>(base + (size_t)kk * ld + r0q);
+    } else {
+      const bool kok = kk < kend;
+      const unsigned short* kp = base + (size_t)(kok ? kk : kend - 1) * ld;  // a k-row that exists
+      unsigned e[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = r0q + i;
+        const unsigned x = kp[rr < rows ? rr : rows - 1];
+        e[i] = (kok && rr < rows) ? x : 0u;
+      }
+      v = u32x2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+    }
+  }
+  __device__ __forceinline__ void store(unsigned short* p0) const {  // piece 0 only
+    const bool odd = threadIdx.x & 1;
+    const unsigned recv =
+        static_cast<unsigned>(__builtin_amdgcn_mov_dpp(static_cast<int>(odd ? v[0] : v[1]), 0xB1, 0xF, 0xF, false));
+    const unsigned ke = odd ? recv : v[0];  // the two rows at the even k
+    const unsigned ko = odd ? v[1] : recv;  // the same two rows at the odd k
+    *reinterpret_cast<unsigned*>(p0 + so) = (ke & 0xFFFFu) | (ko << 16);
+    *reinterpret_cast<unsigned*>(p0 + so + kLDK) = (ke >> 16) | (ko & 0xFFFF0000u);
+  }
+};
+
+template <class S, bool FULL, bool AKC, bool BKC, int BP>
 __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigned short* sm) {
+  static_assert(BP == 3 || (BP == 1 && !BKC && S::BN == 128), "bf16 B: row-contiguous, 128 rows");
+  using OpB = std::conditional_t<BP == 1, X6OperandB16<FULL>, X6Operand<FULL, BKC, S::BN>>;
+  constexpr int NPP = BP == 1 ? 3 : 6;  // piece products per k-step
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / S::WN, wn = wave % S::WN;
   const int half = lane >> 5, r32 = lane & 31;
   const int kbeg = blockIdx.z * g.kps;
   const int kend = min(g.K, kbeg + g.kps);
   X6Operand<FULL, AKC, S::BM> oa;
-  X6Operand<FULL, BKC, S::BN> ob;
+  OpB ob;
   oa.init(g.A, g.lda, m0, g.M, kbeg, kend);
   ob.init(g.B, g.ldb, n0, g.N, kbeg, kend);
   auto store = [&](int buf) __attribute__((always_inline)) {
@@ -284,9 +340,11 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
 #pragma unroll
       for (int i = 0; i < S::FM; ++i)
         fa[q][i] = *reinterpret_cast<const u32x4*>(base + q * S::PA + arow + 32 * i * kLDK);
+      if (q < BP) {
 #pragma unroll
-      for (int j = 0; j < S::FN; ++j)
-        fb[q][j] = *reinterpret_cast<const u32x4*>(base + 3 * S::PA + q * S::PB + brow + 32 * j * kLDK);
+        for (int j = 0; j < S::FN; ++j)
+          fb[q][j] = *reinterpret_cast<const u32x4*>(base + 3 * S::PA + q * S::PB + brow + 32 * j * kLDK);
+      }
     }
     // slice it+1 into the other buffer (its last reads were before the previous barrier)
     store((it & 1) ^ 1);
@@ -294,17 +352,21 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
     oa.load(nxt);
     ob.load(nxt);
 #pragma unroll
-    for (int pp = 0; pp < 6; ++pp)
+    for (int pp = 0; pp < NPP; ++pp) {
+      // one-piece B: (a0, b), (a1, b), (a2, b) -- the non-zero terms of the six-product
+      // order, in that order, so the sums equal the split path's bit for bit
+      const int qa = BP == 1 ? pp : kPa[pp], qb = BP == 1 ? 0 : kPb[pp];
 #pragma unroll
       for (int i = 0; i < S::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < S::FN; ++j) acc[i][j] = mfma_bf16(fa[kPa[pp]][i], fb[kPb[pp]][j], acc[i][j]);
+        for (int j = 0; j < S::FN; ++j) acc[i][j] = mfma_bf16(fa[qa][i], fb[qb][j], acc[i][j]);
+    }
     if constexpr (FULL) {
       // fragment reads first, then the products with the split and the LDS writes spread
       // between them, then the next slice's loads
-      constexpr int kMfma = 6 * S::FM * S::FN;
-      constexpr int kWrites = X6Operand<FULL, AKC, S::BM>::kWrites + X6Operand<FULL, BKC, S::BN>::kWrites;
-      constexpr int kLoads = X6Operand<FULL, AKC, S::BM>::kLoads + X6Operand<FULL, BKC, S::BN>::kLoads;
+      constexpr int kMfma = NPP * S::FM * S::FN;
+      constexpr int kWrites = X6Operand<FULL, AKC, S::BM>::kWrites + OpB::kWrites;
+      constexpr int kLoads = X6Operand<FULL, AKC, S::BM>::kLoads + OpB::kLoads;
       constexpr int kValu = 28 * kLoads;
       __builtin_amdgcn_sched_group_barrier(0x100, 3 * (S::FM + S::FN), 0);
 #pragma unroll
@@ -351,7 +413,7 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
 // FULL: every tile lies inside the matrices and every split is a whole number of slices
 // (M, N multiples of the tile, K and the split length of 16, aligned operands); chosen
 // per launch, so the unmasked kernel carries no edge code.  AKC / BKC: operand k-contiguous.
-template <class S, bool FULL, bool AKC, bool BKC>
+template <class S, bool FULL, bool AKC, bool BKC, int BP>
 __global__ __launch_bounds__(kThreads) void gemm_x6_kernel(X6Args g) {
   extern __shared__ unsigned short x6_smem[];
   int tm, tn;
@@ -367,19 +429,19 @@ __global__ __launch_bounds__(kThreads) void gemm_x6_kernel(X6Args g) {
   } else {
     gemm_tile_order(g.tiles_m, g.tiles_n, &tm, &tn);
   }
-  x6_tile<S, FULL, AKC, BKC>(g, tm * S::BM, tn * S::BN, x6_smem);
+  x6_tile<S, FULL, AKC, BKC, BP>(g, tm * S::BM, tn * S::BN, x6_smem);
 }
 
-template <class S, bool AKC, bool BKC>
+template <class S, bool AKC, bool BKC, int BP = 3>
 void x6_launch(X6Args g, bool vec, int splits, hipStream_t s) {
   g.tiles_m = (g.M + S::BM - 1) / S::BM;
   g.tiles_n = (g.N + S::BN - 1) / S::BN;
   const bool full = vec && g.M % S::BM == 0 && g.N % S::BN == 0 && g.K % kBK == 0 && g.kps % kBK == 0;
   const dim3 grid(g.tiles_m * g.tiles_n, 1, splits);
   if (full)
-    hipLaunchKernelGGL((gemm_x6_kernel<S, true, AKC, BKC>), grid, dim3(kThreads), S::LDS, s, g);
+    hipLaunchKernelGGL((gemm_x6_kernel<S, true, AKC, BKC, BP>), grid, dim3(kThreads), S::LDS, s, g);
   else
-    hipLaunchKernelGGL((gemm_x6_kernel<S, false, AKC, BKC>), grid, dim3(kThreads), S::LDS, s, g);
+    hipLaunchKernelGGL((gemm_x6_kernel<S, false, AKC, BKC, BP>), grid, dim3(kThreads), S::LDS, s, g);
 }
 
 }  // namespace
@@ -406,14 +468,15 @@ int gemm_x6_longk_splits(int M, int N, int K) {
   return s < 1 ? 1 : (int)s;
 }
 
-int gemm_x6_run(const float* A, const float* B, const float* bias, float* C, float* partial, int M, int N, int K,
-                int lda, int ldb, int ldc, int trans_a, int trans_b, int splits, hipStream_t s, int* used) {
+int gemm_x6_run(const float* A, const void* B, const float* bias, float* C, float* partial, int M, int N, int K,
+                int lda, int ldb, int ldc, int trans_a, int trans_b, int splits, hipStream_t s, int* used, int b_bf16) {
   if (M <= 0 || N <= 0 || K <= 0) return fail(HSL_ERR_ARG, "gemm_x6: empty product");
   if (trans_a && trans_b) return fail(HSL_ERR_ARG, "gemm_x6: layout not supported");
+  if (b_bf16 && trans_b) return fail(HSL_ERR_ARG, "gemm_x6: a bf16 B must be [K][N] (trans_b = 0)");
   if (splits < 1 || (splits > 1 && !partial)) splits = 1;
   X6Args g{};
   g.A = A;
-  g.B = B;
+  g.B = static_cast<const float*>(B);  // bf16 data when b_bf16 (read as such by X6OperandB16)
   g.bias = partial ? nullptr : bias;
   g.out = partial ? partial : C;
   g.partial = partial ? 1 : 0;
@@ -429,7 +492,11 @@ int gemm_x6_run(const float* A, const float* B, const float* bias, float* C, flo
   const int n = (K + kps - 1) / kps;
   if (used) *used = n;
   const bool vec = aligned16(A) && aligned16(B) && lda % 4 == 0 && ldb % 4 == 0;
-  if (!trans_a && trans_b)
+  if (b_bf16 && trans_a)
+    x6_launch<ShapeWgrad, false, false, 1>(g, vec, n, s);  // dgates^T x with a bf16 x
+  else if (b_bf16)
+    x6_launch<ShapeWgrad, true, false, 1>(g, vec, n, s);  // dgates W_ih with a bf16 W_ih
+  else if (!trans_a && trans_b)
     x6_launch<ShapeProj, true, true>(g, vec, n, s);  // x W^T: both operands k-contiguous
   else if (trans_a)
     x6_launch<ShapeWgrad, false, false>(g, vec, n, s);  // A^T B: both row-contiguous

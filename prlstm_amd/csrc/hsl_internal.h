@@ -77,6 +77,11 @@ size_t gemm_ws_bytes_layout(int M, int N, int K, int acc64, int trans_a, int tra
 size_t gemm_ws_bytes(int M, int N, int K, int acc64);
 // Full product with optional split-K through ws (ws may be null when ws_bytes==0).
 int gemm_run(const GemmDesc& d, void* ws, size_t ws_bytes, hipStream_t s);
+// C = op(A) B with a 16-bit B ([K][ldb] row-major, d.B; fmt 0 = bf16, 1 = fp16): a bf16 B
+// goes straight to the split kernel where that applies; otherwise B is widened into
+// `widen` (K * ldb floats) and the fp32 product runs.
+int gemm_run_b16(const GemmDesc& d, int fmt, float* widen, void* ws, size_t ws_bytes, hipStream_t s);
+int widen16(const void* src, float* dst, size_t n, int fmt, hipStream_t s);
 // Split-K partial sums kept as fp32 [used][M][N] in `partials` (room for `splits`
 // planes); *used receives the number of planes written (<= splits).  Used by the
 // fused epilogues of the weight gradients.
@@ -93,8 +98,10 @@ bool gemm_x6_applies(int M, int N, int K);  // C = A B^T products (input project
 int gemm_x6_longk_splits(int M, int N, int K);  // C = A^T B or A B: split count, 0 = not taken
 // Split-bf16 product (gemm_x6.hip): any layout but trans_a = trans_b = 1;
 // with partial != nullptr the k-splits go to planes [used][M][N] (no bias).
-int gemm_x6_run(const float* A, const float* B, const float* bias, float* C, float* partial, int M, int N, int K,
-                int lda, int ldb, int ldc, int trans_a, int trans_b, int splits, hipStream_t s, int* used);
+// b_bf16: B holds bf16 values (one piece each; trans_b = 0 only), three products per step.
+int gemm_x6_run(const float* A, const void* B, const float* bias, float* C, float* partial, int M, int N, int K,
+                int lda, int ldb, int ldc, int trans_a, int trans_b, int splits, hipStream_t s, int* used,
+                int b_bf16 = 0);
 int gemm_b16_run(const void* A, const void* B, const float* bias, float* C, int M, int N, int K, int lda, int ldb,
                  int ldc, int fmt, hipStream_t s);
 

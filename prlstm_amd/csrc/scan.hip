@@ -23,6 +23,8 @@
 // next chunk's loads are issued before the current chunk is processed.  Every [T,...]
 // stream is read or written once, with non-temporal accesses (the streams bypass the
 // caches' retention; measured 9% faster forward on MI355X).
+#include <algorithm>
+
 #include "hsl_internal.h"
 
 namespace hsl {
@@ -299,6 +301,61 @@ size_t carve_par(void* ws, size_t cap, int T, int B, int D, int H, ParWs* o) {
   return c.off;
 }
 
+// The parallel backward with an fp32 (fmt < 0) or 16-bit (fmt 0 bf16, 1 fp16) x and W_ih.
+// The 16-bit workspace adds one region that holds a widened x or W_ih when a product has
+// to run on the fp32 kernels.
+size_t carve_par_b16(void* ws, size_t cap, int T, int B, int D, int H, ParWs* o, float** widen) {
+  const size_t off = carve_par(ws, cap, T, B, D, H, o);
+  Carver c(ws, cap);
+  c.off = off;
+  const size_t n = std::max((size_t)T * B * D, (size_t)4 * H * D);
+  float* w = c.take<float>(n + 1);
+  if (widen) *widen = w;
+  return c.off;
+}
+
+int par_bwd_impl(const float* dout, const float* dh_n, const float* dc_n, const void* x, const float* c0,
+                 const float* gates, const float* c_seq, const void* w_ih, float eps, float* dx, float* dw_ih,
+                 float* db_ih, float* dc0, void* ws, size_t ws_bytes, int T, int B, int D, int H, int fmt,
+                 hipStream_t s) {
+  const char* fn = fmt < 0 ? "hsl_par_bwd" : "hsl_par_bwd_b16";
+  HSL_CHECK(check_scan_dims(T, B, H));
+  if (D < 0) return fail(HSL_ERR_ARG, "negative D");
+  if (H == 0) return HSL_OK;
+  if (!dw_ih || !db_ih || !w_ih) return fail(HSL_ERR_ARG, "%s: null pointer", fn);
+  ParWs w;
+  float* widen = nullptr;
+  const size_t need =
+      fmt < 0 ? carve_par(ws, ws_bytes, T, B, D, H, &w) : carve_par_b16(ws, ws_bytes, T, B, D, H, &w, &widen);
+  if (!ws || ws_bytes < need) return fail(HSL_ERR_ARG, "%s: workspace %zu bytes, need %zu", fn, ws_bytes, need);
+  if (T == 0 || B == 0) {
+    HSL_CHECK(copy_f32(dw_ih, nullptr, (size_t)4 * H * D, s));
+    HSL_CHECK(copy_f32(db_ih, nullptr, (size_t)4 * H, s));
+    if (dc0) HSL_CHECK(copy_f32(dc0, nullptr, (size_t)B * H, s));
+    return HSL_OK;
+  }
+  if (!dout || !x || !gates || !c_seq) return fail(HSL_ERR_ARG, "%s: null pointer", fn);
+  HSL_CHECK(scan_bwd(gates, c0, c_seq, dout, dh_n, dc_n, eps, w.dgates, w.db_part, dc0, T, B, H, s));
+  HSL_CHECK(bias_grads_from_parts(w.db_part, B, nullptr, nullptr, nullptr, db_ih, nullptr, nullptr, H, s));
+  const int TB = T * B;
+  if (D > 0) {
+    // dW_ih = dgates^T x, dx = dgates W_ih (B operands [K][N]; 16-bit ones pass as such)
+    GemmDesc g5{w.dgates, static_cast<const float*>(x), nullptr, dw_ih, 4 * H, D, TB, 4 * H, D, D, 1, 0, 1};
+    if (fmt < 0)
+      HSL_CHECK(gemm_run(g5, w.gemm, w.gemm_bytes, s));
+    else
+      HSL_CHECK(gemm_run_b16(g5, fmt, widen, w.gemm, w.gemm_bytes, s));
+    if (dx) {
+      GemmDesc g6{w.dgates, static_cast<const float*>(w_ih), nullptr, dx, TB, D, 4 * H, 4 * H, D, D, 0, 0, 1};
+      if (fmt < 0)
+        HSL_CHECK(gemm_run(g6, w.gemm, w.gemm_bytes, s));
+      else
+        HSL_CHECK(gemm_run_b16(g6, fmt, widen, w.gemm, w.gemm_bytes, s));
+    }
+  }
+  return HSL_OK;
+}
+
 }  // namespace
 }  // namespace hsl
 
@@ -356,37 +413,26 @@ size_t hsl_par_bwd_ws_bytes(int T, int B, int D, int H) {
   return carve_par(nullptr, 0, T, B, D, H, &w);
 }
 
+size_t hsl_par_bwd_b16_ws_bytes(int T, int B, int D, int H) {
+  if (T < 0 || B < 0 || D < 0 || H < 0) return 0;
+  ParWs w;
+  return carve_par_b16(nullptr, 0, T, B, D, H, &w, nullptr);
+}
+
 int hsl_par_bwd(const float* dout, const float* dh_n, const float* dc_n, const float* x, const float* c0,
                 const float* gates, const float* c_seq, const float* w_ih, float eps, float* dx, float* dw_ih,
                 float* db_ih, float* dc0, void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream) {
-  HSL_CHECK(check_scan_dims(T, B, H));
-  if (D < 0) return fail(HSL_ERR_ARG, "negative D");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (H == 0) return HSL_OK;
-  if (!dw_ih || !db_ih || !w_ih) return fail(HSL_ERR_ARG, "hsl_par_bwd: null pointer");
-  ParWs w;
-  const size_t need = carve_par(ws, ws_bytes, T, B, D, H, &w);
-  if (!ws || ws_bytes < need) return fail(HSL_ERR_ARG, "hsl_par_bwd: workspace %zu bytes, need %zu", ws_bytes, need);
-  if (T == 0 || B == 0) {
-    HSL_CHECK(copy_f32(dw_ih, nullptr, (size_t)4 * H * D, s));
-    HSL_CHECK(copy_f32(db_ih, nullptr, (size_t)4 * H, s));
-    if (dc0) HSL_CHECK(copy_f32(dc0, nullptr, (size_t)B * H, s));
-    return HSL_OK;
-  }
-  if (!dout || !x || !gates || !c_seq)
-    return fail(HSL_ERR_ARG, "hsl_par_bwd: null pointer");
-  HSL_CHECK(scan_bwd(gates, c0, c_seq, dout, dh_n, dc_n, eps, w.dgates, w.db_part, dc0, T, B, H, s));
-  HSL_CHECK(bias_grads_from_parts(w.db_part, B, nullptr, nullptr, nullptr, db_ih, nullptr, nullptr, H, s));
-  const int TB = T * B;
-  if (D > 0) {
-    GemmDesc g5{w.dgates, x, nullptr, dw_ih, 4 * H, D, TB, 4 * H, D, D, 1, 0, 1};
-    HSL_CHECK(gemm_run(g5, w.gemm, w.gemm_bytes, s));
-    if (dx) {
-      GemmDesc g6{w.dgates, w_ih, nullptr, dx, TB, D, 4 * H, 4 * H, D, D, 0, 0, 1};
-      HSL_CHECK(gemm_run(g6, w.gemm, w.gemm_bytes, s));
-    }
-  }
-  return HSL_OK;
+  return par_bwd_impl(dout, dh_n, dc_n, x, c0, gates, c_seq, w_ih, eps, dx, dw_ih, db_ih, dc0, ws, ws_bytes, T, B, D,
+                      H, -1, static_cast<hipStream_t>(stream));
+}
+
+int hsl_par_bwd_b16(const float* dout, const float* dh_n, const float* dc_n, const void* x, const float* c0,
+                    const float* gates, const float* c_seq, const void* w_ih, float eps, float* dx, float* dw_ih,
+                    float* db_ih, float* dc0, void* ws, size_t ws_bytes, int T, int B, int D, int H, int fmt,
+                    void* stream) {
+  if (fmt != 0 && fmt != 1) return fail(HSL_ERR_ARG, "hsl_par_bwd_b16: format must be 0 (bf16) or 1 (fp16)");
+  return par_bwd_impl(dout, dh_n, dc_n, x, c0, gates, c_seq, w_ih, eps, dx, dw_ih, db_ih, dc0, ws, ws_bytes, T, B, D,
+                      H, fmt, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

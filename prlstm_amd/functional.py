@@ -182,8 +182,9 @@ class ParallelHalfFn(torch.autograd.Function):
     """Parallel mode of a bf16/fp16 module: x and W_ih stay 16-bit for the input
     projection, which runs on 16-bit MFMA with fp32 accumulation (each product of two
     16-bit values is exact in fp32); c0 and b_ih arrive widened, and the scan, the
-    outputs and the whole backward are fp32 (x and W_ih widened there), as in
-    ``ParallelFn``."""
+    outputs and the whole backward are fp32, as in ``ParallelFn``; the backward reads
+    the 16-bit x and W_ih itself (``hsl_par_bwd_b16``, results equal to those on the
+    widened operands)."""
 
     @staticmethod
     def forward(ctx, x, c0, w_ih, b_ih, eps):
@@ -219,17 +220,18 @@ class ParallelHalfFn(torch.autograd.Function):
         dout = _grad_or_zeros(dout, c_seq)
         dh_n, dc_n = _c(dh_n), _c(dc_n)
         need = ctx.needs_input_grad
-        x32, w32 = x.float(), w_ih.float()
-        dx = torch.empty_like(x32) if need[0] else None
-        dc0 = x32.new_empty(B, H) if need[1] else None
-        dw_ih = torch.empty_like(w32)
-        db_ih = x32.new_empty(4 * H)
+        f32 = dict(device=x.device, dtype=torch.float32)
+        dx = torch.empty(T, B, D, **f32) if need[0] else None
+        dc0 = torch.empty(B, H, **f32) if need[1] else None
+        dw_ih = torch.empty(4 * H, D, **f32)
+        db_ih = torch.empty(4 * H, **f32)
         lib = _lib.load()
-        nbytes = lib.hsl_par_bwd_ws_bytes(T, B, D, H)
+        nbytes = lib.hsl_par_bwd_b16_ws_bytes(T, B, D, H)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
         P = _lib.ptr
-        _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(x32), P(c0), P(gates), P(c_seq),
-                  P(w32), ctx.eps, P(dx), P(dw_ih), P(db_ih), P(dc0), P(ws), nbytes, T, B, D, H,
+        fmt = 0 if x.dtype == torch.bfloat16 else 1
+        _lib.call("hsl_par_bwd_b16", P(dout), P(dh_n), P(dc_n), P(x), P(c0), P(gates), P(c_seq),
+                  P(w_ih), ctx.eps, P(dx), P(dw_ih), P(db_ih), P(dc0), P(ws), nbytes, T, B, D, H, fmt,
                   _lib.stream_of(x.device))
         # autograd casts each gradient to its input's dtype (x and W_ih: 16-bit)
         return dx, dc0, dw_ih, db_ih, None

@@ -125,3 +125,52 @@ def test_gemm_b16_unaligned_rows(dev):
     scale = a[:, :K].double().abs() @ b[:, :K].double().abs().t()
     err = (C.cpu().double() - ref).abs()
     assert bool((err <= 2e-6 * K ** 0.5 * scale + 1e-30).all())
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("T,B,D,H", [(32, 4, 16, 24), (4096, 16, 256, 1024)])
+def test_parallel_backward_16bit_operands_equal_widened(dev, fmt, T, B, D, H):
+    """hsl_par_bwd_b16 reads the 16-bit x and W_ih itself: a bf16 value is one bf16 piece,
+    so the split-product kernel issues three products per k-step instead of six (at
+    configs[4] size), and otherwise the operand is widened into the workspace.  Either way
+    the gradients must equal hsl_par_bwd's on the widened operands bit for bit (the six
+    products' extra terms are exact zeros added in the same order)."""
+    dt = torch.bfloat16 if fmt == 0 else torch.float16
+    print(f"par bwd 16-bit fmt={fmt} T={T} B={B} D={D} H={H}", flush=True)
+    from prlstm_amd import _lib
+    P, s = _lib.ptr, _lib.stream_of(dev)
+    g = torch.Generator().manual_seed(T + D)
+    x16 = torch.randn(T, B, D, generator=g).to(dt).to(dev)
+    w16 = (torch.randn(4 * H, D, generator=g) * 0.05).to(dt).to(dev)
+    b_ih = (torch.randn(4 * H, generator=g) * 0.05).to(dev)
+    c0 = (torch.randn(B, H, generator=g) * 0.5).to(dev)
+    gates = torch.empty(T, B, 4 * H, device=dev)
+    out = torch.empty(T, B, H, device=dev)
+    c_seq = torch.empty(T, B, H, device=dev)
+    _lib.call("hsl_par_fwd_b16", P(x16), P(c0), P(w16), P(b_ih), 1e-6, P(gates), P(out), P(c_seq),
+              T, B, D, H, fmt, s)
+    dout = torch.randn(T, B, H, generator=g).to(dev)
+    dh_n = torch.randn(B, H, generator=g).to(dev)
+    dc_n = torch.randn(B, H, generator=g).to(dev)
+    res = []
+    for widened in (False, True):
+        dx = torch.empty(T, B, D, device=dev)
+        dw = torch.empty(4 * H, D, device=dev)
+        db = torch.empty(4 * H, device=dev)
+        dc0 = torch.empty(B, H, device=dev)
+        if widened:
+            xw, ww = x16.float(), w16.float()
+            n = _lib.load().hsl_par_bwd_ws_bytes(T, B, D, H)
+            ws = torch.empty(n, dtype=torch.uint8, device=dev)
+            _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(xw), P(c0), P(gates), P(c_seq), P(ww), 1e-6,
+                      P(dx), P(dw), P(db), P(dc0), P(ws), n, T, B, D, H, s)
+        else:
+            n = _lib.load().hsl_par_bwd_b16_ws_bytes(T, B, D, H)
+            ws = torch.empty(n, dtype=torch.uint8, device=dev)
+            _lib.call("hsl_par_bwd_b16", P(dout), P(dh_n), P(dc_n), P(x16), P(c0), P(gates), P(c_seq), P(w16),
+                      1e-6, P(dx), P(dw), P(db), P(dc0), P(ws), n, T, B, D, H, fmt, s)
+        torch.cuda.synchronize()
+        res.append((dx.clone(), dw.clone(), db.clone(), dc0.clone()))
+    for name, a, b in zip(("dx", "dW_ih", "db_ih", "dc0"), res[0], res[1]):
+        assert torch.isfinite(a).all(), name
+        assert torch.equal(a, b), (name, float((a - b).abs().max()))

@@ -24,6 +24,16 @@ def _eager(m, x):
 @pytest.mark.parametrize("parallel", [False, True])
 @pytest.mark.parametrize("shape", [(16, 8, 32, 64), (256, 32, 256, 512)])
 def test_graph_replays_match_eager(dev, parallel, shape):
+    _check_replays(dev, parallel, shape)
+
+
+def test_graph_replays_split_products(dev):
+    """Parallel mode at a size whose input projection (1024 tiles of 256x256) and dW_ih
+    (34 GFLOP in 8 k-splits summed in fp64) run on the split-bf16 kernels."""
+    _check_replays(dev, True, (1024, 16, 256, 1024))
+
+
+def _check_replays(dev, parallel, shape):
     T, B, D, H = shape
     print(f"graph T={T} B={B} D={D} H={H} parallel={parallel}", flush=True)
     torch.manual_seed(0)

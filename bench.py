@@ -219,6 +219,13 @@ def bench_modes(args):
     return res
 
 
+def _split_products_state():
+    from prlstm_amd import _lib
+    prev = _lib.set_split_products(1)
+    _lib.set_split_products(prev)
+    return prev
+
+
 def bench_cpu(args):
     """The reference torch backend restated (oracle/), fp32 on this host's cores."""
     from oracle.hsl_oracle import RefHeadStartLSTM
@@ -319,6 +326,11 @@ def main():
         "wall_ms_per_step": round(wall_ms, 5),
         "scan": scan,
         "modes": modes,
+        # products of the modes table: with this switch on (the library default), input
+        # projections of >= 256 tiles of 256x256 and weight-gradient / dx products of >= 8
+        # GFLOP run as exact three-piece bf16 splits (six piece products, fp32 accuracy);
+        # the headline step's products are fused into its persistent kernels (fp32 MFMA)
+        "split_products": bool(_split_products_state()),
         "cpu_baseline": cpu,
     }
     if cpu:

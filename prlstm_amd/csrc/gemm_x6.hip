@@ -32,18 +32,22 @@
 // beyond the bf16 range (|v| > 3.3895e38) rounds to v0 = +-inf and counts as non-finite.
 // hsl_set_split_products(0) gives the IEEE results of the fp32 instruction instead.
 //
-// Workgroup = 8 waves (2 x 4) on a 256 x 256 tile, each wave 128 x 64 (4 x 2 fragments
-// of 32 x 32).  One k-slice is 16 deep.  The fp32 operands of slice s+2 are requested
-// while slice s multiplies; the registers of slice s+1 are split into the three bf16
-// pieces and written to the other LDS buffer ([piece][row][k], 48-byte rows, conflict-free
-// 128-bit fragment reads) in between this slice's 48 products (scheduling groups), then
-// one barrier.  The output is written with non-temporal stores (it is read back only by
-// later kernels), which keeps the operand panels in L2.  The loop body has no branches: the last slices store and request a
-// repeat of the last slice, so the compiler can interleave the split with the products.
+// Workgroup = 8 waves.  The projection uses 256 x 256 tiles (2 x 4 waves of 128 x 64, i.e.
+// 4 x 2 fragments of 32 x 32); the long-K products use 256 x 128 tiles (4 x 2 waves of
+// 64 x 64), which leave registers for the second accumulator.  One k-slice is 16 deep.  The
+// fp32 operands of slice s+2 are requested while slice s multiplies; the registers of slice
+// s+1 are split into the three bf16 pieces and written to the other LDS buffer
+// ([piece][row][k], 48-byte rows, conflict-free 128-bit fragment reads) in between this
+// slice's products (scheduling groups), then one barrier.  The loop body has no branches:
+// the last slices store and request a repeat of the last slice, so the compiler can
+// interleave the split with the products.  The output is written with non-temporal stores
+// (it is read back only by later kernels), which keeps the operand panels in L2.
 // Shapes with partial tiles (or operands without 16-byte alignment) launch a second
 // instance that reads element-wise from clamped addresses and zeroes what lies outside.
-// A row-contiguous operand ([k][row]) is loaded as two k-rows of four rows per thread and
-// written transposed, each row's k-pair as one 32-bit word per piece.
+// A row-contiguous operand ([k][row]) is loaded as k-rows of four rows per thread and
+// written transposed, each row's k-pair as one 32-bit word per piece.  A bf16 B operand
+// (a half-precision module's x or W_ih) is its own single piece: only it is staged and
+// three products per k-step are issued (X6OperandB16).
 #include <type_traits>
 
 #include "gemm_core.h"

@@ -172,13 +172,13 @@ size_t gemm_ws_bytes(int M, int N, int K, int acc64) {
 namespace {
 // Split count of the split-bf16 A^T B / A B kernel for this product when it is taken with at
 // most `max_planes` partial planes (0: not taken, because split products are off, the
-// product is small, or the planes would leave fp32 running sums longer than 2048 k).
+// product is small, or the planes would leave splits longer than kSplitLongKRun).
 int x6_longk_take(const GemmDesc& d, long max_planes) {
   if (d.trans_b || !split_products_mode()) return 0;  // A^T B or A B
   int s = gemm_x6_longk_splits(d.M, d.N, d.K);
   if (s <= 0) return 0;
   if (s > max_planes) s = (int)max_planes;
-  if (s < 1 || (long)s * 2048 < d.K) return 0;
+  if (s < 1 || (long)s * kSplitLongKRun < d.K) return 0;
   return s;
 }
 }  // namespace

@@ -4,7 +4,7 @@
 //  * C[M,N] = A[K,M]^T . B[K,N]: the weight gradients dgates^T h and dgates^T x over
 //    K = T*B (_torch.py:157-162, and autograd's in parallel mode), and C[M,N] = A[M,K] .
 //    B[K,N]: dx = dgates W_ih (K = 4H); both summed as fp32 runs of 64 k folded into a
-//    second fp32 accumulator, split along K into planes of at most 2048 k each that are
+//    second fp32 accumulator, split along K into planes of at most kSplitLongKRun (2048) k each that are
 //    added in fp64 (splitk_reduce, or the caller's own fp64 finalisation) -- the accuracy
 //    that the fp32 kernel gets from folding its accumulators into fp64 registers, which the
 //    8-wave tile has no room for.
@@ -63,7 +63,6 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kBK = 16;                    // k per slice
 constexpr int kThreads = 512;              // 8 waves
 constexpr int kLDK = kBK + 8;              // LDS row stride in bf16 elements (48 bytes)
-constexpr int kLongKRun = 2048;            // longest k-range of one split of an A^T B / A B product
 
 // Tile shape: BM x BN with WM x WN waves; FOLD > 0 adds the MFMA accumulators into a
 // second fp32 accumulator every FOLD slices (so no accumulator rounding happens at the
@@ -459,13 +458,13 @@ bool gemm_x6_applies(int M, int N, int K) {
 int gemm_x6_longk_splits(int M, int N, int K) {
   // C = A^T B (weight gradients, K = T*B) or C = A B (dx = dgates W_ih, K = 4H): at least
   // one tile each way and >= 8 GFLOP.
-  // Splits fill the chip (one workgroup per CU) and keep every split to at most kLongKRun k,
+  // Splits fill the chip (one workgroup per CU) and keep every split to at most kSplitLongKRun k,
   // summed inside the kernel as fp32 runs of 64 k (FOLD); the planes are added in fp64.
   using S = ShapeWgrad;
   if (M < S::BM || N < S::BN || K < 2 * kBK || 2.0 * M * N * K < 8e9) return 0;
   const long tiles = (long)((M + S::BM - 1) / S::BM) * ((N + S::BN - 1) / S::BN);
   long s = (256 + tiles - 1) / tiles;
-  const long by_run = (K + kLongKRun - 1) / kLongKRun;
+  const long by_run = (K + kSplitLongKRun - 1) / kSplitLongKRun;
   if (by_run > s) s = by_run;
   if (s > K / kBK) s = K / kBK;
   if (s > 64) s = 64;

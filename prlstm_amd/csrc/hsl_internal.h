@@ -94,6 +94,10 @@ int splitk_reduce(const float* P, int splits, const float* bias, float* C, int M
 int gemm_pick_splits(int M, int N, int K, int acc64);
 // C[M][N] = A[M][K] . B[N][K]^T (+ bias[N]) with 16-bit A and B (fmt 0 bf16, 1 fp16),
 // fp32 accumulation and output (gemm_b16.hip).
+// Longest k-range of one split of a split-bf16 A^T B / A B product (its fp32 running sum
+// is folded every 64 k; the splits are added in fp64).  4096 put configs[4] dW_ih at 1.48x
+// the parity tolerance against fp64 (the CPU's own fp32 product: 1.12x); 2048 gives 1.08x.
+constexpr int kSplitLongKRun = 2048;
 bool gemm_x6_applies(int M, int N, int K);  // C = A B^T products (input projection)
 int gemm_x6_longk_splits(int M, int N, int K);  // C = A^T B or A B: split count, 0 = not taken
 // Split-bf16 product (gemm_x6.hip): any layout but trans_a = trans_b = 1;

@@ -79,8 +79,9 @@ int hsl_set_exchange_scope(int mode);
  * the previous value.  Process-wide.  No counterpart in the reference (its torch
  * backend calls torch.nn.functional.linear). */
 int hsl_set_split_products(int on);
-/* Which path the last hsl_rec_fwd / hsl_rec_bwd on this host thread used:
- * 1 = per-step, 2 = persistent. */
+/* Which path the last hsl_rec_fwd / hsl_rec_bwd in this process (on any host
+ * thread; autograd runs the backward on its own thread) used: 1 = per-step,
+ * 2 = persistent. */
 int hsl_last_recurrent_path(void);
 /* Whether the last hsl_rec_bwd (in this process, on any thread) accumulated the
  * weight gradients inside the persistent kernel: 0 = no (separate GEMMs), 1 = dW_hh,
@@ -97,6 +98,21 @@ int hsl_timing_collect(int kind, double* total_ms, int* count);
 /* Copy the device error flag kept at the start of a recurrent workspace into
  * *flag (synchronises `stream`); nonzero means a persistent wait timed out. */
 int hsl_poll_error(const void* ws, int* flag, void* stream);
+/* Device errors raised by this library's kernels on the current device since
+ * they were last cleared: one sticky word per device, whatever workspace or
+ * stream the failing call used.  Bit 0: a persistent kernel gave up a wait
+ * between workgroups (hsl_set_spin_timeout_us).  Waits for `stream`, stores the
+ * word in *flags and, when clear != 0, resets it.  Such an abort is never
+ * silent: the aborting workgroups also fill every output they own with NaN
+ * (forward: their rows of h_save, c_save, gact, tanh_c; backward: their dW
+ * planes, bias partials, dgates and dh0/dc0), so the results of the call are NaN.
+ * Counterpart of the reference's loud failures (TORCH_CHECK at
+ * _csrc/lstm_cell.cpp:38-43, RuntimeError at _metal.py:85-87). */
+int hsl_device_errors(int* flags, int clear, void* stream);
+/* Test hook (no reference counterpart): y[i] = f(x[i]) for n fp32 values with
+ * the device math of the kernels, fn 0 = exp, 1 = sigmoid, 2 = tanh (the
+ * reference computes them with torch.sigmoid / torch.tanh, _torch.py:29-34). */
+int hsl_eval_math(int fn, const float* x, float* y, size_t n, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Recurrent mode: replaces HeadStartLSTMTorchFn (_torch.py:86-170).

@@ -20,7 +20,8 @@ import torch
 import torch.nn as nn
 
 from .functional import EPS, headstartlstm_parallel, headstartlstm_recurrent
-from ._lib import last_recurrent_path, set_exchange_scope, set_recurrent_path, set_spin_timeout_us, set_split_products
+from ._lib import (check_errors, last_recurrent_path, set_exchange_scope, set_recurrent_path, set_spin_timeout_us,
+                   set_split_products)
 
 __version__ = "0.1.0"
 
@@ -103,5 +104,6 @@ class HeadStartLSTM(nn.Module):
 __all__ = [
     "HeadStartLSTM", "headstartlstm_recurrent", "headstartlstm_parallel", "EPS",
     "set_recurrent_path", "set_spin_timeout_us", "set_exchange_scope", "set_split_products", "last_recurrent_path",
+    "check_errors",
     "__version__",
 ]

@@ -29,6 +29,8 @@ SIGNATURES = {
     "hsl_set_exchange_scope": (_I, [_I]),
     "hsl_set_split_products": (_I, [_I]),
     "hsl_poll_error": (_I, [_P, _P, _P]),
+    "hsl_device_errors": (_I, [_P, _I, _P]),
+    "hsl_eval_math": (_I, [_I, _P, _P, _Z, _P]),
     "hsl_set_timing": (_I, [_I]),
     "hsl_timing_collect": (_I, [_I, _P, _P]),
     "hsl_rec_fwd_ws_bytes": (_Z, [_I, _I, _I, _I]),
@@ -111,6 +113,28 @@ def set_exchange_scope(mode):
 
 def set_spin_timeout_us(us):
     return load().hsl_set_spin_timeout_us(int(us))
+
+
+def device_errors(device=None, clear=True):
+    """The sticky device-error word of the current (or given) device; waits for its
+    current stream.  Bit 0: a persistent kernel gave up a wait between workgroups."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    flags = ctypes.c_int(0)
+    call("hsl_device_errors", ctypes.byref(flags), 1 if clear else 0, stream_of(dev))
+    return flags.value
+
+
+def check_errors(device=None):
+    """Raise RuntimeError if a kernel of this library reported an error on the device
+    since the last check (and clear it).  A persistent kernel that gives up a wait
+    also leaves NaN in the outputs of that call, so the failure shows in the loss
+    even without this check; this names it."""
+    flags = device_errors(device, clear=True)
+    if flags:
+        raise RuntimeError(
+            f"prlstm_amd: device error word {flags:#x}: a persistent recurrent kernel gave up a wait "
+            "between workgroups (not all of its workgroups were resident at once, or a wait exceeded "
+            "the spin timeout); the outputs of that call are NaN")
 
 
 def last_recurrent_path():

@@ -11,8 +11,9 @@ namespace hsl {
 
 namespace {
 thread_local char g_err[512] = "";
-thread_local int g_last_path = 0;
-std::atomic<int> g_last_fused{0};  // process-wide: autograd runs backward on its own thread
+// process-wide, not per thread: autograd runs the backward on its own worker thread
+std::atomic<int> g_last_path{0};
+std::atomic<int> g_last_fused{0};
 std::atomic<int> g_path_mode{0};
 std::atomic<int> g_exchange_scope{0};
 std::atomic<int> g_split_products{1};
@@ -81,8 +82,18 @@ int recurrent_path_mode() { return g_path_mode.load(); }
 int exchange_scope_mode() { return g_exchange_scope.load(); }
 int split_products_mode() { return g_split_products.load(); }
 long long spin_timeout_ticks() { return g_spin_us.load() * 100; }  // 100 MHz clock
-void note_recurrent_path(int path) { g_last_path = path; }
+void note_recurrent_path(int path) { g_last_path.store(path); }
 void note_backward_fused(int fused) { g_last_fused.store(fused); }
+
+namespace {
+// y[i] = f(x[i]) for the device math of the kernels (fn 0 exp_f, 1 sigmoid_f, 2 tanh_f).
+__global__ void eval_math_kernel(int fn, const float* __restrict__ x, float* __restrict__ y, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const float v = x[i];
+    y[i] = fn == 0 ? exp_f(v) : fn == 1 ? sigmoid_f(v) : tanh_f(v);
+  }
+}
+}  // namespace
 
 }  // namespace hsl
 
@@ -102,7 +113,7 @@ long long hsl_set_spin_timeout_us(long long us) {
   return hsl::g_spin_us.exchange(us);
 }
 
-int hsl_last_recurrent_path(void) { return hsl::g_last_path; }
+int hsl_last_recurrent_path(void) { return hsl::g_last_path.load(); }
 int hsl_last_backward_fused(void) { return hsl::g_last_fused.load(); }
 
 int hsl_set_exchange_scope(int mode) { return hsl::g_exchange_scope.exchange(mode == 1 ? 1 : 0); }
@@ -133,6 +144,18 @@ int hsl_timing_collect(int kind, double* total_ms, int* count) {
   hsl::g_trecs.swap(keep);
   *total_ms = sum;
   *count = n;
+  return HSL_OK;
+}
+
+int hsl_eval_math(int fn, const float* x, float* y, size_t n, void* stream) {
+  if (fn < 0 || fn > 2) return hsl::fail(HSL_ERR_ARG, "hsl_eval_math: fn %d is not 0 (exp), 1 (sigmoid) or 2 (tanh)", fn);
+  if (n == 0) return HSL_OK;
+  if (!x || !y) return hsl::fail(HSL_ERR_ARG, "hsl_eval_math: null pointer");
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(hsl::eval_math_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), fn,
+                     x, y, n);
+  HSL_HIP(hipGetLastError());
   return HSL_OK;
 }
 

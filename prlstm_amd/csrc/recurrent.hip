@@ -330,6 +330,23 @@ __global__ __launch_bounds__(256) void step_cell_bwd_kernel(const float* __restr
 // its receive (write-back and invalidation of the XCD's L2).
 constexpr unsigned kEmpty = 0xFFFFFFFFu;
 constexpr unsigned long long kEmpty2 = ~0ull;
+
+}  // namespace
+
+// Device errors of this library since they were last read (one word per device, sticky):
+// bit 0 = a persistent kernel gave up a wait between workgroups.  Read and cleared by
+// hsl_device_errors.
+__device__ unsigned g_device_errors;
+
+namespace {
+
+// A wait gave up: the workgroup's LDS abort flag, the call's workspace flag and the
+// sticky device word are raised (vector atomics to global memory).
+__device__ __forceinline__ void raise_abort(int* abort_flag, int* err) {
+  *abort_flag = 1;
+  atomicOr(err, 1);
+  atomicOr(&g_device_errors, 1u);
+}
 __device__ __forceinline__ float canon_nan(float v) { return v == v ? v : __uint_as_float(0x7FC00000u); }
 
 // base + a byte offset held in 32 bits.  With a wave-uniform base this is the form
@@ -425,8 +442,7 @@ __device__ __forceinline__ bool words_wait(const float* base, unsigned off, cons
     }
     if (__all(ok)) return true;
     if (wall_clock64() - t0 > spin) {
-      *abort_flag = 1;
-      atomicOr(err, 1);
+      raise_abort(abort_flag, err);
       return false;
     }
     words_load<N>(base, off, need, v);
@@ -439,14 +455,6 @@ __device__ __forceinline__ unsigned xcc_id() {
   return x;
 }
 
-// Workgroup barrier that orders LDS accesses only.  __syncthreads() also waits for
-// the wave's outstanding global loads and stores; the persistent kernels keep those
-// in flight across the barrier on purpose.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // Within-wave ordering of LDS writes before reads by other lanes of the same wave.
 __device__ __forceinline__ void wave_sync() {
@@ -474,8 +482,7 @@ __device__ bool agree_placement(unsigned long long* hello, int wg, int nw, long 
       w = tag_load(hello + tid);
       if (tag_of(w) == 1u) break;
       if (wall_clock64() - t0 > spin) {
-        *abort_flag = 1;
-        atomicOr(err, 1);
+        raise_abort(abort_flag, err);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -831,8 +838,7 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
             if (min(min(m0, m1), min(m2, m3)) > t) break;
             if (abort_flag) return false;
             if (wall_clock64() - t0 > p.spin) {
-              abort_flag = 1;
-              atomicOr(p.err, 1);
+              raise_abort(&abort_flag, p.err);
               return false;
             }
             __builtin_amdgcn_s_sleep(1);
@@ -853,8 +859,30 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
   }
 }
 
+// After an abort every output the workgroup owns is NaN: the h_save/c_save rows 0..T and
+// the gact/tanh_c rows of its units for the batch slot of the calling recurrent wave (the
+// elements that wave's cell lanes write), so a loss or gradient computed from a call that
+// gave up is NaN instead of silently wrong.
+__device__ void poison_fwd(const PFwdArgs& p, int grp, int wg) {
+  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int cb = grp * p.Bg + q, cu = wg * kUnits + (lane & 15);
+  if (lane >= kUnits || q >= p.Bg || cb >= p.B || cu >= p.H) return;
+  const float nan = __uint_as_float(0x7FC00000u);
+  const size_t plane = (size_t)p.B * p.H, e = (size_t)cb * p.H + cu;
+  for (int t = 0; t <= p.T; ++t) {
+    p.h_save[t * plane + e] = nan;
+    p.c_save[t * plane + e] = nan;
+    if (t < p.T) {
+      p.tanh_c[t * plane + e] = nan;
+      *reinterpret_cast<f4*>(p.gact + (t * plane + e) * 4) = f4{nan, nan, nan, nan};
+    }
+  }
+}
+
 // XP: 512 threads; waves 4-7 compute the input projection (rec_fwd_xproj), which then
-// is not read from gih.
+// is not read from gih.  Every wave ends with one more workgroup barrier: a wave that
+// gave up a wait has set abort_flag before it (waves that left early have terminated
+// and are not waited for), so all waves agree on whether to poison their outputs.
 template <int KQ, bool XP>
 __global__ __launch_bounds__(XP ? 512 : 256, 1) void rec_fwd_persistent(PFwdArgs p) {
   constexpr int HP = 4 * KQ;
@@ -868,17 +896,23 @@ __global__ __launch_bounds__(XP ? 512 : 256, 1) void rec_fwd_persistent(PFwdArgs
   if (threadIdx.x < 4) step_flags()[threadIdx.x] = 0;  // steps whose h wave q has published
   const bool fast = agree_placement(p.hello + (size_t)grp * (HP / kUnits), wg, p.NW, p.spin, &abort_flag, p.err) &&
                     !p.device_scope;
-  if (abort_flag) return;
-  if constexpr (XP) {
-    if (threadIdx.x >= 256) {
-      rec_fwd_xproj<KQ>(p, grp, wg, xin, abort_flag);
-      return;
+  if (!abort_flag) {
+    bool proj = false;
+    if constexpr (XP) {
+      if (threadIdx.x >= 256) {
+        rec_fwd_xproj<KQ>(p, grp, wg, xin, abort_flag);
+        proj = true;
+      }
+    }
+    if (!proj) {
+      if (fast)
+        rec_fwd_body<KQ, true, XP>(p, grp, wg, red, xin, abort_flag);
+      else
+        rec_fwd_body<KQ, false, XP>(p, grp, wg, red, xin, abort_flag);
     }
   }
-  if (fast)
-    rec_fwd_body<KQ, true, XP>(p, grp, wg, red, xin, abort_flag);
-  else
-    rec_fwd_body<KQ, false, XP>(p, grp, wg, red, xin, abort_flag);
+  lds_barrier();
+  if (abort_flag && threadIdx.x < 256) poison_fwd(p, grp, wg);
 }
 
 // Per-step inputs of the persistent backward, loaded one step ahead: dout[t], c_{t-1}
@@ -1292,8 +1326,7 @@ __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg
       if (min(min(m0, m1), min(m2, m3)) > s) break;
       if (abort_flag) return false;
       if (wall_clock64() - t0 > p.spin) {
-        abort_flag = 1;
-        atomicOr(p.err, 1);
+        raise_abort(&abort_flag, p.err);
         return false;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -1345,8 +1378,56 @@ __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg
   }
 }
 
+// After an abort, a recurrent wave sets what its cell lanes own to NaN: dh0/dc0, the
+// bias partials and (when they are stored) the dgates of its batch slot and the
+// workgroup's units.
+__device__ void poison_bwd(const PBwdArgs& p, int grp, int wg) {
+  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int cb = grp * p.Bg + q, cu = wg * kUnits + (lane & 15);
+  if (lane >= kUnits || q >= p.Bg || cb >= p.B || cu >= p.H) return;
+  const float nan = __uint_as_float(0x7FC00000u);
+  const int H = p.H;
+  const size_t e = (size_t)cb * H + cu;
+  if (p.dh0) p.dh0[e] = nan;
+  if (p.dc0) p.dc0[e] = nan;
+  for (int gt = 0; gt < 4; ++gt) p.db_part[(size_t)cb * 4 * H + gt * H + cu] = (double)nan;
+  if (p.store_dg)
+    for (int t = 0; t < p.T; ++t)
+      for (int gt = 0; gt < 4; ++gt) p.dgates[((size_t)t * p.B + cb) * 4 * H + gt * H + cu] = nan;
+}
+
+// ... and a weight-gradient wave sets every element of the planes it writes to NaN: its
+// 32-column tiles of the workgroup's 64 rows in the group's dW_hh_s plane of every chunk
+// and, with XT > 0, in the group's fp64 dW_ih plane.
+template <int KQ, int XT>
+__device__ void poison_wgrad(const PBwdArgs& p, int grp, int wg) {
+  constexpr int HT = KQ >= 32 ? KQ / 32 : 1;
+  const int lane = threadIdx.x & 63, w = (threadIdx.x >> 6) - 4;
+  const int H = p.H, D = p.D;
+  const float nan = __uint_as_float(0x7FC00000u);
+  const int chunks = (p.T + p.TS - 1) / p.TS;
+  for (int r = lane >> 5; r < 64; r += 2) {
+    const int u = wg * kUnits + (r & 15);
+    if (u >= H) continue;
+    const size_t row = (size_t)(r >> 4) * H + u;
+    for (int i = 0; i < HT; ++i) {
+      const int c = (w + 4 * i) * 32 + (lane & 31);
+      if (c >= H) continue;
+      for (int ch = 0; ch < chunks; ++ch) p.wph[(((size_t)ch * p.NG + grp) * 4 * H + row) * H + c] = nan;
+    }
+    if constexpr (XT > 0) {
+      for (int i = 0; i < XT; ++i) {
+        const int c = (w + 4 * i) * 32 + (lane & 31);
+        if (c < D) p.wpx[((size_t)grp * 4 * H + row) * D + c] = (double)nan;
+      }
+    }
+  }
+}
+
 // XT < 0: 256 threads, recurrent waves only (weight gradients by separate GEMMs).
 // XT >= 0: 512 threads; waves 4-7 accumulate dW_hh_s and, when XT > 0, dW_ih.
+// As in the forward, every wave ends with one more workgroup barrier and then poisons
+// its outputs if any wave of the workgroup gave up a wait.
 template <int KQ, int XT>
 __global__ __launch_bounds__(XT >= 0 ? 512 : 256, 1) void rec_bwd_persistent(PBwdArgs p) {
   constexpr int NWMAX = 4 * KQ / kUnits;
@@ -1359,19 +1440,33 @@ __global__ __launch_bounds__(XT >= 0 ? 512 : 256, 1) void rec_bwd_persistent(PBw
   if (threadIdx.x < 4) step_flags()[threadIdx.x] = 0;  // steps whose products wave q has issued
   const bool fast = agree_placement(p.hello + (size_t)grp * NWMAX, wg, p.NW, p.spin, &abort_flag, p.err) &&
                     !p.device_scope;
-  if (abort_flag) return;
-  if constexpr (GW) {
-    if (threadIdx.x >= 256) {
-      extern __shared__ double xacc[];  // [64][256] fp64 dW_ih accumulator (dynamic LDS)
-      rec_bwd_wgrad<KQ, (XT > 0 ? XT : 0)>(p, grp, wg, dgl, xacc, abort_flag);
-      return;
+  const bool wgrad_wave = GW && threadIdx.x >= 256;
+  if (!abort_flag) {
+    if constexpr (GW) {
+      if (wgrad_wave) {
+        extern __shared__ double xacc[];  // [64][256] fp64 dW_ih accumulator (dynamic LDS)
+        rec_bwd_wgrad<KQ, (XT > 0 ? XT : 0)>(p, grp, wg, dgl, xacc, abort_flag);
+      } else {
+        __builtin_amdgcn_s_setprio(2);  // the recurrent chain first when both waves can issue
+      }
     }
-    __builtin_amdgcn_s_setprio(2);  // the recurrent chain first when both waves can issue
+    if (!wgrad_wave) {
+      if (fast)
+        rec_bwd_body<KQ, true, GW>(p, grp, wg, dgl, abort_flag);
+      else
+        rec_bwd_body<KQ, false, GW>(p, grp, wg, dgl, abort_flag);
+    }
   }
-  if (fast)
-    rec_bwd_body<KQ, true, GW>(p, grp, wg, dgl, abort_flag);
-  else
-    rec_bwd_body<KQ, false, GW>(p, grp, wg, dgl, abort_flag);
+  lds_barrier();
+  if (abort_flag) {
+    if constexpr (GW) {
+      if (wgrad_wave) {
+        poison_wgrad<KQ, (XT > 0 ? XT : 0)>(p, grp, wg);
+        return;
+      }
+    }
+    poison_bwd(p, grp, wg);
+  }
 }
 
 // ---------------------------------------------------------------------------------
@@ -1670,9 +1765,30 @@ int bias_grads_from_parts(const double* db_part, int B, const double* rowdot, co
 
 }  // namespace hsl
 
+namespace hsl {
+namespace {
+__global__ void clear_device_errors_kernel() { g_device_errors = 0u; }
+}  // namespace
+}  // namespace hsl
+
 using namespace hsl;
 
 extern "C" {
+
+int hsl_device_errors(int* flags, int clear, void* stream) {
+  if (!flags) return fail(HSL_ERR_ARG, "hsl_device_errors: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  unsigned v = 0;
+  HSL_HIP(hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(g_device_errors), sizeof(v), 0, hipMemcpyDeviceToHost, s));
+  HSL_HIP(hipStreamSynchronize(s));
+  if (clear && v) {
+    hipLaunchKernelGGL(clear_device_errors_kernel, dim3(1), dim3(1), 0, s);
+    HSL_HIP(hipGetLastError());
+    HSL_HIP(hipStreamSynchronize(s));
+  }
+  *flags = static_cast<int>(v);
+  return HSL_OK;
+}
 
 size_t hsl_rec_fwd_ws_bytes(int T, int B, int D, int H) {
   (void)D;

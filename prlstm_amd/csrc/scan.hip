@@ -37,7 +37,8 @@ template <int NW, int L>
 __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restrict__ gates, const float* __restrict__ c0,
                                                           float eps, float* __restrict__ out, float* __restrict__ cseq,
                                                           int T, int B, int H) {
-  __shared__ float sA[NW][64], sV[NW][64], sC[64];
+  __shared__ float2 sAV[NW][64];  // each wave's composed map (A, V) of the chunk
+  __shared__ float sC[64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int C = B * H;
   const int ch = blockIdx.x * 64 + lane;
@@ -79,23 +80,33 @@ __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restri
         V = fv[s] * V + bv[s];
       }
     }
-    sA[w][lane] = A;
-    sV[w][lane] = V;
-    __syncthreads();
+    sAV[w][lane] = float2{A, V};
+    lds_barrier();
+    // carry-in: the chunk's carry through the maps of waves 0 .. w-1, applied in order;
+    // the maps are read four at a time (one LDS latency per four, where a serial loop
+    // would wait for each read; an unrolled loop over all of them spilled registers)
     float c = sC[lane];
-    for (int u = 0; u < w; ++u) c = sA[u][lane] * c + sV[u][lane];
+#pragma unroll 1
+    for (int u0 = 0; u0 < w; u0 += 4) {
+      float2 m[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m[i] = sAV[min(u0 + i, NW - 1)][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (u0 + i < w) c = m[i].x * c + m[i].y;
+    }
 #pragma unroll
     for (int s = 0; s < L; ++s) {
       const int t = k * CH + w * L + s;
       if (t < T) {
         c = fv[s] * c + bv[s];
-        if (ok) {
-          __builtin_nontemporal_store(ov[s] * tanh_f(c), out + (size_t)t * ostride + ch);
+        if (ok) {  // c >= eps > 0 (a positive combination of positive terms)
+          __builtin_nontemporal_store(ov[s] * tanh_pos_f(c), out + (size_t)t * ostride + ch);
           __builtin_nontemporal_store(c, cseq + (size_t)t * ostride + ch);
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (w == NW - 1) sC[lane] = c;
 #pragma unroll
     for (int s = 0; s < L; ++s)
@@ -113,7 +124,8 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
     const float* __restrict__ gates, const float* __restrict__ c0, const float* __restrict__ cseq,
     const float* __restrict__ dout, const float* __restrict__ dh_n, const float* __restrict__ dc_n, float eps,
     float* __restrict__ dgates, double* __restrict__ db_part, float* __restrict__ dc0, int T, int B, int H) {
-  __shared__ float sA[NW][64], sV[NW][64], sG[64];
+  __shared__ float2 sAV[NW][64];  // each wave's composed reverse map (A, V) of the chunk
+  __shared__ float sG[64];
   __shared__ double sdb[NW][4][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int C = B * H;
@@ -157,18 +169,23 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
   for (int k = nchunks - 1; k >= 0; --k) {
     if (k > 0) load(k - 1, nxt, nxt_fn, nxt_cp);
     const int ws = k * CH + w * L;
-    // f~_{t+1} for each step (0 beyond T), e_t
-    float fn[L], ev[L];
+    // sigma(z_f), sigma(z_o) and tanh(c) of each step, computed once and used by both
+    // passes; f~_{t+1} (0 beyond T) is step s+1's sigma(z_f), e_t
+    float fgv[L], ogv[L], tcv[L], fn[L], ev[L];
+#pragma unroll
+    for (int s = 0; s < L; ++s) {
+      fgv[s] = sigmoid_f(cur[1][s]);
+      ogv[s] = sigmoid_f(cur[3][s]);
+      tcv[s] = tanh_f(cur[4][s]);
+    }
+    const float fg_after = sigmoid_f(cur_fn);
 #pragma unroll
     for (int s = 0; s < L; ++s) {
       const int t = ws + s;
-      const float znext = (s + 1 < L) ? cur[1][s + 1] : cur_fn;
-      fn[s] = (t + 1 < T) ? fmaxf(sigmoid_f(znext), eps) : 0.f;
-      const float og = sigmoid_f(cur[3][s]);
-      const float tc = tanh_f(cur[4][s]);
+      fn[s] = (t + 1 < T) ? fmaxf(s + 1 < L ? fgv[s + 1] : fg_after, eps) : 0.f;
       float d = cur[5][s];
       if (t == T - 1) d = d + dhn;
-      float e = d * og * (1.0f - tc * tc);
+      float e = d * ogv[s] * (1.0f - tcv[s] * tcv[s]);
       if (t == T - 1) e = e + dcn;
       ev[s] = (t < T) ? e : 0.f;
     }
@@ -180,19 +197,24 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
         A = fn[s] * A;
       }
     }
-    sA[w][lane] = A;
-    sV[w][lane] = V;
-    __syncthreads();
+    sAV[w][lane] = float2{A, V};
+    lds_barrier();
+    // carry-in from the later waves NW-1 .. w+1, applied in order; with 8 waves all maps
+    // fit in registers and are read at once (one LDS latency instead of one per map)
     float G = sG[lane];
-    for (int u = NW - 1; u > w; --u) G = sA[u][lane] * G + sV[u][lane];
+    float2 m[NW - 1];
+#pragma unroll
+    for (int u = 1; u < NW; ++u) m[u - 1] = sAV[u][lane];
+#pragma unroll
+    for (int u = NW - 1; u >= 1; --u)
+      if (u > w) G = m[u - 1].x * G + m[u - 1].y;
 #pragma unroll
     for (int s = L - 1; s >= 0; --s) {
       const int t = ws + s;
       if (t < T) {
         G = ev[s] + fn[s] * G;
-        const float ig = sigmoid_f(cur[0][s]), fg = sigmoid_f(cur[1][s]);
-        const float gg = sigmoid_f(cur[2][s]), og = sigmoid_f(cur[3][s]);
-        const float tc = tanh_f(cur[4][s]);
+        const float ig = sigmoid_f(cur[0][s]), gg = sigmoid_f(cur[2][s]);
+        const float fg = fgv[s], og = ogv[s], tc = tcv[s];
         const float cprev = s > 0 ? cur[4][s - 1] : cur_cp;
         float d = cur[5][s];
         if (t == T - 1) d = d + dhn;
@@ -219,7 +241,7 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (w == 0) sG[lane] = G;
 #pragma unroll
     for (int s = 0; s < L; ++s)

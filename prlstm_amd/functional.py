@@ -21,7 +21,9 @@ _debug_checks = False
 
 def debug_checks(enabled=True):
     """When enabled, every recurrent call synchronises and raises if a persistent
-    kernel reported a timed-out wait (the device error flag of its workspace)."""
+    kernel reported a timed-out wait (the device error flag of its workspace, and the
+    sticky device word that ``prlstm_amd.check_errors`` reads).  Without it a timed-out
+    call is still not silent: its outputs are NaN."""
     global _debug_checks
     _debug_checks = bool(enabled)
 
@@ -32,8 +34,9 @@ def _poll(ws, device):
     flag = ctypes.c_int(0)
     _lib.call("hsl_poll_error", _lib.ptr(ws), ctypes.byref(flag), _lib.stream_of(device))
     if flag.value:
+        _lib.device_errors(device, clear=True)
         raise RuntimeError(f"a persistent kernel reported device error flag {flag.value} "
-                           "(a wait between workgroups timed out)")
+                           "(a wait between workgroups timed out); its outputs are NaN")
 
 
 def _check(x, h0, c0, w_ih, w_hh, b_ih, b_hh, a):

@@ -67,23 +67,45 @@ def test_half_module_equals_rounded_fp32(dev, dtype, parallel):
             same(n, g16[n], g32[n])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("parallel", [False, True])
-def test_bf16_module_within_reference_tolerance(dev, parallel):
-    """The reference's bf16 bar (max |diff| < 1e-2) against the fp64 oracle."""
+def test_half_module_within_reference_tolerance(dev, parallel, dtype):
+    """Against the fp64 oracle on the same (16-bit) operands.  bf16: the reference's bar,
+    max |diff| < 1e-2 (test_parallel.py:22-24).  fp16 (no bar in the reference): 1e-3,
+    the same bar scaled to fp16's 3 more significand bits (its half-ulp at 1 is 4.9e-4).
+    Gradients (x and every parameter the mode trains) by the same bar, relative to the
+    largest magnitude of each gradient (they are sums over T*B terms)."""
     T, B, D, H = 32, 4, 16, 24
+    bar = 1e-2 if dtype == torch.bfloat16 else 1e-3
+    print(f"half {dtype} parallel={parallel} vs fp64 oracle", flush=True)
     torch.manual_seed(0)
-    m16 = prlstm_amd.HeadStartLSTM(D, H, parallel=parallel).to(dev, torch.bfloat16)
-    x16 = torch.randn(T, B, D, device=dev).to(torch.bfloat16)
+    m16 = prlstm_amd.HeadStartLSTM(D, H, parallel=parallel).to(dev, dtype)
+    with torch.no_grad():
+        m16.a.fill_(0.25)
+    x16 = torch.randn(T, B, D, device=dev).to(dtype).requires_grad_(True)
     out16, (h16, c16) = m16(x16)
+    out16.float().sum().backward()
     ref = O.RefHeadStartLSTM(D, H, parallel=parallel).double()
     with torch.no_grad():
         for pr, p16 in zip(ref.parameters(), m16.parameters()):
             pr.copy_(p16.double().cpu())
-    out64, (h64, c64) = ref(x16.double().cpu())
+    x64 = x16.detach().double().cpu().requires_grad_(True)
+    out64, (h64, c64) = ref(x64)
+    out64.sum().backward()
     for name, got, want in [("out", out16, out64), ("h_n", h16, h64), ("c_n", c16, c64)]:
         d = (got.double().cpu() - want).abs().max().item()
-        print(f"  {name} max |bf16 - fp64| = {d:.3e}", flush=True)
-        assert d < 1e-2, name
+        print(f"  {name} max |{dtype} - fp64| = {d:.3e}", flush=True)
+        assert d < bar, name
+    grads = [("dx", x16.grad, x64.grad)]
+    grads += [("d" + n, p.grad, q.grad) for (n, p), q in zip(m16.named_parameters(), ref.parameters())]
+    for name, got, want in grads:
+        if want is None:
+            assert got is None, name
+            continue
+        assert got.dtype == dtype, name
+        d = (got.double().cpu() - want).abs().max().item() / max(want.abs().max().item(), 1e-30)
+        print(f"  {name} max |{dtype} - fp64| / max|fp64| = {d:.3e}", flush=True)
+        assert d < bar, name
 
 
 @pytest.mark.parametrize("fmt", [0, 1])

@@ -1,0 +1,102 @@
+"""The kernels' device math (exp_f, sigmoid_f, tanh_f in csrc/hsl_internal.h) against
+fp64 torch on the CPU, elementwise over a dense sweep, through ``hsl_eval_math``.
+
+The reference computes the gates with ``torch.sigmoid`` and the cell output with
+``torch.tanh`` (``_torch.py:29-34``).  Bounds, in units in the last place of the fp32
+result (ulp of the fp64 value, 2^-149 below the normal range):
+  exp      <= 1.5 ulp for results in the normal range (v_exp_f32 plus the rounding of
+           x log2 e, which is put back; measured 1.21);
+  sigmoid  <= 3.5 ulp (exp, the rounding of 1 + e and v_rcp_f32; measured 3.10, torch's
+           own fp32 CPU sigmoid 2.47);
+  tanh     <= 2 ulp (below |x| = 0.625 an odd polynomial, measured 0.53 there; above
+           it 1 - 2/(1 + e^{2|x|}), whose cancellation is bounded there; measured 1.49).
+Results below the normal range (exp(x < -87.3), sigmoid(x < -87.3)) may be flushed:
+their absolute error must stay below 2^-126.  Special values: exp(+-inf) = inf / 0,
+sigmoid(+-inf) = 1 / 0, tanh(+-inf) = +-1, NaN in gives NaN out.
+"""
+
+import math
+
+import pytest
+import torch
+
+from prlstm_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+FN = {"exp": 0, "sigmoid": 1, "tanh": 2}
+BOUND = {"exp": 1.5, "sigmoid": 3.5, "tanh": 2.0}
+TORCH64 = {"exp": torch.exp, "sigmoid": torch.sigmoid, "tanh": torch.tanh}
+
+
+def _dev_eval(name, x, dev):
+    xd = x.to(dev)
+    y = torch.empty_like(xd)
+    _lib.call("hsl_eval_math", FN[name], _lib.ptr(xd), _lib.ptr(y), xd.numel(), _lib.stream_of(dev))
+    torch.cuda.synchronize()
+    return y.cpu()
+
+
+def _ulp(ref):
+    """fp32 ulp of each fp64 value (2^-149 below the normal range)."""
+    a = ref.abs().clamp_min(2.0 ** -126)
+    e = torch.floor(torch.log2(a))
+    return torch.exp2(e - 23)
+
+
+def _sweep():
+    small = torch.logspace(-8, -1, 20001, dtype=torch.float64)
+    mid = torch.linspace(-20, 20, 400001, dtype=torch.float64)
+    wide = torch.linspace(-100, 100, 200001, dtype=torch.float64)
+    big = torch.tensor([0.625, 0.62499, 0.62501, 1.0, 5.0, 9.0, 20.0, 44.0, 80.0, 87.0, 88.0, 88.7, 89.0,
+                        100.0, 1e4, 3e38], dtype=torch.float64)
+    x = torch.cat([small, -small, mid, wide, big, -big]).float()
+    return x[torch.isfinite(x)]
+
+
+@pytest.mark.parametrize("name", ["exp", "sigmoid", "tanh"])
+def test_device_math_ulp(dev, name):
+    x = _sweep()
+    y = _dev_eval(name, x, dev).double()
+    ref = TORCH64[name](x.double())
+    cpu32 = TORCH64[name](x).double()
+    finite = torch.isfinite(ref) & (ref.abs() < 3.4e38)
+    normal = finite & (ref.abs() >= 2.0 ** -126)
+    err = (y - ref).abs() / _ulp(ref)
+    worst = float(err[normal].max())
+    cpu_worst = float(((cpu32 - ref).abs() / _ulp(ref))[normal].max())
+    small = normal & (x.abs() < 0.1)
+    print(f"{name}: max {worst:.3f} ulp (|x| < 0.1: {float(err[small].max()):.3f}), "
+          f"torch CPU fp32 {cpu_worst:.3f} ulp", flush=True)
+    assert worst <= BOUND[name], (name, worst, float(x[normal][err[normal].argmax()]))
+    sub = finite & ~normal
+    if bool(sub.any()):
+        assert float((y[sub] - ref[sub]).abs().max()) < 2.0 ** -126
+    if name == "exp":  # results beyond fp32's range are inf
+        over = x.double() > 88.73
+        assert bool(torch.isinf(y[over]).all())
+
+
+def test_device_math_small_arguments_relative(dev):
+    """tanh near zero keeps its relative accuracy (a 1 - 2/(1 + e^{2x}) form loses it:
+    1.7e-4 relative error at x = 1e-4); sigmoid(x) - 1/2 and exp(x) - 1 are not asked of
+    these functions, so only tanh is checked here down to 1e-8."""
+    x = torch.tensor([1e-8, -1e-8, 1e-6, -1e-6, 1e-4, -1e-4, 3e-3, 0.1], dtype=torch.float32)
+    y = _dev_eval("tanh", x, dev).double()
+    ref = torch.tanh(x.double())
+    rel = ((y - ref).abs() / ref.abs()).max().item()
+    assert rel < 2 * 2.0 ** -24, rel
+
+
+@pytest.mark.parametrize("name", ["exp", "sigmoid", "tanh"])
+def test_device_math_special_values(dev, name):
+    x = torch.tensor([math.inf, -math.inf, math.nan, 0.0, -0.0], dtype=torch.float32)
+    y = _dev_eval(name, x, dev)
+    want = {"exp": [math.inf, 0.0, math.nan, 1.0, 1.0],
+            "sigmoid": [1.0, 0.0, math.nan, 0.5, 0.5],
+            "tanh": [1.0, -1.0, math.nan, 0.0, 0.0]}[name]
+    for got, w, xi in zip(y.tolist(), want, x.tolist()):
+        if math.isnan(w):
+            assert math.isnan(got), (name, xi, got)
+        else:
+            assert got == w, (name, xi, got)

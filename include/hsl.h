@@ -118,7 +118,12 @@ int hsl_eval_math(int fn, const float* x, float* y, size_t n, void* stream);
  * Recurrent mode: replaces HeadStartLSTMTorchFn (_torch.py:86-170).
  * ------------------------------------------------------------------------- */
 
-/* Workspace for hsl_rec_fwd: input-gate buffer [T,B,4H], exchange buffers. */
+/* Workspace for hsl_rec_fwd on the current device: the exchange buffers of the
+ * persistent kernel, plus the input-gate buffer [T,B,4H] when the input projection
+ * is not fused into it, or the per-step path's buffers when that path runs.  The
+ * size assumes a 16-byte aligned x (the fused projection reads x in 16-byte pieces;
+ * with an unaligned x the call needs the input-gate buffer too and reports the
+ * size).  Without a usable device, the size that covers every path. */
 size_t hsl_rec_fwd_ws_bytes(int T, int B, int D, int H);
 
 /* Forward: _torch.py:86-131 (a-prescale :91-94, input GEMM :96, time loop
@@ -134,9 +139,15 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0,
                 float* h_save, float* c_save, float* gact, float* tanh_c,
                 void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream);
 
-/* Workspace for hsl_rec_bwd: dgates [T,B,4H], exchange buffers, GEMM
- * split-K partials, fp64 reduction buffers. */
+/* Workspace for hsl_rec_bwd on the current device: fp64 reduction buffers, the
+ * exchange buffers or the per-step buffers of the path that runs, the weight-
+ * gradient planes / GEMM split-K partials, and dgates [T,B,4H] when a product reads
+ * them (dx requested, or dW_ih not accumulated inside the persistent kernel).
+ * hsl_rec_bwd_ws_bytes is enough for any call (dx requested); _for gives the size for
+ * a call with (with_dx != 0) == (dx != NULL).  Without a usable device, the size
+ * that covers every path. */
 size_t hsl_rec_bwd_ws_bytes(int T, int B, int D, int H);
+size_t hsl_rec_bwd_ws_bytes_for(int T, int B, int D, int H, int with_dx);
 
 /* Backward: _torch.py:133-170 (reverse loop :143-150, batched GEMMs :153-162,
  * a-unscale :165-168).  dout [T,B,H], dh_n/dc_n [B,H].  Writes dx [T,B,D] (skipped

@@ -36,6 +36,7 @@ SIGNATURES = {
     "hsl_rec_fwd_ws_bytes": (_Z, [_I, _I, _I, _I]),
     "hsl_rec_fwd": (_I, [_P] * 12 + [_P, _Z, _I, _I, _I, _I, _P]),
     "hsl_rec_bwd_ws_bytes": (_Z, [_I, _I, _I, _I]),
+    "hsl_rec_bwd_ws_bytes_for": (_Z, [_I, _I, _I, _I, _I]),
     "hsl_rec_bwd": (_I, [_P] * 20 + [_P, _Z, _I, _I, _I, _I, _P]),
     "hsl_par_fwd": (_I, [_P, _P, _P, _P, _F, _P, _P, _P, _I, _I, _I, _I, _P]),
     "hsl_par_fwd_b16": (_I, [_P, _P, _P, _P, _F, _P, _P, _P, _I, _I, _I, _I, _I, _P]),

@@ -1638,37 +1638,58 @@ int copy_f32_impl(float* dst, const float* src, size_t n, hipStream_t s) {
 // Workspace layouts.  The int error flag sits at offset 0 of both.
 struct FwdWs {
   int* err;
-  float* gih;                 // [T*B*4H]
   float* xbuf;                // [4*NG*4*Hp] (persistent)
   size_t xfloats;
   unsigned long long* hello;  // [NG*Hp/16]  (persistent)
   size_t hwords;
+  float* gih;                 // [T*B*4H]    (input projection not fused)
   float* w_perm;              // [4H*H]      (per-step)
   float* bs;                  // [4H]        (per-step)
   float* part;                // [S*B*4H]    (per-step split-K planes)
 };
 
-size_t carve_fwd(void* ws, size_t cap, int T, int B, int H, FwdWs* o) {
+// Which parts of the forward workspace a call uses: the persistent exchange buffers, the
+// [T,B,4H] input-gate buffer (not when the projection is fused into the persistent
+// kernel) and the per-step buffers.  All three when the path is not known (no device).
+struct FwdNeeds {
+  bool xch = true, gih = true, step = true;
+};
+
+size_t carve_fwd(void* ws, size_t cap, int T, int B, int H, FwdNeeds nd, FwdWs* o) {
   Carver c(ws, cap);
+  *o = FwdWs{};
   o->err = c.take<int>(64);
-  o->gih = c.take<float>((size_t)T * B * 4 * H);
   const int kq = pick_kq(H);
-  const size_t ng = (size_t)(B + 3) / 4;
-  o->hwords = kq ? ng * (size_t)(4 * kq / kUnits) : 0;
-  o->xfloats = kq ? 4 * ng * 4 * (size_t)(4 * kq) : 0;
-  o->xbuf = c.take<float>(o->xfloats);
-  o->hello = c.take<unsigned long long>(o->hwords);
-  o->w_perm = c.take<float>((size_t)4 * H * H);
-  o->bs = c.take<float>((size_t)4 * H);
-  int kps;
-  const int sp = step_splits(B, 4 * H, H, &kps);
-  o->part = c.take<float>(sp > 1 ? (size_t)sp * B * 4 * H : 0);
+  if (nd.xch && kq) {
+    const size_t ng = (size_t)(B + 3) / 4;
+    o->hwords = ng * (size_t)(4 * kq / kUnits);
+    o->xfloats = 4 * ng * 4 * (size_t)(4 * kq);
+    o->xbuf = c.take<float>(o->xfloats);
+    o->hello = c.take<unsigned long long>(o->hwords);
+  }
+  if (nd.gih) o->gih = c.take<float>((size_t)T * B * 4 * H);
+  if (nd.step) {
+    o->w_perm = c.take<float>((size_t)4 * H * H);
+    o->bs = c.take<float>((size_t)4 * H);
+    int kps;
+    const int sp = step_splits(B, 4 * H, H, &kps);
+    o->part = c.take<float>(sp > 1 ? (size_t)sp * B * 4 * H : 0);
+  }
   return c.off;
+}
+
+// The workspace parts of a forward call with this plan; the fused projection needs a
+// 16-byte aligned x.
+FwdNeeds fwd_needs(const PersistentPlan& pl, bool x_aligned) {
+  FwdNeeds nd;
+  nd.xch = pl.ok;
+  nd.gih = !(pl.ok && pl.XP && x_aligned);
+  nd.step = !pl.ok;
+  return nd;
 }
 
 struct BwdWs {
   int* err;
-  float* dgates;             // [T*B*4H]
   double* db_part;           // [B*4H]
   double* rowdot;            // [4H]
   float* dc;                 // [B*H]   (per-step)
@@ -1680,6 +1701,7 @@ struct BwdWs {
   size_t hwords;
   float* gemm;               // shared by the weight-gradient GEMMs
   size_t gemm_bytes;
+  float* dgates;             // [T*B*4H] (when they feed a product)
 };
 
 size_t gemm_region_bytes(int T, int B, int D, int H) {
@@ -1701,27 +1723,48 @@ size_t gemm_region_bytes(int T, int B, int D, int H) {
   return need;
 }
 
-size_t carve_bwd(void* ws, size_t cap, int T, int B, int D, int H, BwdWs* o) {
+// Which parts of the backward workspace a call uses: the persistent exchange buffers,
+// the per-step buffers and the [T,B,4H] dgates (only when a product reads them: dx, or
+// dW_ih when the persistent kernel does not accumulate it).  All when the path is not
+// known (no device).
+struct BwdNeeds {
+  bool xch = true, step = true, dgates = true;
+};
+
+BwdNeeds bwd_needs(const PersistentPlan& pl, bool with_dx) {
+  BwdNeeds nd;
+  nd.xch = pl.ok;
+  nd.step = !pl.ok;
+  nd.dgates = !(pl.ok && pl.XT > 0) || with_dx;
+  return nd;
+}
+
+size_t carve_bwd(void* ws, size_t cap, int T, int B, int D, int H, BwdNeeds nd, BwdWs* o) {
   Carver c(ws, cap);
+  *o = BwdWs{};
   o->err = c.take<int>(64);
-  o->dgates = c.take<float>((size_t)T * B * 4 * H);
   o->db_part = c.take<double>((size_t)B * 4 * H);
   o->rowdot = c.take<double>((size_t)4 * H);
-  o->dc = c.take<float>((size_t)B * H);
-  o->w_s = c.take<float>((size_t)4 * H * H);
-  int kps;
-  const int sp = step_splits(B, H, 4 * H, &kps);
-  o->part = c.take<float>(sp > 1 ? (size_t)sp * B * H : 0);
+  if (nd.step) {
+    o->dc = c.take<float>((size_t)B * H);
+    o->w_s = c.take<float>((size_t)4 * H * H);
+    int kps;
+    const int sp = step_splits(B, H, 4 * H, &kps);
+    o->part = c.take<float>(sp > 1 ? (size_t)sp * B * H : 0);
+  }
   const int kq = pick_kq(H);
-  const size_t ng = (size_t)(B + 3) / 4;
-  const size_t nwmax = kq ? (size_t)(4 * kq / kUnits) : 0;
-  const size_t per = (nwmax + 3) / 4;
-  o->hwords = ng * nwmax;
-  o->pfloats = 3 * ng * nwmax * 4 * 64 * per;
-  o->pbuf = c.take<float>(o->pfloats);
-  o->hello = c.take<unsigned long long>(o->hwords);
+  if (nd.xch && kq) {
+    const size_t ng = (size_t)(B + 3) / 4;
+    const size_t nwmax = (size_t)(4 * kq / kUnits);
+    const size_t per = (nwmax + 3) / 4;
+    o->hwords = ng * nwmax;
+    o->pfloats = 3 * ng * nwmax * 4 * 64 * per;
+    o->pbuf = c.take<float>(o->pfloats);
+    o->hello = c.take<unsigned long long>(o->hwords);
+  }
   o->gemm_bytes = gemm_region_bytes(T, B, D, H);
   o->gemm = c.take<float>(o->gemm_bytes / sizeof(float) + 1);
+  if (nd.dgates) o->dgates = c.take<float>((size_t)T * B * 4 * H);
   return c.off;
 }
 
@@ -1791,10 +1834,12 @@ int hsl_device_errors(int* flags, int clear, void* stream) {
 }
 
 size_t hsl_rec_fwd_ws_bytes(int T, int B, int D, int H) {
-  (void)D;
-  if (T < 0 || B < 0 || H < 0) return 0;
+  if (T < 0 || B < 0 || D < 0 || H < 0) return 0;
   FwdWs w;
-  return carve_fwd(nullptr, 0, T, B, H, &w);
+  FwdNeeds nd;  // every part when the path cannot be planned (no device)
+  PersistentPlan pl;
+  if (B > 0 && H > 0 && plan_persistent(B, H, D, false, &pl) == HSL_OK) nd = fwd_needs(pl, true);
+  return carve_fwd(nullptr, 0, T, B, H, nd, &w);
 }
 
 int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w_ih, const float* w_hh,
@@ -1805,14 +1850,17 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
   if (B == 0 || H == 0) return HSL_OK;
   if (!w_hh || !b_hh || !a || !h_save || !c_save || (T > 0 && (!x || !w_ih || !b_ih || !gact || !tanh_c)))
     return fail(HSL_ERR_ARG, "hsl_rec_fwd: null pointer");
-  FwdWs w;
-  const size_t need = carve_fwd(ws, ws_bytes, T, B, H, &w);
-  if (!ws || ws_bytes < need) return fail(HSL_ERR_ARG, "hsl_rec_fwd: workspace %zu bytes, need %zu", ws_bytes, need);
-
   PersistentPlan pl;
   HSL_CHECK(plan_persistent(B, H, D, false, &pl));
   if (recurrent_path_mode() == 2 && !pl.ok)
     return fail(HSL_ERR_UNSUPPORTED, "persistent path does not fit (B=%d H=%d)", B, H);
+  const bool x_aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0;
+  if (pl.XP && !x_aligned) pl.XP = false;  // the fused projection loads x in 16-byte pieces
+  FwdWs w;
+  const size_t need = carve_fwd(ws, ws_bytes, T, B, H, fwd_needs(pl, x_aligned), &w);
+  if (!ws || ws_bytes < need)
+    return fail(HSL_ERR_ARG, "hsl_rec_fwd: workspace %zu bytes, need %zu%s", ws_bytes, need,
+                pl.ok && !x_aligned ? " (x is not 16-byte aligned, so the input-gate buffer is needed)" : "");
 
   if (pl.ok && T > 0)
     HSL_CHECK(prepare_persistent(w.err, w.xbuf, w.xfloats, w.hello, w.hwords, s));
@@ -1823,7 +1871,6 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
     HSL_CHECK(copy_f32(c_save, c0, (size_t)B * H, s));
     return HSL_OK;
   }
-  if (pl.XP && reinterpret_cast<uintptr_t>(x) % 16 != 0) pl.XP = false;  // 16-byte x loads
   if (!(pl.ok && pl.XP)) {
     // input projection for all T at once (_torch.py:96)
     GemmDesc g1{x, w_ih, b_ih, w.gih, T * B, 4 * H, D, D, D, 4 * H, 0, 1};
@@ -1888,11 +1935,16 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
   return HSL_OK;
 }
 
-size_t hsl_rec_bwd_ws_bytes(int T, int B, int D, int H) {
+size_t hsl_rec_bwd_ws_bytes_for(int T, int B, int D, int H, int with_dx) {
   if (T < 0 || B < 0 || D < 0 || H < 0) return 0;
   BwdWs w;
-  return carve_bwd(nullptr, 0, T, B, D, H, &w);
+  BwdNeeds nd;  // every part when the path cannot be planned (no device)
+  PersistentPlan pl;
+  if (B > 0 && H > 0 && plan_persistent(B, H, D, true, &pl) == HSL_OK) nd = bwd_needs(pl, with_dx != 0);
+  return carve_bwd(nullptr, 0, T, B, D, H, nd, &w);
 }
+
+size_t hsl_rec_bwd_ws_bytes(int T, int B, int D, int H) { return hsl_rec_bwd_ws_bytes_for(T, B, D, H, 1); }
 
 int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const float* x, const float* h_save,
                 const float* c_save, const float* gact, const float* tanh_c, const float* w_ih, const float* w_hh,
@@ -1905,8 +1957,12 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     return fail(HSL_ERR_ARG, "hsl_rec_bwd: null pointer");
   if (T > 0 && B > 0 && H > 0 && (!dout || !x || !h_save || !c_save || !gact || !tanh_c))
     return fail(HSL_ERR_ARG, "hsl_rec_bwd: null pointer");
+  PersistentPlan pl;
+  if (T > 0 && B > 0 && H > 0) HSL_CHECK(plan_persistent(B, H, D, true, &pl));
+  if (T > 0 && B > 0 && H > 0 && recurrent_path_mode() == 2 && !pl.ok)
+    return fail(HSL_ERR_UNSUPPORTED, "persistent path does not fit (B=%d H=%d)", B, H);
   BwdWs w;
-  const size_t need = carve_bwd(ws, ws_bytes, T, B, D, H, &w);
+  const size_t need = carve_bwd(ws, ws_bytes, T, B, D, H, bwd_needs(pl, dx != nullptr), &w);
   if (!ws || ws_bytes < need) return fail(HSL_ERR_ARG, "hsl_rec_bwd: workspace %zu bytes, need %zu", ws_bytes, need);
   const int TB = T * B;
   const size_t plane = (size_t)B * H, plane4 = (size_t)B * 4 * H;
@@ -1921,11 +1977,6 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     if (dc0) HSL_CHECK(copy_f32(dc0, dc_n, plane, s));
     return HSL_OK;
   }
-
-  PersistentPlan pl;
-  HSL_CHECK(plan_persistent(B, H, D, true, &pl));
-  if (recurrent_path_mode() == 2 && !pl.ok)
-    return fail(HSL_ERR_UNSUPPORTED, "persistent path does not fit (B=%d H=%d)", B, H);
 
   // fused weight gradients: fp32 partial planes [nsplit][4H][H] and [nsplit][4H][D]
   // (the GEMM region, which the GEMMs below only use after these planes are reduced)

@@ -90,6 +90,8 @@ class RecurrentFn(torch.autograd.Function):
     def forward(ctx, x, h0, c0, w_ih, w_hh, b_ih, b_hh, a):
         T, B, D, H = _check(x, h0, c0, w_ih, w_hh, b_ih, b_hh, a)
         x, h0, c0, w_ih, w_hh, b_ih, b_hh, a = map(_c, (x, h0, c0, w_ih, w_hh, b_ih, b_hh, a))
+        if x.data_ptr() % 16:  # the workspace query assumes a 16-byte aligned x
+            x = x.clone()
         ctx.set_materialize_grads(False)
         h_save = x.new_empty(T + 1, B, H)
         c_save = x.new_empty(T + 1, B, H)
@@ -123,7 +125,7 @@ class RecurrentFn(torch.autograd.Function):
         db_hh = x.new_empty(4 * H)
         da = x.new_empty(4)
         lib = _lib.load()
-        nbytes = lib.hsl_rec_bwd_ws_bytes(T, B, D, H)
+        nbytes = lib.hsl_rec_bwd_ws_bytes_for(T, B, D, H, 1 if dx is not None else 0)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
         P = _lib.ptr
         _lib.call("hsl_rec_bwd", P(dout), P(dh_n), P(dc_n), P(x), P(h_save), P(c_save), P(gact),

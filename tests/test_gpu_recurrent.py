@@ -251,3 +251,17 @@ def test_fused_weight_gradients(dev, shape, fused):
     parity bar is the same as for the separate GEMMs.  (130 steps: two dW_hh planes.)"""
     check(*shape, dev, 2, a=[0.4, 0.3, 0.2, 0.1])
     assert prlstm_amd._lib.last_backward_fused() == fused
+
+
+def test_workspaces_sized_by_path(dev):
+    """The workspace queries plan the path on the device: the fused persistent forward needs
+    no [T,B,4H] input-gate buffer, and a backward without dx (store_dg=0) no dgates buffer."""
+    lib = prlstm_amd._lib.load()
+    T, B, D, H = 256, 32, 256, 512
+    gates = T * B * 4 * H * 4
+    assert lib.hsl_rec_fwd_ws_bytes(T, B, D, H) < 1 << 20
+    with_dx = lib.hsl_rec_bwd_ws_bytes_for(T, B, D, H, 1)
+    assert with_dx == lib.hsl_rec_bwd_ws_bytes(T, B, D, H)
+    assert with_dx - lib.hsl_rec_bwd_ws_bytes_for(T, B, D, H, 0) >= gates
+    # configs[3] runs one launch per step: its forward needs the input-gate buffer
+    assert lib.hsl_rec_fwd_ws_bytes(64, 32, 1024, 2048) >= 64 * 32 * 4 * 2048 * 4

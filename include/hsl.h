@@ -139,6 +139,23 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0,
                 float* h_save, float* c_save, float* gact, float* tanh_c,
                 void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream);
 
+/* hsl_rec_fwd without a workspace argument, for callers that cannot allocate
+ * device memory (code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  Its workspace is a static
+ * scratch array of 4 MiB inside the library, one per device, held until the
+ * process ends; the call allocates nothing (no hipMalloc, no events) and clears
+ * the parts that must start empty with a fill kernel.  Shapes whose workspace
+ * exceeds 4 MiB are rejected with HSL_ERR_UNSUPPORTED; the persistent path with
+ * the input projection fused (H <= 512, D <= 256, D % 4 == 0, 16-byte aligned x,
+ * a batch that fits the chip) needs well under 1 MiB.  Every call on one device
+ * shares that device's scratch: calls that overlap on one device (two streams,
+ * two threads) race.  Results equal hsl_rec_fwd's bit for bit. */
+int hsl_rec_fwd_noalloc(const float* x, const float* h0, const float* c0,
+                        const float* w_ih, const float* w_hh, const float* b_ih,
+                        const float* b_hh, const float* a,
+                        float* h_save, float* c_save, float* gact, float* tanh_c,
+                        int T, int B, int D, int H, void* stream);
+
 /* Workspace for hsl_rec_bwd on the current device: fp64 reduction buffers, the
  * exchange buffers or the per-step buffers of the path that runs, the weight-
  * gradient planes / GEMM split-K partials, and dgates [T,B,4H] when a product reads

@@ -35,6 +35,7 @@ SIGNATURES = {
     "hsl_timing_collect": (_I, [_I, _P, _P]),
     "hsl_rec_fwd_ws_bytes": (_Z, [_I, _I, _I, _I]),
     "hsl_rec_fwd": (_I, [_P] * 12 + [_P, _Z, _I, _I, _I, _I, _P]),
+    "hsl_rec_fwd_noalloc": (_I, [_P] * 12 + [_I, _I, _I, _I, _P]),
     "hsl_rec_bwd_ws_bytes": (_Z, [_I, _I, _I, _I]),
     "hsl_rec_bwd_ws_bytes_for": (_Z, [_I, _I, _I, _I, _I]),
     "hsl_rec_bwd": (_I, [_P] * 20 + [_P, _Z, _I, _I, _I, _I, _P]),

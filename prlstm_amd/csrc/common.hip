@@ -62,8 +62,15 @@ std::vector<TimingRec> g_trecs;
 std::atomic<int> g_timing{0};
 }  // namespace
 
+namespace {
+thread_local int g_timing_off = 0;  // > 0 inside a TimingSuppress scope on this thread
+}  // namespace
+
+TimingSuppress::TimingSuppress() { ++g_timing_off; }
+TimingSuppress::~TimingSuppress() { --g_timing_off; }
+
 int timing_begin(int kind, hipStream_t s) {
-  if (!g_timing.load()) return -1;
+  if (!g_timing.load() || g_timing_off > 0) return -1;
   TimingRec r{nullptr, nullptr, kind};
   if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) return -1;
   if (hipEventRecord(r.start, s) != hipSuccess) return -1;

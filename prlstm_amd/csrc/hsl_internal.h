@@ -41,6 +41,14 @@ enum TimingKind { kTimeRecFwd = 1, kTimeRecBwd = 2, kTimeScanFwd = 3, kTimeScanB
                   kTimeInputProj = 5, kTimeStepFwd = 6, kTimeStepBwd = 7 };
 int timing_begin(int kind, hipStream_t s);
 void timing_end(int slot, hipStream_t s);
+// While one is alive, timing_begin records nothing on this thread (it creates HIP events,
+// which the allocation-free entry points must not do).
+struct TimingSuppress {
+  TimingSuppress();
+  ~TimingSuppress();
+  TimingSuppress(const TimingSuppress&) = delete;
+  TimingSuppress& operator=(const TimingSuppress&) = delete;
+};
 long long spin_timeout_ticks();   // in wall_clock64 ticks (100 MHz)
 void note_recurrent_path(int path);
 void note_backward_fused(int fused);  // 0, 1 (dW_hh) or 2 (dW_hh and dW_ih)

@@ -23,6 +23,7 @@
 // A_b[i][0], B from lane 4b+j is B_b[0][j], result lane 4b+j, reg i holds D_b[i][j].
 // With cbsz=4, abid=0 every block uses block 0's A (lanes 0-3).
 #include <algorithm>
+#include <mutex>
 #include <cstdlib>
 #include <type_traits>
 
@@ -1811,6 +1812,32 @@ int bias_grads_from_parts(const double* db_part, int B, const double* rowdot, co
 namespace hsl {
 namespace {
 __global__ void clear_device_errors_kernel() { g_device_errors = 0u; }
+
+// ---- the allocation-free forward (hsl_rec_fwd_noalloc) ----------------------------
+// Its workspace is `scratch`, a static device array: each device that loads the library
+// holds its own copy until the process ends.  In host code the array's name is only a
+// stand-in; the device address comes from hipGetSymbolAddress, once per device with that
+// device current, and is what the kernels are given.
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_addr[64] = {};
+
+int scratch_address(void** out) {
+  int dev = 0;
+  HSL_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return fail(HSL_ERR_UNSUPPORTED, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    HSL_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(HSL_ERR_HIP, "hipGetSymbolAddress(scratch) gave a null address");
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return HSL_OK;
+}
 }  // namespace
 }  // namespace hsl
 
@@ -1933,6 +1960,31 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
   timing_end(slot, s);
   note_recurrent_path(1);
   return HSL_OK;
+}
+
+int hsl_rec_fwd_noalloc(const float* x, const float* h0, const float* c0, const float* w_ih, const float* w_hh,
+                        const float* b_ih, const float* b_hh, const float* a, float* h_save, float* c_save,
+                        float* gact, float* tanh_c, int T, int B, int D, int H, void* stream) {
+  HSL_CHECK(check_dims(T, B, D, H));
+  if (B == 0 || H == 0) return HSL_OK;
+  PersistentPlan pl;
+  HSL_CHECK(plan_persistent(B, H, D, false, &pl));
+  const bool x_aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0;
+  if (pl.XP && !x_aligned) pl.XP = false;
+  FwdWs w;
+  const size_t need = carve_fwd(nullptr, 0, T, B, H, fwd_needs(pl, x_aligned), &w);
+  if (need > kNoAllocScratchBytes)
+    return fail(HSL_ERR_UNSUPPORTED,
+                "hsl_rec_fwd_noalloc: T=%d B=%d D=%d H=%d needs %zu bytes of scratch, more than the %zu bytes of "
+                "its static scratch buffer (the persistent path with the input projection fused -- H <= 512, "
+                "D <= 256, D %% 4 == 0, 16-byte aligned x -- needs well under 1 MiB); call hsl_rec_fwd with a "
+                "workspace instead",
+                T, B, D, H, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  HSL_CHECK(scratch_address(&ws));
+  TimingSuppress no_events;
+  return hsl_rec_fwd(x, h0, c0, w_ih, w_hh, b_ih, b_hh, a, h_save, c_save, gact, tanh_c, ws, kNoAllocScratchBytes, T,
+                     B, D, H, stream);
 }
 
 size_t hsl_rec_bwd_ws_bytes_for(int T, int B, int D, int H, int with_dx) {

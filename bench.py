@@ -12,15 +12,23 @@ Prints ONE JSON line:
   roofline    the dominant kernel of the step (persistent recurrent kernel),
               algorithmic fp32 MFMA FLOPs per launch / its mean launch time,
               timed with HIP events on its launch stream; the backward kernel's
-              FLOPs include the weight-gradient products it accumulates
+              FLOPs include the weight-gradient products it accumulates.  traffic:
+              HBM bytes per launch from the committed rocprofv3 --pmc summary
+              (traffic_source)
+  recurrence  per-step latency of the persistent kernels (launch time / T) beside
+              the fp32 MFMA floor of one step's recurrent product
+  step_tflops FLOPs the step executes (x is data: no dx product) / step time
   cpu_baseline the CPU restatement of the reference torch backend (oracle/),
-              same workload, timed on this host's cores
+              same workload, timed on every core of this process's CPU affinity;
+              with the parallel-mode restatement (_parallel.py) at configs[1] and
+              configs[4] beside it
   scan        configs[4] parallel scan (T=4096 B=16 H=1024) forward and
               backward kernels: algorithmic HBM bytes / launch time
   modes       every configured shape (configs[0..4], configs[1] in both modes)
-              as one graph-replayed fwd+bwd step each; algorithmic TFLOP/s counts
-              24*T*B*H*(D+H) (recurrent) or the projection and dW_ih products
-              2*2*T*B*D*4H (parallel, x is data so no dx)
+              as one graph-replayed fwd+bwd step each; TFLOP/s counts the products
+              the step executes: 16*T*B*H*D + 24*T*B*H^2 (recurrent: projection,
+              recurrence both ways, dW_ih, dW_hh) or 2*2*T*B*D*4H (parallel:
+              projection and dW_ih); x is data, so no dx
 """
 
 import argparse
@@ -43,19 +51,26 @@ T, B, D, H = 256, 32, 256, 512
 ST, SB, SD, SH = 4096, 16, 256, 1024
 
 
+def executed_flops(t, b, d, h, parallel):
+    """FLOPs of the products one training step executes with x as data (no dx)."""
+    if parallel:
+        return 2 * (2 * t * b * d * 4 * h)           # projection, dW_ih
+    return 16 * t * b * h * d + 24 * t * b * h * h   # projection + dW_ih, 3 recurrent products
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
 def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
-    (FETCH_SIZE + WRITE_SIZE, calibrated against a known-size copy), or None."""
+    """(HBM bytes per launch of `kernel`, source file) from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated against a known-size copy), or (None, None)."""
     for f in sorted((ROOT / "profiles").glob("hbm_traffic_*.md")):
         for line in f.read_text().splitlines():
             parts = line.split()
             if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel:
-                return int(float(parts[2]))
-    return None
+                return int(float(parts[2])), str(f.relative_to(ROOT))
+    return None, None
 
 
 def make_inputs():
@@ -159,8 +174,9 @@ def bench_scan(args):
         "roofline": {"bound": "hbm", "achieved": round((fwd_b + bwd_b) / (fwd_ms + bwd_ms) / 1e6, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round((fwd_b + bwd_b) / (fwd_ms + bwd_ms) / 1e6 / HBM_PEAK_GBS, 4),
-                     "traffic": (measured_traffic("scan_fwd_kernel") or 0) + (measured_traffic("scan_bwd_kernel") or 0)
-                     or None,
+                     "traffic": (measured_traffic("scan_fwd_kernel")[0] or 0)
+                     + (measured_traffic("scan_bwd_kernel")[0] or 0) or None,
+                     "traffic_source": measured_traffic("scan_fwd_kernel")[1],
                      "algorithmic_bytes": fwd_b + bwd_b},
     }
     log(f"scan fwd {fwd_ms:.4f} ms ({res['fwd_GBps']} GB/s) bwd {bwd_ms:.4f} ms ({res['bwd_GBps']} GB/s)")
@@ -207,12 +223,11 @@ def bench_modes(args):
         e1.record()
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / n
-        # parallel: the projection and dW_ih products, 2 * (2*T*B*D*4H); recurrent: 24*T*B*H*(D+H)
-        flops = 2 * (2 * t * b * d * 4 * h) if par else 24 * t * b * h * (d + h)
+        flops = executed_flops(t, b, d, h, par)
         res.append({"config": name, "mode": "parallel" if par else "recurrent", "dtype": str(dt).split(".")[-1],
                     "T": t, "B": b, "D": d, "H": h,
                     "ms_per_step": round(ms, 4), "timesteps_batch_per_s": round(t * b / ms * 1e3, 1),
-                    "algorithmic_tflops": round(flops / ms / 1e9, 2)})
+                    "executed_tflops": round(flops / ms / 1e9, 2)})
         log(f"mode {name} {'parallel' if par else 'recurrent'}: {ms:.4f} ms/step")
         del step, m
         torch.cuda.empty_cache()
@@ -226,16 +241,26 @@ def _split_products_state():
     return prev
 
 
-def bench_cpu(args):
-    """The reference torch backend restated (oracle/), fp32 on this host's cores."""
-    from oracle.hsl_oracle import RefHeadStartLSTM
-    cores = len(os.sched_getaffinity(0))
-    cores = min(cores, args.cpu_threads) if args.cpu_threads else cores
-    torch.set_num_threads(cores)
-    torch.manual_seed(0)
-    m = RefHeadStartLSTM(D, H, a_init=1e-4)
-    x = torch.randn(T, B, D)
+def _host_info():
+    """CPU model, cgroup CPU quota and torch's thread settings of this host."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), model)
+    except OSError:
+        pass
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota = f.read().strip()
+    except OSError:
+        quota = None
+    info = [l.strip() for l in torch.__config__.parallel_info().splitlines() if l.strip() and not l.startswith("-")]
+    return model, quota, info[:8]
 
+
+def _cpu_steps(m, x, budget_s, min_n, max_n):
+    """Median seconds of zero_grad + forward + out.sum().backward() over min_n..max_n steps
+    after one warm-up, stopping once budget_s seconds are spent (at least min_n steps)."""
     def one():
         m.zero_grad(set_to_none=True)
         t0 = time.perf_counter()
@@ -243,19 +268,48 @@ def bench_cpu(args):
         out.sum().backward()
         return time.perf_counter() - t0
 
-    first = one()  # warm-up
-    times = []
-    budget = args.cpu_seconds
-    spent = first
-    while (len(times) < 1 or spent + statistics.median(times) <= budget) and len(times) < 15:
+    first = one()
+    times, spent = [], first
+    while len(times) < min_n or (len(times) < max_n and spent + statistics.median(times) <= budget_s):
         times.append(one())
         spent += times[-1]
-    med = statistics.median(times)
-    log(f"cpu baseline: {cores} threads, median {med:.3f} s over {len(times)} steps (warm-up {first:.3f} s)")
-    return {"value": round(T * B / med, 1), "unit": "timesteps·batch/s", "cores": cores,
-            "kind": "port", "ms_per_step": round(med * 1e3, 2),
-            "sample": f"configs[2] fwd+bwd (out.sum() loss), fp32, torch CPU restatement of "
-                      f"_torch.py, median of {len(times)} full steps after 1 warm-up"}
+    return statistics.median(times), len(times), first
+
+
+def bench_cpu(args):
+    """The reference torch backend restated (oracle/), fp32 on every core of this process's
+    CPU affinity (configs[2] recurrent), and the parallel-mode restatement (_parallel.py)
+    at configs[1] and configs[4] beside it."""
+    from oracle.hsl_oracle import RefHeadStartLSTM
+    affinity = len(os.sched_getaffinity(0))
+    cores = min(affinity, args.cpu_threads) if args.cpu_threads else affinity
+    torch.set_num_threads(cores)
+    model, quota, pinfo = _host_info()
+    torch.manual_seed(0)
+    m = RefHeadStartLSTM(D, H, a_init=1e-4)
+    x = torch.randn(T, B, D)
+    med, n, first = _cpu_steps(m, x, args.cpu_seconds, 1, 15)
+    log(f"cpu baseline: {cores} threads ({model}), median {med:.3f} s over {n} steps (warm-up {first:.3f} s)")
+    res = {"value": round(T * B / med, 1), "unit": "timesteps·batch/s", "cores": cores,
+           "kind": "port", "ms_per_step": round(med * 1e3, 2),
+           "sample": f"configs[2] fwd+bwd (out.sum() loss), fp32, torch CPU restatement of "
+                     f"_torch.py, median of {n} full steps after 1 warm-up",
+           "affinity_cores": affinity, "cpu_model": model, "cgroup_cpu_max": quota, "torch_parallel_info": pinfo}
+    if not args.no_cpu_parallel:
+        par = []
+        for name, t, b, d, h, nmin in (("configs[1]", 128, 32, 256, 256, 5), ("configs[4]", 4096, 16, 256, 1024, 3)):
+            torch.manual_seed(0)
+            mp = RefHeadStartLSTM(d, h, a_init=1e-4 if name == "configs[1]" else 0.0, parallel=True)
+            xp = torch.randn(t, b, d)
+            pmed, pn, pfirst = _cpu_steps(mp, xp, 0.0, nmin, nmin)
+            log(f"cpu parallel {name}: median {pmed:.3f} s over {pn} steps (warm-up {pfirst:.3f} s)")
+            par.append({"config": name, "mode": "parallel", "T": t, "B": b, "D": d, "H": h,
+                        "ms_per_step": round(pmed * 1e3, 2), "timesteps_batch_per_s": round(t * b / pmed, 1),
+                        "sample": f"median of {pn} full fwd+bwd steps after 1 warm-up, torch CPU restatement "
+                                  f"of _parallel.py:21-74"})
+            del mp, xp
+        res["parallel_mode"] = par
+    return res
 
 
 def main():
@@ -265,8 +319,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="bound on the CPU baseline sample (seconds of CPU work)")
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="threads of the CPU baseline (default 0: every core of the CPU affinity)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-cpu-parallel", action="store_true", help="skip the parallel-mode CPU baseline")
     ap.add_argument("--no-scan", action="store_true")
     ap.add_argument("--no-modes", action="store_true", help="skip the per-config table of both modes")
     args = ap.parse_args()
@@ -283,7 +339,7 @@ def main():
     modes = None if args.no_modes else bench_modes(args)
     cpu = None if args.no_cpu else bench_cpu(args)
 
-    step_flops = 24.0 * T * B * H * (D + H)           # algorithmic fwd+bwd FLOPs
+    step_flops = float(executed_flops(T, B, D, H, False))  # fwd+bwd products executed (no dx)
     rec_flops = 2.0 * T * B * H * 4 * H               # recurrent product of one direction
     # per-launch FLOPs: the backward kernel also accumulates dW_hh (and dW_ih) when fused,
     # the forward kernel computes the input projection when no separate launch ran
@@ -319,9 +375,20 @@ def main():
         "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(achieved, 3),
                      "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4),
-                     "traffic": measured_traffic(kname) if kname.endswith("persistent") else None,
+                     "traffic": measured_traffic(kname)[0] if kname.endswith("persistent") else None,
+                     "traffic_source": measured_traffic(kname)[1] if kname.endswith("persistent") else None,
                      "kernel_ms": round(kms, 5), "flops_per_launch": kflops[name]},
+        # per-step latency of the recurrence: launch time / T, beside the time one step's
+        # recurrent product (2*B*4H*H FLOPs) takes at the fp32 MFMA peak
+        "recurrence": {
+            **{f"{k}_us_per_step": round(kern[k] * 1e3 / T, 4) for k in ("rec_fwd", "rec_bwd", "step_fwd", "step_bwd")
+               if k in kern},
+            "floor_us_per_step": round(rec_flops / T / (MFMA_F32_PEAK_TFLOPS * 1e12) * 1e6, 4),
+            "floor_note": "2*B*4H*H FLOPs of one step's recurrent product at the fp32 MFMA peak; "
+                          "rec_fwd also runs the input projection (2*B*4H*D per step) and rec_bwd "
+                          "the dW_hh and dW_ih products (2*B*4H*(H+D) per step)"},
         "step_tflops": round(step_flops / (ms * 1e-3) / 1e12, 3),
+        "step_flops": step_flops,
         "kernels_ms": {k: round(v, 5) for k, v in kern.items()},
         "wall_ms_per_step": round(wall_ms, 5),
         "scan": scan,
@@ -335,6 +402,12 @@ def main():
     }
     if cpu:
         line["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+        for p in cpu.get("parallel_mode", []):  # GPU step of the same config from the modes table
+            g = next((r for r in modes or [] if r["config"] == p["config"] and r["mode"] == "parallel"
+                      and r["dtype"] == "float32"), None)
+            if g:
+                p["gpu_ms_per_step"] = g["ms_per_step"]
+                p["speedup_vs_cpu"] = round(p["ms_per_step"] / g["ms_per_step"], 1)
     print(json.dumps(line), flush=True)
 
 

@@ -62,7 +62,12 @@ class GraphedTrainStep:
             out, (h_n, c_n) = m(self.static_x, self.hx)
             torch.autograd.backward([out], [self.grad_out])
         grads = {n: p.grad for n, p in m.named_parameters()}
-        self._graphs[mode] = (graph, out, h_n, c_n, grads)
+        # Only detached views of the static outputs are kept (same memory): the captured
+        # autograd graph, and with it the parameters' AccumulateGrad nodes created on the
+        # capture stream, is released, so later eager steps on another stream build their
+        # own nodes instead of reusing those (a stream mismatch torch warns about).
+        self._graphs[mode] = (graph, out.detach(), h_n.detach(), c_n.detach(), grads)
+        del out, h_n, c_n
 
     @property
     def graph(self):

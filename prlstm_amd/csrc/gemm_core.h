@@ -137,6 +137,42 @@ __device__ __forceinline__ void load_b(const GemmArgs& g, int n0, int k0, int ke
   }
 }
 
+// Unmasked loads of one slice for a tile that lies inside both operands with 16-byte
+// aligned rows and a whole slice of k (the condition is uniform over the workgroup; see
+// gemm_tile): straight-line code, where the masked loads above carry a bounds and
+// alignment branch per 16-byte chunk.
+template <class Cfg, bool TA, bool TB>
+__device__ __forceinline__ void load_ab_full(const GemmArgs& g, int m0, int n0, int k0, f4 (&ra)[Cfg::A_CHUNKS],
+                                             f4 (&rb)[Cfg::B_CHUNKS]) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < Cfg::A_CHUNKS; ++j) {
+    const int c = t + Cfg::kThreads * j;
+    const float* p;
+    if (!TA) {
+      const int row = c / (Cfg::BK / 4), kq = c % (Cfg::BK / 4);
+      p = g.A + (size_t)(m0 + row) * g.lda + k0 + kq * 4;
+    } else {
+      const int krow = c / (Cfg::BM / 4), mq = c % (Cfg::BM / 4);
+      p = g.A + (size_t)(k0 + krow) * g.lda + m0 + mq * 4;
+    }
+    ra[j] = *reinterpret_cast<const f4*>(p);
+  }
+#pragma unroll
+  for (int j = 0; j < Cfg::B_CHUNKS; ++j) {
+    const int c = t + Cfg::kThreads * j;
+    const float* p;
+    if (TB) {
+      const int row = c / (Cfg::BK / 4), kq = c % (Cfg::BK / 4);
+      p = g.B + (size_t)(n0 + row) * g.ldb + k0 + kq * 4;
+    } else {
+      const int krow = c / (Cfg::BN / 4), nq = c % (Cfg::BN / 4);
+      p = g.B + (size_t)(k0 + krow) * g.ldb + n0 + nq * 4;
+    }
+    rb[j] = *reinterpret_cast<const f4*>(p);
+  }
+}
+
 template <class Cfg, bool TA, bool TB>
 __device__ __forceinline__ void store_ab(float* As, float* Bs, const f4 (&ra)[Cfg::A_CHUNKS],
                                          const f4 (&rb)[Cfg::B_CHUNKS]) {
@@ -200,18 +236,31 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
         for (int r = 0; r < (ACC64 ? 16 : 1); ++r) acc64[i][j][r] = 0.0;
   }
 
+  // full: the tile lies inside both operands, rows are 16-byte aligned and k splits
+  // into whole slices, so every slice takes the unmasked loads (uniform branch)
+  const bool full = g.vec_a && g.vec_b && (kend - kbeg) % Cfg::BK == 0 &&
+                    (TA ? m0 + Cfg::BM <= g.M && g.M % 4 == 0 : m0 + Cfg::BM <= g.M) &&
+                    (TB ? n0 + Cfg::BN <= g.N : n0 + Cfg::BN <= g.N && g.N % 4 == 0);
   f4 ra[Cfg::A_CHUNKS], rb[Cfg::B_CHUNKS];
   if (kbeg < kend) {
-    load_a<Cfg, TA>(g, m0, kbeg, kend, ra);
-    load_b<Cfg, TB>(g, n0, kbeg, kend, rb);
+    if (full) {
+      load_ab_full<Cfg, TA, TB>(g, m0, n0, kbeg, ra, rb);
+    } else {
+      load_a<Cfg, TA>(g, m0, kbeg, kend, ra);
+      load_b<Cfg, TB>(g, n0, kbeg, kend, rb);
+    }
   }
   for (int k0 = kbeg; k0 < kend; k0 += Cfg::BK) {
     __syncthreads();  // previous stage fully consumed
     store_ab<Cfg, TA, TB>(As, Bs, ra, rb);
     __syncthreads();
     if (k0 + Cfg::BK < kend) {  // prefetch the next stage into registers
-      load_a<Cfg, TA>(g, m0, k0 + Cfg::BK, kend, ra);
-      load_b<Cfg, TB>(g, n0, k0 + Cfg::BK, kend, rb);
+      if (full) {
+        load_ab_full<Cfg, TA, TB>(g, m0, n0, k0 + Cfg::BK, ra, rb);
+      } else {
+        load_a<Cfg, TA>(g, m0, k0 + Cfg::BK, kend, ra);
+        load_b<Cfg, TB>(g, n0, k0 + Cfg::BK, kend, rb);
+      }
     }
     const int kb = wk * Cfg::KS + half * Cfg::KH;
 #pragma unroll
@@ -266,6 +315,85 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
   __syncthreads();
 }
 
+// gemm_tile for a full tile (see load_ab_full) with DEPTH register stages: slices s+1 ..
+// s+DEPTH-1 are loading while slice s is multiplied, and the barriers order LDS only
+// (lds_barrier), so none of them waits for the loads in flight.  The k-steps alternate
+// between two accumulators (even / odd k pairs), so back-to-back MFMAs do not depend on
+// each other; the two are added before the epilogue.
+template <class Cfg, bool TA, bool TB, int DEPTH>
+__device__ __forceinline__ void gemm_tile_full_deep(const GemmArgs& g, int m0, int n0, int kbeg, int kend,
+                                                    float* smem) {
+  float* As = smem;
+  float* Bs = smem + Cfg::BM * Cfg::LDK;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wk = wave % Cfg::WK;
+  const int wn = (wave / Cfg::WK) % Cfg::WN;
+  const int wm = wave / (Cfg::WK * Cfg::WN);
+  const int half = lane >> 5, r32 = lane & 31;
+  f16v acc[Cfg::FM][Cfg::FN], acc2[Cfg::FM][Cfg::FN];
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = acc2[i][j][r] = 0.f;
+  f4 ra[DEPTH][Cfg::A_CHUNKS], rb[DEPTH][Cfg::B_CHUNKS];
+#pragma unroll
+  for (int d = 0; d < DEPTH - 1; ++d)
+    if (kbeg + d * Cfg::BK < kend) load_ab_full<Cfg, TA, TB>(g, m0, n0, kbeg + d * Cfg::BK, ra[d], rb[d]);
+  for (int k0 = kbeg; k0 < kend; k0 += DEPTH * Cfg::BK) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int ks = k0 + d * Cfg::BK;
+      if (ks >= kend) break;
+      lds_barrier();  // previous slice fully consumed
+      store_ab<Cfg, TA, TB>(As, Bs, ra[d], rb[d]);
+      lds_barrier();
+      const int kn = ks + (DEPTH - 1) * Cfg::BK;  // into the stage of the slice before
+      if (kn < kend) load_ab_full<Cfg, TA, TB>(g, m0, n0, kn, ra[(d + DEPTH - 1) % DEPTH], rb[(d + DEPTH - 1) % DEPTH]);
+      const int kb = wk * Cfg::KS + half * Cfg::KH;
+#pragma unroll
+      for (int kk = 0; kk < Cfg::KH; kk += 4) {
+        f4 av[Cfg::FM], bv[Cfg::FN];
+#pragma unroll
+        for (int i = 0; i < Cfg::FM; ++i)
+          av[i] = *reinterpret_cast<const f4*>(As + (wm * Cfg::TM + i * 32 + r32) * Cfg::LDK + kb + kk);
+#pragma unroll
+        for (int j = 0; j < Cfg::FN; ++j)
+          bv[j] = *reinterpret_cast<const f4*>(Bs + (wn * Cfg::TN + j * 32 + r32) * Cfg::LDK + kb + kk);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::FN; ++j) {
+              if (e & 1)
+                acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[j][e], acc2[i][j], 0, 0, 0);
+              else
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[j][e], acc[i][j], 0, 0, 0);
+            }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::FN; ++j) acc[i][j] += acc2[i][j];
+  lds_barrier();  // A/B stage dead; reuse LDS for the epilogue tile
+  float* Cs = smem + wk * Cfg::BM * Cfg::LDC;
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = wm * Cfg::TM + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        const int n = wn * Cfg::TN + j * 32 + r32;
+        Cs[m * Cfg::LDC + n] = acc[i][j][r];
+      }
+  __syncthreads();
+}
+
 // Maps blockIdx.x to a tile (tm, tn).  Workgroup i runs on XCD i % 8, so each XCD gets
 // a contiguous range of the tile sequence (when the tile count divides by 8), and the
 // sequence visits tiles in groups of 8 row panels: consecutive tiles walk down 8 rows
@@ -289,15 +417,23 @@ __device__ __forceinline__ void tile_coords(const GemmArgs& g, int* tm, int* tn)
   gemm_tile_order(g.tiles_m, g.tiles_n, tm, tn);
 }
 
-template <class Cfg, bool TA, bool TB, class Epi, bool ACC64 = false>
+template <class Cfg, bool TA, bool TB, class Epi, bool ACC64 = false, int DEPTH = 1>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi) {
+  static_assert(DEPTH == 1 || !ACC64, "the deep pipeline has no fp64 fold");
   extern __shared__ float smem[];
   int tm, tn;
   tile_coords(g, &tm, &tn);
   const int m0 = tm * Cfg::BM, n0 = tn * Cfg::BN;
   const int kbeg = blockIdx.z * g.k_per_split;
   const int kend = min(g.K, kbeg + g.k_per_split);
-  gemm_tile<Cfg, TA, TB, ACC64>(g, m0, n0, kbeg, kend, smem);
+  bool deep = false;
+  if constexpr (DEPTH > 1)
+    deep = g.vec_a && g.vec_b && (kend - kbeg) % Cfg::BK == 0 && m0 + Cfg::BM <= g.M && n0 + Cfg::BN <= g.N &&
+           (!TA || g.M % 4 == 0) && (TB || g.N % 4 == 0);
+  if (deep)
+    gemm_tile_full_deep<Cfg, TA, TB, (DEPTH > 1 ? DEPTH : 2)>(g, m0, n0, kbeg, kend, smem);
+  else
+    gemm_tile<Cfg, TA, TB, ACC64>(g, m0, n0, kbeg, kend, smem);
   epi.template run<Cfg>(smem, m0, n0, blockIdx.z);
 }
 
@@ -346,14 +482,14 @@ inline int split_layout(int K, int splits, int* k_per_split) {
   return n < 1 ? 1 : n;
 }
 
-template <class Cfg, bool TA, bool TB, class Epi, bool ACC64 = false>
+template <class Cfg, bool TA, bool TB, class Epi, bool ACC64 = false, int DEPTH = 1>
 inline int launch_gemm(const GemmArgs& g0, int splits, const Epi& epi, hipStream_t s) {
   GemmArgs g = g0;
   g.tiles_m = (g.M + Cfg::BM - 1) / Cfg::BM;
   g.tiles_n = (g.N + Cfg::BN - 1) / Cfg::BN;
   splits = split_layout<Cfg>(g.K, splits, &g.k_per_split);
   dim3 grid(g.tiles_m * g.tiles_n, 1, splits);
-  hipLaunchKernelGGL((gemm_kernel<Cfg, TA, TB, Epi, ACC64>), grid, dim3(256), Cfg::LDS_BYTES, s, g, epi);
+  hipLaunchKernelGGL((gemm_kernel<Cfg, TA, TB, Epi, ACC64, DEPTH>), grid, dim3(256), Cfg::LDS_BYTES, s, g, epi);
   HSL_HIP(hipGetLastError());
   return HSL_OK;
 }

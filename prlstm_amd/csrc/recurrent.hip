@@ -33,6 +33,8 @@ namespace hsl {
 
 // Per-step products: 32x32 tiles, four waves splitting each 128-deep k-slice.
 using CfgStep = GemmCfg<32, 32, 128, 1, 1, 4>;
+// Two register stages: the loads of slice s+1 are in flight while slice s multiplies.
+constexpr int kStepDepth = 2;
 
 namespace {
 
@@ -752,8 +754,8 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
 // v_mfma_f32_32x32x2_f32 tile (column = t%8 * 4 + batch slot), rows = the 64 gate rows
 // (two tiles), W_ih's rows held in registers for the whole launch.  The two half-waves
 // take the two 32-wide halves of the quarter (A and B use the same k order).  Block m+1
-// is computed during the first 7 steps of block m (the 64 products spread over them) and
-// written to xin before the barrier of step 8m+7 (parity m+1; recurrent wave w reads its
+// is computed during the first 6 steps of block m (the 64 products spread over them) and
+// written to xin in step 8m+6, before the barrier of step 8m+7 (parity m+1; recurrent wave w reads its
 // plane at the start of each step of block m+1, before that step's barrier, and the
 // last reads of block m-1, which the write replaces, came before the barrier of step
 // 8m-1).  Its x operands are loaded two blocks ahead.  Block 0 is computed and written
@@ -781,14 +783,17 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
   // column l32 = t%8 * 4 + batch slot; absent slots read batch 0 (their column is unused)
   const int bsl = l32 & 3, tl = l32 >> 2, cb = grp * Bg + bsl;
   const int cbr = (bsl < Bg && cb < B) ? cb : 0;
+  // Loads are unconditional at clamped addresses (columns past D read the row's last
+  // four values, finite, and meet zero W_ih registers): a conditional load would need a
+  // select on its result, and the compiler would then wait for the HBM load right here,
+  // two blocks before the values are used (1800 clocks at every block boundary).
   auto load_blk = [&](int m, float (&xo)[32]) {
     const int t = m * kXinSteps + tl;
     const float* row = p.x + ((size_t)(t < T ? t : T - 1) * B + cbr) * D;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int k4 = kb + 4 * j;
-      f4 v = f4{0.f, 0.f, 0.f, 0.f};
-      if (k4 < D) v = *reinterpret_cast<const f4*>(row + k4);
+      const int k4 = min(kb + 4 * j, D - 4);
+      const f4 v = *reinterpret_cast<const f4*>(row + k4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) xo[4 * j + e] = v[e];
     }
@@ -821,7 +826,9 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
   load_blk(2, xa);
   lds_barrier();  // the recurrent waves' barrier ahead of their first step
   // window j: the 8 steps of block j, computing block j+1 from its operand set in steps
-  // 0-6 (k-steps 32 sub / 7 .. 32 (sub+1) / 7 in step sub)
+  // 0-5 (k-steps 32 sub / 6 .. 32 (sub+1) / 6 in step sub) and writing it in step 6, when
+  // those products have long finished (writing right after the last products made the
+  // barrier of step 8m+7 wait for them)
   auto window = [&](int j, float (&xu)[32]) __attribute__((always_inline)) -> bool {
     const bool next = (j + 1) * kXinSteps < T;
 #pragma unroll
@@ -830,7 +837,10 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
       if (t >= T) return false;
       lds_barrier();  // the recurrent waves' barrier of this step
       if (abort_flag) return false;
-      if (next && sub < 7) {
+      if (next && sub == 6) {  // block j+1, whose products ended a step ago, to xin
+        write_blk(j + 1);
+        load_blk(j + 3, xu);
+      } else if (next && sub < 6) {
         if constexpr (kXprojAfterPublish) {  // after the recurrent waves' publish of h_t
           const long long t0 = wall_clock64();
           while (true) {
@@ -845,11 +855,7 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
             __builtin_amdgcn_s_sleep(1);
           }
         }
-        products(xu, 32 * sub / 7, 32 * (sub + 1) / 7);
-        if (sub == 6) {
-          write_blk(j + 1);
-          load_blk(j + 3, xu);
-        }
+        products(xu, 32 * sub / 6, 32 * (sub + 1) / 6);
       }
     }
     return true;
@@ -1947,10 +1953,10 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
     if (nsp == 1) {
       EpiCellFwd epi{w.gih + t * plane4, w.bs, c_save + t * plane, h_save + (t + 1) * plane,
                      c_save + (t + 1) * plane, gact + t * plane4, tanh_c + t * plane, B, H};
-      HSL_CHECK((launch_gemm<CfgStep, false, true>(ga, 1, epi, s)));
+      HSL_CHECK((launch_gemm<CfgStep, false, true, EpiCellFwd, false, kStepDepth>(ga, 1, epi, s)));
     } else {
       EpiPartial epi{w.part, B, 4 * H};
-      HSL_CHECK((launch_gemm<CfgStep, false, true>(ga, nsp, epi, s)));
+      HSL_CHECK((launch_gemm<CfgStep, false, true, EpiPartial, false, kStepDepth>(ga, nsp, epi, s)));
       hipLaunchKernelGGL(step_cell_fwd_kernel, dim3(grid_for(plane)), dim3(256), 0, s, w.part, nsp,
                          w.gih + t * plane4, w.bs, c_save + t * plane, h_save + (t + 1) * plane,
                          c_save + (t + 1) * plane, gact + t * plane4, tanh_c + t * plane, B, H);
@@ -2087,12 +2093,12 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
       if (nsp == 1) {
         EpiCellBwd epi{dout + t * plane, t == T - 1 ? dh_n : nullptr, c_save + t * plane, gact + t * plane4,
                        tanh_c + t * plane, w.dc, w.dgates + t * plane4, B, H};
-        HSL_CHECK((launch_gemm<CfgStep, false, false>(ga, 1, epi, s)));
+        HSL_CHECK((launch_gemm<CfgStep, false, false, EpiCellBwd, false, kStepDepth>(ga, 1, epi, s)));
       } else {
         // the last step has no dgates_{t+1}: no product, zero planes summed
         if (ga.K > 0) {
           EpiPartial epi{w.part, B, H};
-          HSL_CHECK((launch_gemm<CfgStep, false, false>(ga, nsp, epi, s)));
+          HSL_CHECK((launch_gemm<CfgStep, false, false, EpiPartial, false, kStepDepth>(ga, nsp, epi, s)));
         }
         hipLaunchKernelGGL(step_cell_bwd_kernel, dim3(grid_for(plane)), dim3(256), 0, s, w.part,
                            ga.K > 0 ? nsp : 0, t == T - 1 ? dh_n : nullptr, dout + t * plane, c_save + t * plane,

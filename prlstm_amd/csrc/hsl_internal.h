@@ -129,48 +129,54 @@ int copy_f32(float* dst, const float* src, size_t n, hipStream_t s);
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
-// exp(x) = 2^(x log2 e) on v_exp_f32.  The product t = x*L (L = fp32 log2 e) is rounded,
-// and at |x| ~ 80 that rounding alone is ~64 ulp of the result, so the product's exact
-// rounding error fma(x, L, -t) plus x times the low part of log2 e (Llo = log2 e - L) is
-// put back as 2^t + 2^t (d ln 2) (as one fma, so the correction is not rounded against
-// 1).  For |t| >= 128 the result is 0 or inf (or NaN for NaN x) and is returned as
-// v_exp_f32 gives it (there d can be infinite or NaN).  7 VALU operations and one
-// transcendental.  exp_scaled_f<K>(x) = exp_f(K x) bit for bit for K = +-1, +-2 (x L K is
-// x L scaled by a power of two), without the multiply by K.
+// exp(x) = 2^t (1 + dl) with t = x*L (L = fp32 log2 e) on v_exp_f32.  t is rounded, and
+// at |x| ~ 80 that rounding alone is ~64 ulp of the result, so the reduced argument
+// dl = x - t ln 2 is formed in two fmas (Cody and Waite's split ln 2 = C1 + C2, C1 with
+// 16 significant bits; the first fma cancels almost exactly and is computed with one
+// rounding) and put back as fma(2^t, dl, 2^t), so the correction is not rounded against 1.
+// |dl| < 0.35 whenever |t| < 2^24.  For |t| >= 128 the result is 0 or inf (or NaN for NaN
+// x) and is returned as v_exp_f32 gives it (there dl can be infinite or NaN).  Six VALU
+// operations and one transcendental.  exp_scaled_f<K>(x) = exp_f(K x) bit for bit for
+// K = +-1, +-2 (x L K is x L scaled by a power of two).
 template <int K>
 __device__ __forceinline__ float exp_scaled_f(float x) {
-  constexpr float L = 1.44269502162933349609375f * K, Llo = 1.925963033500011e-08f * K,
-                  Ln2 = 0.693147182464599609375f;
+  constexpr float L = 1.44269502162933349609375f * K, C1 = 0.693145751953125f, C2 = 1.428606765330187e-06f;
   const float t = x * L;
-  const float d = __builtin_fmaf(x, Llo, __builtin_fmaf(x, L, -t));
+  const float dl = __builtin_fmaf(-t, C2, __builtin_fmaf(-t, C1, K * x));
   const float r = __builtin_amdgcn_exp2f(t);
-  return __builtin_fabsf(t) < 128.0f ? __builtin_fmaf(r, d * Ln2, r) : r;
+  return __builtin_fabsf(t) < 128.0f ? __builtin_fmaf(r, dl, r) : r;
 }
 __device__ __forceinline__ float exp_f(float x) { return exp_scaled_f<1>(x); }
 // sigmoid from its definition with v_rcp_f32; exp overflow gives inf and rcp(inf) = 0, so
 // sigmoid(-large) -> 0 and sigmoid(+large) -> 1 without NaN.  Error: exp's, the rounding
 // of 1 + e and v_rcp_f32's (about 1 ulp each).
 __device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + exp_scaled_f<-1>(x)); }
-// tanh: for |x| < 0.625 the odd polynomial x + x^3 P(x^2), P of degree 4 fitted to
-// (tanh(x)/x - 1)/x^2 on [0, 0.625] by iteratively reweighted least squares in fp64
-// (relative error of the model 4.4e-9); there 1 - 2/(1 + e^{2x}) would cancel (1.7e-4
-// relative error at x = 1e-4).  For |x| >= 0.625, 1 - 2/(1 + e^{2|x|}) with the sign
-// restored; it saturates to +-1 for large |x| (rcp(inf) = 0).  Both sides are computed
-// and one is selected, so the dependent chain is the longer of the two, not their sum.
+// tanh: for |x| < 1 the odd polynomial x + x^3 P(x^2), P of degree 6 fitted to
+// (tanh(x)/x - 1)/x^2 on [0, 1] by iteratively reweighted least squares in fp64 (relative
+// error of the model 4.6e-9); there 1 - 2/(1 + e^{2x}) would cancel (1.7e-4 relative error
+// at x = 1e-4).  For |x| >= 1, 1 - 2/(1 + e^{2|x|}) with the sign restored; it saturates to
+// +-1 for large |x| (rcp(inf) = 0).  Its exp needs no argument correction: an error e in
+// e^{2|x|} moves the result by 2E/(1+E)^2 e (E = e^{2|x|}), at most 0.21 e for |x| >= 1,
+// and e grows only with |x| while that factor falls as 2/E.  Both sides are computed and
+// one is selected, so the dependent chain is the longer of the two, not their sum.
 // tanh_pos_f: the same for x >= 0 (or NaN), without the sign handling.
 template <bool POS>
 __device__ __forceinline__ float tanh_impl(float x) {
-  constexpr float P0 = -0.3333328068256378f, P1 = 0.13331441581249237f, P2 = -0.05373970419168472f,
-                  P3 = 0.020639054477214813f, P4 = -0.005704952869564295f;
+  constexpr float P0 = -0.33333295583724976f, P1 = 0.13332344591617584f, P2 = -0.05387980490922928f,
+                  P3 = 0.021486664190888405f, P4 = -0.007946118712425232f, P5 = 0.0023013753816485405f,
+                  P6 = -0.00035845543607138097f;
+  constexpr float L2 = 2.8853900432586669921875f;  // fp32 2 log2 e
   const float ax = POS ? x : __builtin_fabsf(x);
   const float s = x * x;
-  float p = __builtin_fmaf(s, P4, P3);
+  float p = __builtin_fmaf(s, P6, P5);
+  p = __builtin_fmaf(s, p, P4);
+  p = __builtin_fmaf(s, p, P3);
   p = __builtin_fmaf(s, p, P2);
   p = __builtin_fmaf(s, p, P1);
   p = __builtin_fmaf(s, p, P0);
   const float small = __builtin_fmaf(x * s, p, x);
-  const float big = __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + exp_scaled_f<2>(ax)), 1.0f);
-  return ax < 0.625f ? small : (POS ? big : __builtin_copysignf(big, x));
+  const float big = __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(ax * L2)), 1.0f);
+  return ax < 1.0f ? small : (POS ? big : __builtin_copysignf(big, x));
 }
 __device__ __forceinline__ float tanh_f(float x) { return tanh_impl<false>(x); }
 __device__ __forceinline__ float tanh_pos_f(float x) { return tanh_impl<true>(x); }

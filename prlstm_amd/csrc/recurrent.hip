@@ -452,6 +452,17 @@ __device__ __forceinline__ bool words_wait(const float* base, unsigned off, cons
   }
 }
 
+// x[l] + x[l ^ 16] and x[l] + x[l ^ 32] with gfx950's row and half swaps: with both
+// operands x, the two results of a swap hold x[l] and x[partner] in every lane.
+__device__ __forceinline__ float add_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ unsigned xcc_id() {
   unsigned x;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
@@ -1083,8 +1094,8 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
       float part = 0.f;
 #pragma unroll
       for (int j = 0; j < PER; ++j) part += wv[j] ? __uint_as_float(v[j]) : 0.f;
-      part += __shfl_xor(part, 16);
-      part += __shfl_xor(part, 32);
+      part = add_xor16(part);
+      part = add_xor32(part);
       dh = part;
       asm volatile("" : "+v"(dh));  // settled before the loads below are issued
     }

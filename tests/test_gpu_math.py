@@ -8,8 +8,8 @@ result (ulp of the fp64 value, 2^-149 below the normal range):
            x log2 e, which is put back; measured 1.21);
   sigmoid  <= 3.5 ulp (exp, the rounding of 1 + e and v_rcp_f32; measured 3.10, torch's
            own fp32 CPU sigmoid 2.47);
-  tanh     <= 2 ulp (below |x| = 0.625 an odd polynomial, measured 0.53 there; above
-           it 1 - 2/(1 + e^{2|x|}), whose cancellation is bounded there; measured 1.49).
+  tanh     <= 1.5 ulp (below |x| = 1 an odd polynomial, measured 0.53 near zero; above
+           it 1 - 2/(1 + e^{2|x|}), whose cancellation is bounded there; measured 1.02).
 Results below the normal range (exp(x < -87.3), sigmoid(x < -87.3)) may be flushed:
 their absolute error must stay below 2^-126.  Special values: exp(+-inf) = inf / 0,
 sigmoid(+-inf) = 1 / 0, tanh(+-inf) = +-1, NaN in gives NaN out.
@@ -25,7 +25,7 @@ from prlstm_amd import _lib
 pytestmark = pytest.mark.gpu
 
 FN = {"exp": 0, "sigmoid": 1, "tanh": 2}
-BOUND = {"exp": 1.5, "sigmoid": 3.5, "tanh": 2.0}
+BOUND = {"exp": 1.5, "sigmoid": 3.5, "tanh": 1.5}
 TORCH64 = {"exp": torch.exp, "sigmoid": torch.sigmoid, "tanh": torch.tanh}
 
 
@@ -48,7 +48,7 @@ def _sweep():
     small = torch.logspace(-8, -1, 20001, dtype=torch.float64)
     mid = torch.linspace(-20, 20, 400001, dtype=torch.float64)
     wide = torch.linspace(-100, 100, 200001, dtype=torch.float64)
-    big = torch.tensor([0.625, 0.62499, 0.62501, 1.0, 5.0, 9.0, 20.0, 44.0, 80.0, 87.0, 88.0, 88.7, 89.0,
+    big = torch.tensor([0.625, 0.99999, 1.0, 1.00001, 5.0, 9.0, 20.0, 44.0, 80.0, 87.0, 88.0, 88.7, 89.0,
                         100.0, 1e4, 3e38], dtype=torch.float64)
     x = torch.cat([small, -small, mid, wide, big, -big]).float()
     return x[torch.isfinite(x)]

@@ -570,6 +570,30 @@ __device__ __forceinline__ lds_vint* step_flags() { return (lds_vint*)(s_step_fl
 constexpr int kXinSteps = 8;
 constexpr bool kXprojAfterPublish = true;  // projection products wait for the step's publish
 typedef float XinBuf[2][4][64][kXinSteps * 4 + 4];
+// With the projection waves present, recurrent wave q's cell lanes do not store the
+// step's saved activations themselves: they leave them in LDS and projection wave q
+// stores them a step later, so that the recurrent wave's single completion counter
+// covers only its hand-off stores and loads.  [step parity][wave][unit][h, c, tanh c, -,
+// i, f, g, o]; it follows xin in the padding LDS.
+typedef float SaveBuf[2][4][kUnits][8];
+__device__ __forceinline__ SaveBuf* save_buf(XinBuf* xin) {
+  return reinterpret_cast<SaveBuf*>(reinterpret_cast<char*>(xin) + sizeof(XinBuf));
+}
+
+// Projection wave w stores the activations of step ts that recurrent wave w staged
+// (batch slot w, the workgroup's 16 units; lanes 0-15).
+__device__ __forceinline__ void store_saves(const PFwdArgs& p, int grp, int wg, const SaveBuf* sv, int w,
+                                            int ts) {
+  const int lane = threadIdx.x & 63, cb = grp * p.Bg + w, cu = wg * kUnits + (lane & 15);
+  if (lane >= kUnits || w >= p.Bg || cb >= p.B || cu >= p.H) return;
+  const f4 hc = *reinterpret_cast<const f4*>(&(*sv)[ts & 1][w][lane][0]);
+  const f4 g = *reinterpret_cast<const f4*>(&(*sv)[ts & 1][w][lane][4]);
+  const size_t plane = (size_t)p.B * p.H, e = (size_t)cb * p.H + cu;
+  __builtin_nontemporal_store(hc[0], p.h_save + (size_t)(ts + 1) * plane + e);
+  __builtin_nontemporal_store(hc[1], p.c_save + (size_t)(ts + 1) * plane + e);
+  __builtin_nontemporal_store(hc[2], p.tanh_c + (size_t)ts * plane + e);
+  __builtin_nontemporal_store(g, reinterpret_cast<f4*>(p.gact + ((size_t)ts * plane + e) * 4));
+}
 
 // Forward.  Wave q multiplies the q-th quarter of k (KQ values).  h_{t-1} of a quarter
 // comes from NS = KQ/16 source workgroups (16 units each).  Lane l of wave q needs
@@ -660,8 +684,9 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
   // after step t's receive (two register sets alternate, so no copy waits for it) and
   // is forced into registers right after step t+1's receive, by when it has long arrived
   // (forcing it earlier would also wait for the stores of step t, before the first
-  // poll); the saved activations and the slot clear are stored after the publish.  All
-  // of them have completed once the next receive has (one in-order completion counter).
+  // poll); the saved activations (staged in LDS for the projection waves when they are
+  // present) and the slot clear are stored after the publish.  All of these stores have
+  // completed once the next receive has (one in-order completion counter).
   // The streamed activations use non-temporal accesses so that they do not push the
   // hand-off slots out of L2.
   float giA[4] = {0.f, 0.f, 0.f, 0.f}, giB[4] = {0.f, 0.f, 0.f, 0.f};
@@ -735,11 +760,17 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
       c_reg = c;
       if constexpr (!FAST) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
       word_put<FAST>(xg + (size_t)(t & 3) * slot_words, woff, canon_nan(h));
-      __builtin_nontemporal_store(h, byte_at(hs_row + (size_t)(t + 1) * plane, 4u * cu));
-      __builtin_nontemporal_store(c, byte_at(cs_row + (size_t)(t + 1) * plane, 4u * cu));
-      __builtin_nontemporal_store(tc, byte_at(tc_row + (size_t)t * plane, 4u * cu));
-      __builtin_nontemporal_store(f4{act[0], act[1], act[2], act[3]},
-                                  reinterpret_cast<f4*>(byte_at(ga_row + (size_t)t * plane4, 16u * cu)));
+      if constexpr (XP) {  // projection wave q stores them (store_saves)
+        float* const sv = &(*save_buf(xin))[t & 1][q][lane & 15][0];
+        *reinterpret_cast<f4*>(sv) = f4{h, c, tc, 0.f};
+        *reinterpret_cast<f4*>(sv + 4) = f4{act[0], act[1], act[2], act[3]};
+      } else {
+        __builtin_nontemporal_store(h, byte_at(hs_row + (size_t)(t + 1) * plane, 4u * cu));
+        __builtin_nontemporal_store(c, byte_at(cs_row + (size_t)(t + 1) * plane, 4u * cu));
+        __builtin_nontemporal_store(tc, byte_at(tc_row + (size_t)t * plane, 4u * cu));
+        __builtin_nontemporal_store(f4{act[0], act[1], act[2], act[3]},
+                                    reinterpret_cast<f4*>(byte_at(ga_row + (size_t)t * plane4, 16u * cu)));
+      }
       word_put<FAST>(xg + (size_t)((t + 2) & 3) * slot_words, woff, __uint_as_float(kEmpty));
     }
     if constexpr (XP && kXprojAfterPublish) {  // the projection waves' products may start now
@@ -848,6 +879,7 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
       if (t >= T) return false;
       lds_barrier();  // the recurrent waves' barrier of this step
       if (abort_flag) return false;
+      if (t > 0) store_saves(p, grp, wg, save_buf(xin), w, t - 1);  // staged before this barrier
       if (next && sub == 6) {  // block j+1, whose products ended a step ago, to xin
         write_blk(j + 1);
         load_blk(j + 3, xu);
@@ -898,7 +930,7 @@ __device__ void poison_fwd(const PFwdArgs& p, int grp, int wg) {
 }
 
 // XP: 512 threads; waves 4-7 compute the input projection (rec_fwd_xproj), which then
-// is not read from gih.  Every wave ends with one more workgroup barrier: a wave that
+// is not read from gih, and store the saved activations.  Every wave ends with one more workgroup barrier: a wave that
 // gave up a wait has set abort_flag before it (waves that left early have terminated
 // and are not waited for), so all waves agree on whether to poison their outputs.
 template <int KQ, bool XP>
@@ -929,8 +961,19 @@ __global__ __launch_bounds__(XP ? 512 : 256, 1) void rec_fwd_persistent(PFwdArgs
         rec_fwd_body<KQ, false, XP>(p, grp, wg, red, xin, abort_flag);
     }
   }
+  // The projection waves' save stores complete before the barrier (workgroup-scope
+  // release), so that the poison stores after it are the last writes.  The last step's
+  // activations, staged before it, are stored after it.
+  if (XP && threadIdx.x >= 256) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   lds_barrier();
-  if (abort_flag && threadIdx.x < 256) poison_fwd(p, grp, wg);
+  if constexpr (XP) {
+    if (threadIdx.x >= 256 && !abort_flag && p.T > 0)
+      store_saves(p, grp, wg, save_buf(xin), (threadIdx.x >> 6) - 4, p.T - 1);
+  }
+  if (abort_flag && threadIdx.x < 256) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    poison_fwd(p, grp, wg);
+  }
 }
 
 // Per-step inputs of the persistent backward, loaded one step ahead: dout[t], c_{t-1}
@@ -1795,7 +1838,7 @@ int check_dims(int T, int B, int D, int H) {
 
 template <int KQ>
 void launch_fwd_persistent(const PFwdArgs& a, int grid, bool xp, hipStream_t s) {
-  static_assert(sizeof(XinBuf) <= (size_t)kPadLdsBytes, "xin lives in the padding LDS");
+  static_assert(sizeof(XinBuf) + sizeof(SaveBuf) <= (size_t)kPadLdsBytes, "xin and the staged saves live in the padding LDS");
   if (xp)
     hipLaunchKernelGGL((rec_fwd_persistent<KQ, true>), dim3(grid), dim3(512), kPadLdsBytes, s, a);
   else

@@ -641,19 +641,23 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
     }
   }
 
-  // cell thread: wave q, lane < 16 -> (batch slot q, unit cu); cb is wave-uniform
+  // cell lanes: wave q, lane < 16 -> (batch slot q, unit cu); cb is wave-uniform.  The
+  // gate pre-activations are formed and activated one gate per lane (gate lane/16, unit
+  // lane%16) by all 64 lanes, and lanes 0-15 gather their unit's other three gates.
   const int cb = grp * Bg + q;
   const unsigned cu = wg * kUnits + (lane & 15);
-  const bool c_ok = lane < kUnits && q < Bg && cb < B && (int)cu < H;
+  const int lgate = lane >> 4;
+  const bool u_ok = q < Bg && cb < B && (int)cu < H;
+  const bool c_ok = lane < kUnits && u_ok;
   const int cbc = cb < B ? cb : 0;  // clamped for the uniform bases below
-  float bs[4] = {0.f, 0.f, 0.f, 0.f};
+  const unsigned cuc = (int)cu < H ? cu : H - 1;
+  float bl = 0.f;  // the lane's gate bias: a_g b_hh (+ b_ih when the projection is fused)
   float c_reg = 0.f;
+  if (u_ok) {
+    bl = p.a[lgate] * p.b_hh[lgate * H + cu];
+    if constexpr (XP) bl = p.b_ih[lgate * H + cu] + bl;  // the projection's bias joins here
+  }
   if (c_ok) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      bs[g] = p.a[g] * p.b_hh[g * H + cu];
-      if constexpr (XP) bs[g] = p.b_ih[g * H + cu] + bs[g];  // the projection's bias joins here
-    }
     const size_t b0 = (size_t)cb * H + cu;
     c_reg = p.c0 ? p.c0[b0] : 0.f;
     p.h_save[b0] = p.h0 ? p.h0[b0] : 0.f;
@@ -689,15 +693,15 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
   // completed once the next receive has (one in-order completion counter).
   // The streamed activations use non-temporal accesses so that they do not push the
   // hand-off slots out of L2.
-  float giA[4] = {0.f, 0.f, 0.f, 0.f}, giB[4] = {0.f, 0.f, 0.f, 0.f};
-  if (!XP && c_ok) {
-#pragma unroll
-    for (int gt = 0; gt < 4; ++gt) giA[gt] = gih_row[gt * H + cu];
-  }
+  // (the lane's gate of) the input projection of a step; clamped address, so that the
+  // load needs no condition
+  const unsigned goff = 4u * (lgate * H + cuc);
+  float giA = 0.f, giB = 0.f;
+  if constexpr (!XP) giA = *byte_at(gih_row, goff);
 
-  // One step; gi holds this step's projection row, gn receives the next one.  Returns
+  // One step; gi holds this step's projection value, gn receives the next one.  Returns
   // false when the group aborted.
-  auto step = [&](int t, float (&gi)[4], float (&gn)[4]) __attribute__((always_inline)) -> bool {
+  auto step = [&](int t, float& gi, float& gn) __attribute__((always_inline)) -> bool {
     // XP: projection wave q's partials of this step (lane = gate row, element = batch
     // slot) seed the accumulator of wave q, so the workgroup sum below includes x_t W_ih^T
     f4 xp = f4{0.f, 0.f, 0.f, 0.f};
@@ -721,12 +725,8 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
         asm volatile("" : "+v"(hv[j]));  // settled before the loads below are issued
       }
     }
-    asm volatile("" : "+v"(gi[0]), "+v"(gi[1]), "+v"(gi[2]), "+v"(gi[3]));
-    if (!XP && c_ok && t + 1 < T) {
-      const float* g = gih_row + (size_t)(t + 1) * plane4;
-#pragma unroll
-      for (int gt = 0; gt < 4; ++gt) gn[gt] = __builtin_nontemporal_load(byte_at(g, 4u * (gt * H + cu)));
-    }
+    asm volatile("" : "+v"(gi));
+    if (!XP && t + 1 < T) gn = __builtin_nontemporal_load(byte_at(gih_row + (size_t)(t + 1) * plane4, goff));
     f4 acc[4];
     acc[0] = xp;
 #pragma unroll
@@ -742,18 +742,22 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
     lds_barrier();
     if (abort_flag) return false;
 
+    // every lane: its gate of its unit (the four k-quarter sums of the row), then lanes
+    // 0-15 take f, g and o of their unit from lanes +16, +32 and +48 (gfx950 row and half
+    // swaps; the second result of a swap holds lane l+16 or l+32 in rows 0 and 2)
+    float act[4];
+    {
+      const f4 pr = red[t & 1][q][lane];
+      const float mm = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+      act[0] = sigmoid_f((XP ? mm : gi + mm) + bl);
+      const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(act[0]), __float_as_uint(act[0]), false, false);
+      const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(act[0]), __float_as_uint(act[0]), false, false);
+      const auto s48 = __builtin_amdgcn_permlane32_swap(s16[1], s16[1], false, false);
+      act[1] = __uint_as_float(s16[1]);
+      act[2] = __uint_as_float(s32[1]);
+      act[3] = __uint_as_float(s48[1]);
+    }
     if (c_ok) {
-      const int uu = lane & 15;
-      float act[4];
-      f4 pr[4];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) pr[g] = red[t & 1][q][g * kUnits + uu];
-      asm volatile("" : "+v"(pr[0]), "+v"(pr[1]), "+v"(pr[2]), "+v"(pr[3]));  // four reads in flight
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float mm = (pr[g][0] + pr[g][1]) + (pr[g][2] + pr[g][3]);
-        act[g] = sigmoid_f((XP ? mm : gi[g] + mm) + bs[g]);
-      }
       const float c = act[1] * c_reg + act[0] * act[2];
       const float tc = tanh_f(c);
       const float h = act[3] * tc;

@@ -1534,6 +1534,8 @@ __global__ __launch_bounds__(XT >= 0 ? 512 : 256, 1) void rec_bwd_persistent(PBw
   }
 }
 
+#include "rec_wide.h"
+
 // ---------------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------------
@@ -1643,6 +1645,26 @@ int plan_persistent(int B, int H, int D, bool bwd, PersistentPlan* pl) {
   return HSL_OK;
 }
 
+// The W_hh-resident forward for large H (rec_wide.h): H = 2048, B <= 32, eight XCDs and all
+// 256 workgroups resident at once (one per CU).
+struct WidePlan {
+  bool ok = false;
+};
+
+constexpr size_t kWideLdsBytes = WideShape<64>::RED_BYTES;  // 128 KB: one workgroup per CU
+
+int plan_wide(int B, int H, WidePlan* pl) {
+  *pl = WidePlan{};
+  if (recurrent_path_mode() == 1 || B < 1 || B > 32 || H != 2048) return HSL_OK;
+  DeviceInfo di;
+  HSL_CHECK(device_info(&di));
+  if (di.num_xcds != kWideXcds || di.num_cus < kWideWgs) return HSL_OK;
+  int occ = 0;
+  HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, rec_fwd_wide<64>, 256, kWideLdsBytes));
+  pl->ok = occ >= 1 && (long)occ * di.num_cus >= kWideWgs;
+  return HSL_OK;
+}
+
 // Steps per fp32 partial plane of the fused weight gradients: at most 128 steps
 // (512 products per running sum at four batch slots) while there are at most 8 planes
 // per group.
@@ -1708,6 +1730,9 @@ struct FwdWs {
   unsigned long long* hello;  // [NG*Hp/16]  (persistent)
   size_t hwords;
   float* gih;                 // [T*B*4H]    (input projection not fused)
+  float* wbuf;                // h blocks, then partial inboxes (wide persistent)
+  size_t wfloats, whfloats;   // all of wbuf; its h blocks
+  unsigned long long* whello; // [256]       (wide persistent)
   float* w_perm;              // [4H*H]      (per-step)
   float* bs;                  // [4H]        (per-step)
   float* part;                // [S*B*4H]    (per-step split-K planes)
@@ -1717,7 +1742,7 @@ struct FwdWs {
 // [T,B,4H] input-gate buffer (not when the projection is fused into the persistent
 // kernel) and the per-step buffers.  All three when the path is not known (no device).
 struct FwdNeeds {
-  bool xch = true, gih = true, step = true;
+  bool xch = true, gih = true, step = true, wide = true;
 };
 
 size_t carve_fwd(void* ws, size_t cap, int T, int B, int H, FwdNeeds nd, FwdWs* o) {
@@ -1733,6 +1758,13 @@ size_t carve_fwd(void* ws, size_t cap, int T, int B, int H, FwdNeeds nd, FwdWs* 
     o->hello = c.take<unsigned long long>(o->hwords);
   }
   if (nd.gih) o->gih = c.take<float>((size_t)T * B * 4 * H);
+  if (nd.wide && H == 2048) {
+    const size_t U = 64;
+    o->whfloats = (size_t)kWideHSlots * kWideXcds * kWideRowSubs * 32 * U;
+    o->wfloats = o->whfloats + (size_t)kWidePSlots * kWideWgs * kWideKBlocks * (U / 8) * 32 * 4;
+    o->wbuf = c.take<float>(o->wfloats);
+    o->whello = c.take<unsigned long long>(kWideWgs);
+  }
   if (nd.step) {
     o->w_perm = c.take<float>((size_t)4 * H * H);
     o->bs = c.take<float>((size_t)4 * H);
@@ -1745,11 +1777,12 @@ size_t carve_fwd(void* ws, size_t cap, int T, int B, int H, FwdNeeds nd, FwdWs* 
 
 // The workspace parts of a forward call with this plan; the fused projection needs a
 // 16-byte aligned x.
-FwdNeeds fwd_needs(const PersistentPlan& pl, bool x_aligned) {
+FwdNeeds fwd_needs(const PersistentPlan& pl, const WidePlan& wp, bool x_aligned) {
   FwdNeeds nd;
   nd.xch = pl.ok;
   nd.gih = !(pl.ok && pl.XP && x_aligned);
-  nd.step = !pl.ok;
+  nd.wide = !pl.ok && wp.ok;
+  nd.step = !pl.ok && !wp.ok;
   return nd;
 }
 
@@ -1929,7 +1962,9 @@ size_t hsl_rec_fwd_ws_bytes(int T, int B, int D, int H) {
   FwdWs w;
   FwdNeeds nd;  // every part when the path cannot be planned (no device)
   PersistentPlan pl;
-  if (B > 0 && H > 0 && plan_persistent(B, H, D, false, &pl) == HSL_OK) nd = fwd_needs(pl, true);
+  WidePlan wp;
+  if (B > 0 && H > 0 && plan_persistent(B, H, D, false, &pl) == HSL_OK && plan_wide(B, H, &wp) == HSL_OK)
+    nd = fwd_needs(pl, wp, true);
   return carve_fwd(nullptr, 0, T, B, H, nd, &w);
 }
 
@@ -1943,18 +1978,22 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
     return fail(HSL_ERR_ARG, "hsl_rec_fwd: null pointer");
   PersistentPlan pl;
   HSL_CHECK(plan_persistent(B, H, D, false, &pl));
-  if (recurrent_path_mode() == 2 && !pl.ok)
+  WidePlan wp;
+  if (!pl.ok) HSL_CHECK(plan_wide(B, H, &wp));
+  if (recurrent_path_mode() == 2 && !pl.ok && !wp.ok)
     return fail(HSL_ERR_UNSUPPORTED, "persistent path does not fit (B=%d H=%d)", B, H);
   const bool x_aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0;
   if (pl.XP && !x_aligned) pl.XP = false;  // the fused projection loads x in 16-byte pieces
   FwdWs w;
-  const size_t need = carve_fwd(ws, ws_bytes, T, B, H, fwd_needs(pl, x_aligned), &w);
+  const size_t need = carve_fwd(ws, ws_bytes, T, B, H, fwd_needs(pl, wp, x_aligned), &w);
   if (!ws || ws_bytes < need)
     return fail(HSL_ERR_ARG, "hsl_rec_fwd: workspace %zu bytes, need %zu%s", ws_bytes, need,
                 pl.ok && !x_aligned ? " (x is not 16-byte aligned, so the input-gate buffer is needed)" : "");
 
   if (pl.ok && T > 0)
     HSL_CHECK(prepare_persistent(w.err, w.xbuf, w.xfloats, w.hello, w.hwords, s));
+  else if (wp.ok && T > 0)
+    HSL_CHECK(prepare_persistent(w.err, w.wbuf, w.wfloats, w.whello, kWideWgs, s));
   else
     HSL_CHECK(zero_words(reinterpret_cast<unsigned long long*>(w.err), 32, s));
   if (T == 0) {
@@ -1984,6 +2023,16 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
     HSL_HIP(hipGetLastError());
     timing_end(slot, s);
     note_recurrent_path(2);
+    return HSL_OK;
+  }
+  if (wp.ok) {
+    WFwdArgs wa{w.gih, w_hh, b_hh, a, h0, c0, h_save, c_save, gact, tanh_c, w.wbuf, w.wbuf + w.whfloats, w.whello,
+                w.err, T, B, H, exchange_scope_mode(), spin_timeout_ticks()};
+    const int slot = timing_begin(kTimeRecFwd, s);
+    hipLaunchKernelGGL(rec_fwd_wide<64>, dim3(kWideWgs), dim3(256), kWideLdsBytes, s, wa);
+    HSL_HIP(hipGetLastError());
+    timing_end(slot, s);
+    note_recurrent_path(3);
     return HSL_OK;
   }
 
@@ -2033,10 +2082,12 @@ int hsl_rec_fwd_noalloc(const float* x, const float* h0, const float* c0, const 
   if (B == 0 || H == 0) return HSL_OK;
   PersistentPlan pl;
   HSL_CHECK(plan_persistent(B, H, D, false, &pl));
+  WidePlan wp;
+  if (!pl.ok) HSL_CHECK(plan_wide(B, H, &wp));
   const bool x_aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0;
   if (pl.XP && !x_aligned) pl.XP = false;
   FwdWs w;
-  const size_t need = carve_fwd(nullptr, 0, T, B, H, fwd_needs(pl, x_aligned), &w);
+  const size_t need = carve_fwd(nullptr, 0, T, B, H, fwd_needs(pl, wp, x_aligned), &w);
   if (need > kNoAllocScratchBytes)
     return fail(HSL_ERR_UNSUPPORTED,
                 "hsl_rec_fwd_noalloc: T=%d B=%d D=%d H=%d needs %zu bytes of scratch, more than the %zu bytes of "

@@ -46,6 +46,7 @@ def _run_gpu(m, x, hx, wts, dev):
     if hx is not None:
         hx = tuple(t.to(dev).requires_grad_(True) for t in hx)
     out, (h_n, c_n) = m(x, hx)
+    fwd_path = prlstm_amd.last_recurrent_path()
     w = [t.to(dev) for t in wts]
     loss = (out * w[0]).sum() + (h_n[0] * w[1]).sum() + (c_n[0] * w[2]).sum()
     loss.backward()
@@ -54,10 +55,13 @@ def _run_gpu(m, x, hx, wts, dev):
         res["d" + n] = p.grad
     if hx is not None:
         res["dh0"], res["dc0"] = hx[0].grad, hx[1].grad
-    return res
+    return res, fwd_path
 
 
-def check(T, B, D, H, dev, path, a=None, seed=0, with_hx=False, batch_first=False):
+def check(T, B, D, H, dev, path, a=None, seed=0, with_hx=False, batch_first=False, fwd_path=None):
+    """path: 1 or 2 forces that path (and checks the backward took it); 0 lets the library
+    choose.  fwd_path: the path the forward must have taken (3 = the W_hh-resident forward
+    for large H)."""
     print(f"recurrent T={T} B={B} D={D} H={H} path={path} a={a} hx={with_hx} bf={batch_first}",
           flush=True)
     torch.manual_seed(seed)
@@ -84,8 +88,11 @@ def check(T, B, D, H, dev, path, a=None, seed=0, with_hx=False, batch_first=Fals
     m.load_state_dict(ref.state_dict())
     m = m.to(dev)
     prlstm_amd.set_recurrent_path(path)
-    rg = _run_gpu(m, x, hx, wts, dev)
-    assert prlstm_amd.last_recurrent_path() == path
+    rg, fp = _run_gpu(m, x, hx, wts, dev)
+    if path:
+        assert prlstm_amd.last_recurrent_path() == path
+    if fwd_path is not None:
+        assert fp == fwd_path, (fp, fwd_path)
     torch.cuda.synchronize()
     for k in r32:
         assert_parity(k, rg[k], r32[k], r64[k])
@@ -162,8 +169,22 @@ def test_per_step_split_products(dev):
 
 
 def test_config3_large_hidden(dev):
-    """T64 B32 D1024 H2048 (per-step path: W_hh does not fit on chip)."""
+    """T64 B32 D1024 H2048 on the one-launch-per-step path."""
     check(64, 32, 1024, 2048, dev, 1)
+
+
+def test_config3_wide_forward(dev):
+    """configs[3] with the automatic path: the forward holds W_hh (64 MiB) in the registers
+    of 256 workgroups (rec_fwd_wide, path 3); the backward runs one launch per step."""
+    check(64, 32, 1024, 2048, dev, 0, fwd_path=3)
+
+
+@pytest.mark.parametrize("scope", [0, 1])
+def test_wide_forward_partial_batch_hx(dev, scope):
+    """The wide forward with B < 32 (absent batch columns), h0/c0 given, a ~ U(0, 0.5), and
+    with device-scope stores for the partial exchange (scope 1)."""
+    prlstm_amd.set_exchange_scope(scope)
+    check(6, 20, 64, 2048, dev, 0, a=[0.3, 0.5, 0.1, 0.2], with_hx=True, fwd_path=3)
 
 
 def test_sgd_training_step(dev):

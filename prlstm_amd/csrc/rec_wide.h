@@ -2,22 +2,27 @@
 // configs[3]), B <= 32.  Included by recurrent.hip: it shares that file's hand-off
 // helpers and its device error word.
 //
-// W_hh (a-scaled) stays in registers for the whole launch: 64 MiB at H = 2048 is 256 KB per
-// CU over 256 workgroups, where the per-step path streams it from the Infinity Cache every
-// step (_torch.py:111-120 runs one h W_hh^T product per step).  Workgroup (x, r, kb),
+// W_hh stays in registers for the whole launch: 64 MiB at H = 2048 is 256 KB per CU over
+// 256 workgroups, where the per-step path streams it from the Infinity Cache every step
+// (_torch.py:111-120 runs one h W_hh^T product per step).  Workgroup (x, r, kb),
 // blockIdx = x + 8 (8 r + kb), sits on XCD x:
-//   rows: the four gates of units [4U x + U r, +U) (4U gate rows, unit-interleaved);
-//   k:    units [4U kb, +4U); wave w takes [4U kb + U w, +U).
-// Wave w holds its 4U x U block of W in registers (U^2 / 16 per lane: 256 at U = 64) and
-// multiplies it with h_{t-1}[32 batch][its U units] on v_mfma_f32_32x32x2_f32 (M = gate
-// rows, N = batch, 4U/32 row tiles x U/2 k-steps).  Per step:
+//   rows: the four gates of units [4U x + U r, +U) (4U gate rows, unit-interleaved); wave w
+//         takes units [U w / 4, +U/4) of them (two row tiles of 32);
+//   k:    units [4U kb, +4U), all of them for every wave (4U/2 k-steps).
+// Wave w holds its 64 x 256 block of W in the accumulator registers (256 per lane) and
+// multiplies it with h_{t-1}[32 batch][the workgroup's 4U k units] on
+// v_mfma_f32_32x32x2_f32 (M = gate rows, N = batch).  Per step:
 //   1. receive: wave w reads h block (kb, w) (the 32 x U values that row group (kb, w)
-//      publishes) -- from another XCD for 7 of 8 workgroups;
-//   2. products; the four waves' partials go to LDS and are summed there;
-//   3. the workgroup's partial for the 8 slices of U/8 units goes to the 8 workgroups
-//      (x, r, j) of its row group, one slice each (XCD-local);
-//   4. lane (unit su of slice kb, batch b) sums the 8 partials of its slice in source
-//      order, runs the cell and publishes h_t[b][unit] in h block (x, r).
+//      publishes) -- from another XCD for 7 of 8 workgroups -- into LDS, where all four
+//      waves read the workgroup's four blocks as product operands;
+//   2. products; each wave's accumulators are the workgroup's partial (over k block kb) of
+//      its 16 units, two slices of 8 units, sent to the workgroups (x, r, j) of its row group
+//      that run those slices' cells (XCD-local);
+//   3. lane (unit su of slice kb, batch b) sums the 8 partials of its slice in source
+//      order and runs the cell; the workgroup's 256 h values are one contiguous 1 KB group
+//      of h block (x, r), gathered in LDS and published by one wave in full cache lines
+//      (scattered 4-byte device-scope stores from 256 lanes took about 1 us longer to
+//      reach the readers on the other XCDs).
 // Hand-off words are 4-byte values that start out kEmpty, as in the other persistent
 // kernels.  h blocks cross XCDs: device-scope stores and loads.  Partials stay on the XCD:
 // workgroup-scope stores (sc0) when every member of the row group runs on the group's XCD.
@@ -38,14 +43,15 @@ constexpr int kWideHSlots = 4, kWidePSlots = 3;
 
 template <int U>
 struct WideShape {
-  static constexpr int KS = U / 2;          // k-steps of 2 per wave
-  static constexpr int RT = 4 * U / 32;     // row tiles of 32 gate rows
-  static constexpr int SU = U / 8;          // units per slice
+  static constexpr int KS = 2 * U;          // k-steps of 2 per wave (4U k units)
+  static constexpr int SU = U / 8;          // units per slice (8 slices per workgroup)
   static constexpr int CELLS = SU * 32;     // cell lanes (slice units x 32 batch)
   static constexpr int HW = 32 * U;         // words of an h block
   static constexpr int PW = SU * 32 * 4;    // words of one partial slice (one source)
   static constexpr int IW = kWideKBlocks * PW;  // inbox words of a workgroup (8 sources)
-  static constexpr int RED_BYTES = 4 * U * 32 * 16;  // LDS: [wave][unit][batch] f4
+  // LDS: the workgroup's four h blocks, double-buffered: [step parity][block][k-step/4][lane] f4
+  static constexpr int HS_F4 = 4 * (U / 2 / 4) * 64;  // f4 per buffer
+  static constexpr int LDS_BYTES = 2 * HS_F4 * 16;
 };
 
 struct WFwdArgs {
@@ -68,147 +74,136 @@ struct WFwdArgs {
   long long spin;
 };
 
-// Word of (batch b, unit kk of the block) in an h block: lane l = b + 32 (kk % 2) of a reader
-// wave loads the 8-byte pairs (kk/2 = 2j, 2j + 1) at 128 j + 2 l.
-__device__ __forceinline__ unsigned wide_hpos(int b, int kk) {
-  const int i = kk >> 1, l = b + 32 * (kk & 1);
-  return 128u * (i >> 1) + 2u * l + (i & 1);
+// Layout of an h block (32 batch x U units of a row group): the operand of k-step i of the
+// products for lane l (batch l%32, unit 2 i + l/32 of the block) is word 256 (i/4) + 4 l +
+// i%4.  A reader lane loads its 16-byte groups j at 256 j + 4 l; group j (1 KB over the
+// 64 lanes) is exactly what row-group member kb = j publishes (units 8j .. 8j+7).
+
+// Hand-off buffers addressed as raw buffers, so that a lane moves 16 bytes in one access
+// with the coherence bits of the relaxed atomics it replaces: loads sc1 (served by the
+// device's coherent level, as an agent-scope atomic load), stores sc0 (XCD L2, workgroup
+// scope) or sc1 (agent scope).  Each 4-byte word is written whole, and readers accept a
+// word only when it is not kEmpty, so 16-byte accesses need no further ordering.
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
+constexpr int kCpolSc0 = 1, kCpolSc1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wide_rsrc(const float* base, size_t words) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)(4 * words), 0x00020000);
+}
+__device__ __forceinline__ u4v quad_load(__amdgpu_buffer_rsrc_t r, unsigned word) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)(4u * word), 0, kCpolSc1);
+}
+template <bool FAST>
+__device__ __forceinline__ void quad_store(__amdgpu_buffer_rsrc_t r, unsigned word, u4v v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)(4u * word), 0, FAST ? kCpolSc0 : kCpolSc1);
 }
 
-// Polls the lane's N 16-byte groups until no word is kEmpty (groups with expect false are
-// skipped).  Returns false after raising the error flags when the spin limit runs out.
+// Polls the lane's N 16-byte groups until no word is kEmpty (nothing is awaited when
+// expect is false).  Every poll reloads all N groups: that keeps the loop's live state to
+// the values themselves.  kEmpty is the largest 32-bit pattern, so the groups are complete
+// when the maximum of their words differs from it.  Returns false after raising the error
+// flags when the spin limit runs out.
 template <int N>
-__device__ __forceinline__ bool quads_wait(const float* base, const unsigned (&off)[N], bool expect, f4 (&v)[N],
-                                           long long spin, int* abort_flag, int* err) {
-  auto load = [&](int i) {
-    const unsigned long long* p = byte_at(reinterpret_cast<const unsigned long long*>(base), 4u * off[i]);
-    const unsigned long long lo = __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned long long hi = __hip_atomic_load(const_cast<unsigned long long*>(p + 1), __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-    v[i] = f4{__uint_as_float((unsigned)lo), __uint_as_float((unsigned)(lo >> 32)), __uint_as_float((unsigned)hi),
-              __uint_as_float((unsigned)(hi >> 32))};
-  };
-  auto full = [&](int i) {
-    return __float_as_uint(v[i][0]) != kEmpty && __float_as_uint(v[i][1]) != kEmpty &&
-           __float_as_uint(v[i][2]) != kEmpty && __float_as_uint(v[i][3]) != kEmpty;
-  };
-  bool need[N];
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    need[i] = expect;
-    v[i] = f4{0.f, 0.f, 0.f, 0.f};
-    if (need[i]) load(i);
-  }
+__device__ __forceinline__ bool quads_wait(__amdgpu_buffer_rsrc_t r, const unsigned (&off)[N], bool expect,
+                                           f4 (&v)[N], long long spin, int* abort_flag, int* err) {
   const long long t0 = wall_clock64();
   while (true) {
-    bool ok = true;
+    unsigned m = 0u;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      need[i] = need[i] && !full(i);
-      ok = ok && !need[i];
+      const u4v q = expect ? quad_load(r, off[i]) : u4v{0u, 0u, 0u, 0u};
+      m = max(m, max(max(q[0], q[1]), max(q[2], q[3])));
+      v[i] = f4{__uint_as_float(q[0]), __uint_as_float(q[1]), __uint_as_float(q[2]), __uint_as_float(q[3])};
     }
-    if (__all(ok)) return true;
+    if (__all(m != kEmpty)) return true;
     if (wall_clock64() - t0 > spin) {
       raise_abort(abort_flag, err);
       return false;
     }
-#pragma unroll
-    for (int i = 0; i < N; ++i)
-      if (need[i]) load(i);
   }
 }
 
 template <bool FAST>
-__device__ __forceinline__ void quad_put(float* base, unsigned off, f4 v) {
-  unsigned long long* p = byte_at(reinterpret_cast<unsigned long long*>(base), 4u * off);
-  const unsigned long long lo = (unsigned long long)__float_as_uint(canon_nan(v[0])) |
-                                ((unsigned long long)__float_as_uint(canon_nan(v[1])) << 32);
-  const unsigned long long hi = (unsigned long long)__float_as_uint(canon_nan(v[2])) |
-                                ((unsigned long long)__float_as_uint(canon_nan(v[3])) << 32);
-  if constexpr (FAST) {
-    __hip_atomic_store(p, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    __hip_atomic_store(p + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  } else {
-    __hip_atomic_store(p, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+__device__ __forceinline__ void quad_put(__amdgpu_buffer_rsrc_t r, unsigned word, f4 v) {
+  quad_store<FAST>(r, word, u4v{__float_as_uint(canon_nan(v[0])), __float_as_uint(canon_nan(v[1])),
+                                __float_as_uint(canon_nan(v[2])), __float_as_uint(canon_nan(v[3]))});
 }
 
-template <bool FAST>
-__device__ __forceinline__ void quad_clear(float* base, unsigned off) {
-  unsigned long long* p = byte_at(reinterpret_cast<unsigned long long*>(base), 4u * off);
-  if constexpr (FAST) {
-    __hip_atomic_store(p, kEmpty2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    __hip_atomic_store(p + 1, kEmpty2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  } else {
-    __hip_atomic_store(p, kEmpty2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p + 1, kEmpty2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
-// One k-step of the wide products: acc[rt] += W[rt] h for the RT row tiles, on
-// v_mfma_f32_32x32x2_f32 with the W operand read from the accumulator register file (the
-// compiler does not keep a 256-register operand block there by itself).  The leading nops
-// separate the VALU writes of h and of the zeroed accumulators from the products' reads; the
-// RT accumulators are independent, so a tile's next product is RT products behind.
-template <int RT>
-__device__ __forceinline__ void wide_kstep(f16v (&acc)[RT], const float (&w)[RT], float h) {
-  static_assert(RT == 8, "eight row tiles (U = 64)");
+// Four k-steps of the wide products for the wave's two row tiles: acc[rt + 2 (k % 2)] +=
+// W[k][rt] h[k], on v_mfma_f32_32x32x2_f32 with the W operand read from the accumulator
+// register file (the compiler does not keep a 256-register operand block there by itself).
+// Even and odd k-steps go to separate accumulators, so a product depends on the one two
+// instructions back.  The leading nops separate VALU writes of the operands from the
+// products' reads.
+__device__ __forceinline__ void wide_ksteps4(f16v (&acc)[4], const float (&w)[4][2], f4 h) {
   asm volatile(
       "s_nop 1\n\t"
-      "v_mfma_f32_32x32x2_f32 %0, %8, %16, %0\n\t"
-      "v_mfma_f32_32x32x2_f32 %1, %9, %16, %1\n\t"
-      "v_mfma_f32_32x32x2_f32 %2, %10, %16, %2\n\t"
-      "v_mfma_f32_32x32x2_f32 %3, %11, %16, %3\n\t"
-      "v_mfma_f32_32x32x2_f32 %4, %12, %16, %4\n\t"
-      "v_mfma_f32_32x32x2_f32 %5, %13, %16, %5\n\t"
-      "v_mfma_f32_32x32x2_f32 %6, %14, %16, %6\n\t"
-      "v_mfma_f32_32x32x2_f32 %7, %15, %16, %7"
-      : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]), "+v"(acc[6]),
-        "+v"(acc[7])
-      : "a"(w[0]), "a"(w[1]), "a"(w[2]), "a"(w[3]), "a"(w[4]), "a"(w[5]), "a"(w[6]), "a"(w[7]), "v"(h));
+      "v_mfma_f32_32x32x2_f32 %0, %4, %12, %0\n\t"
+      "v_mfma_f32_32x32x2_f32 %1, %5, %12, %1\n\t"
+      "v_mfma_f32_32x32x2_f32 %2, %6, %13, %2\n\t"
+      "v_mfma_f32_32x32x2_f32 %3, %7, %13, %3\n\t"
+      "v_mfma_f32_32x32x2_f32 %0, %8, %14, %0\n\t"
+      "v_mfma_f32_32x32x2_f32 %1, %9, %14, %1\n\t"
+      "v_mfma_f32_32x32x2_f32 %2, %10, %15, %2\n\t"
+      "v_mfma_f32_32x32x2_f32 %3, %11, %15, %3"
+      : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])
+      : "a"(w[0][0]), "a"(w[0][1]), "a"(w[1][0]), "a"(w[1][1]), "a"(w[2][0]), "a"(w[2][1]), "a"(w[3][0]),
+        "a"(w[3][1]), "v"(h[0]), "v"(h[1]), "v"(h[2]), "v"(h[3]));
 }
 
 // Wait states after the last products of a step, before any instruction reads their
 // accumulators (an XDL result read by VALU, LDS or memory instructions needs up to 18 on
 // the 16-pass 32x32x2; the compiler cannot see inside the asm above, so it adds none).
-template <int RT>
-__device__ __forceinline__ void wide_kstep_drain(f16v (&acc)[RT]) {
+__device__ __forceinline__ void wide_ksteps_drain(f16v (&acc)[4]) {
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+v"(acc[rt]));
+  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i]));
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+v"(acc[rt]));
+  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i]));
 }
 
 template <int U, bool FAST>
-__device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int r, int kb, f4* red,
+__device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int r, int kb, f4* hs,
                                                   int& abort_flag) {
   using S = WideShape<U>;
+  static_assert(U == 64, "the row tiles and slices below assume U = 64");
   const int T = p.T, B = p.B, H = p.H;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
 
-  // W_hh block of this wave: row tile rt, k-step i -> row m = l%32 of the tile (unit offset
-  // (32 rt + m) / 4, gate m % 4), k = kbase + 2 i + l/32.  It is held unscaled (a register
-  // that only feeds the products can live in the accumulator file); the gate's a scales the
-  // summed product in the cell.
+  // W_hh block of this wave: row tile rt, k-step 4 i4 + e -> row m = l%32 of the tile (unit
+  // offset U w / 4 + (32 rt + m) / 4, gate m % 4), k = 4U kb + 2 (4 i4 + e) + l/32.  It is
+  // held unscaled (a register that only feeds the products can live in the accumulator
+  // file); the gate's a scales the summed product in the cell.
   const int ubase = 4 * U * x + U * r;  // first unit of the workgroup's rows
-  const int kbase = 4 * U * kb + U * w;  // first k (unit) of the wave's block
-  float wreg[S::KS][S::RT];
+  const int kbase = 4 * U * kb;         // first k (unit) of the workgroup's k block
+  float wreg[S::KS / 4][4][2];
+  {
+    const float* rows[2];
 #pragma unroll
-  for (int rt = 0; rt < S::RT; ++rt) {
-    const int rho = 32 * rt + l32, g = rho & 3, u = ubase + (rho >> 2);
-    const float* row = p.w_hh + ((size_t)g * H + u) * H + kbase + hb;
+    for (int rt = 0; rt < 2; ++rt) {
+      const int rho = 32 * rt + l32, g = rho & 3, u = ubase + U / 4 * w + (rho >> 2);
+      rows[rt] = p.w_hh + ((size_t)g * H + u) * H + kbase + hb;
+    }
+    // loaded 32 at a time and moved to the accumulator file group by group, so that the
+    // loads in flight never hold more than a few dozen VGPRs
 #pragma unroll
-    for (int i = 0; i < S::KS; ++i) wreg[i][rt] = row[2 * i];
+    for (int i8 = 0; i8 < S::KS / 4; i8 += 4) {
+#pragma unroll
+      for (int i4 = i8; i4 < i8 + 4; ++i4)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+            wreg[i4][e][rt] = rows[rt][2 * (4 * i4 + e)];
+#pragma unroll
+      for (int i4 = i8; i4 < i8 + 4; ++i4)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) asm volatile("" : "+a"(wreg[i4][e][rt]));  // held in the accumulator file
+    }
   }
-#pragma unroll
-  for (int i = 0; i < S::KS; ++i)
-#pragma unroll
-    for (int rt = 0; rt < S::RT; ++rt) asm volatile("" : "+a"(wreg[i][rt]));  // held in the accumulator file
 
   // cell lane: tid < CELLS -> unit su of this workgroup's slice kb, batch cb
   const int su = tid >> 5, cb = tid & 31;
@@ -229,46 +224,50 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
   }
   const size_t plane = (size_t)B * H, plane4 = 4 * plane;
   const int me = blockIdx.x;
-  // partial slice j of this workgroup -> inbox of workgroup (x, r, j), source kb
-  const unsigned pofs = (unsigned)kb * S::PW + 4u * (su * 32 + cb);
   const size_t inbox_slot = (size_t)kWideWgs * S::IW;
-  // own h word in block (x, r) and the words this wave reads in block (kb, w)
+  // this workgroup's 1 KB group of h block (x, r) (16-byte group j = kb of every lane) and
+  // the block (kb, w) this wave reads
   const size_t hblock = S::HW, hslot = (size_t)kWideXcds * kWideRowSubs * S::HW;
-  float* const hown = p.hbuf + (size_t)(x * kWideRowSubs + r) * hblock;
+  float* const hown = p.hbuf + (size_t)(x * kWideRowSubs + r) * hblock + 256u * kb;
   const float* const hsrc = p.hbuf + (size_t)(kb * kWideRowSubs + w) * hblock;
-  const unsigned hpos = wide_hpos(cb, S::SU * kb + su);
   const bool h_ok = l32 < B;  // batch column of this lane in the products
+  constexpr int NQ = U / 8;   // 16-byte groups a lane reads from an h block
+  __shared__ float hst[256];  // this step's h values, in the order of the 1 KB group
+  if (tid < 256) hst[tid] = 0.f;  // absent batch columns stay 0
 
   float gin[4] = {0.f, 0.f, 0.f, 0.f};
   for (int t = 0; t < T; ++t) {
-    // ---- 1. h_{t-1} of the wave's k block: hreg[i] = h[l%32][kbase + 2i + l/32] ----
-    float hreg[S::KS];
+    f4* const hsb = hs + (size_t)(t & 1) * S::HS_F4;
+    // ---- 1. h_{t-1} of block (kb, w) into LDS: group j of block w is
+    //         hs[t&1][(8 w + j) * 64 + lane], the operands of k-steps 4j .. 4j+3,
+    //         h[l%32][4U kb + U w + 2 (4j + e) + l/32] -----------------------------------
     if (t == 0) {
 #pragma unroll
-      for (int i = 0; i < S::KS; ++i) {
-        hreg[i] = (h_ok && p.h0) ? p.h0[(size_t)l32 * H + kbase + 2 * i + hb] : 0.f;
-        asm volatile("" : "+v"(hreg[i]));
+      for (int j = 0; j < NQ; ++j) {
+        f4 v = f4{0.f, 0.f, 0.f, 0.f};
+        if (h_ok && p.h0) {
+          const float* row = p.h0 + (size_t)l32 * H + kbase + U * w + hb;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = row[2 * (4 * j + e)];
+        }
+        hsb[(NQ * w + j) * 64 + lane] = v;
       }
     } else {
-      constexpr int NW = S::KS;  // words per lane (pairs loaded together)
-      const float* src = hsrc + (size_t)((t - 1) % kWideHSlots) * hslot;
-      bool need[NW / 2];
-      unsigned long long v2[NW / 2];
+      // groups j at 256 j + 4 lane; groups still holding a kEmpty word are loaded again
+      const __amdgpu_buffer_rsrc_t src = wide_rsrc(hsrc + (size_t)((t - 1) % kWideHSlots) * hslot, S::HW);
+      bool need[NQ];
+      u4v q4[NQ];
 #pragma unroll
-      for (int j = 0; j < NW / 2; ++j) {
+      for (int j = 0; j < NQ; ++j) {
         need[j] = h_ok;
-        v2[j] = 0ull;
-        if (need[j])
-          v2[j] = __hip_atomic_load(
-              const_cast<unsigned long long*>(byte_at(reinterpret_cast<const unsigned long long*>(src), 4u * (128u * j + 2u * lane))),
-              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        q4[j] = need[j] ? quad_load(src, 256u * j + 4u * lane) : u4v{0u, 0u, 0u, 0u};
       }
       const long long t0 = wall_clock64();
       while (true) {
         bool ok = true;
 #pragma unroll
-        for (int j = 0; j < NW / 2; ++j) {
-          need[j] = need[j] && ((unsigned)v2[j] == kEmpty || (unsigned)(v2[j] >> 32) == kEmpty);
+        for (int j = 0; j < NQ; ++j) {
+          need[j] = need[j] && max(max(q4[j][0], q4[j][1]), max(q4[j][2], q4[j][3])) == kEmpty;
           ok = ok && !need[j];
         }
         if (__all(ok)) break;
@@ -277,18 +276,15 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
           return;
         }
 #pragma unroll
-        for (int j = 0; j < NW / 2; ++j)
-          if (need[j])
-            v2[j] = __hip_atomic_load(
-                const_cast<unsigned long long*>(byte_at(reinterpret_cast<const unsigned long long*>(src), 4u * (128u * j + 2u * lane))),
-                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int j = 0; j < NQ; ++j)
+          if (need[j]) q4[j] = quad_load(src, 256u * j + 4u * lane);
       }
 #pragma unroll
-      for (int j = 0; j < NW / 2; ++j) {
-        hreg[2 * j] = h_ok ? __uint_as_float((unsigned)v2[j]) : 0.f;
-        hreg[2 * j + 1] = h_ok ? __uint_as_float((unsigned)(v2[j] >> 32)) : 0.f;
-        asm volatile("" : "+v"(hreg[2 * j]), "+v"(hreg[2 * j + 1]));
-      }
+      for (int j = 0; j < NQ; ++j)
+        hsb[(NQ * w + j) * 64 + lane] =
+            h_ok ? f4{__uint_as_float(q4[j][0]), __uint_as_float(q4[j][1]), __uint_as_float(q4[j][2]),
+                      __uint_as_float(q4[j][3])}
+                 : f4{0.f, 0.f, 0.f, 0.f};
     }
     // this step's input projection for the cell lanes (used after the products)
     if (c_ok) {
@@ -296,42 +292,48 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
 #pragma unroll
       for (int gt = 0; gt < 4; ++gt) gin[gt] = __builtin_nontemporal_load(g + (size_t)gt * H);
     }
-
-    // ---- 2. products, the four waves' partials summed through LDS ------------------
-    f16v acc[S::RT];
-#pragma unroll
-    for (int rt = 0; rt < S::RT; ++rt) acc[rt] = f16v{};
-#pragma unroll
-    for (int i = 0; i < S::KS; ++i) wide_kstep<S::RT>(acc, wreg[i], hreg[i]);
-    wide_kstep_drain<S::RT>(acc);
-    // D layout: lane l, register 4 q + g -> gate row 8 q + 4 (l/32) + g of the tile, batch l%32;
-    // with unit-interleaved rows that is gate g of unit offset 8 rt + 2 q + l/32
-#pragma unroll
-    for (int rt = 0; rt < S::RT; ++rt)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        red[(w * U + 8 * rt + 2 * q + hb) * 32 + l32] =
-            f4{acc[rt][4 * q], acc[rt][4 * q + 1], acc[rt][4 * q + 2], acc[rt][4 * q + 3]};
-    lds_barrier();
+    lds_barrier();  // the four blocks are in LDS; the other buffer is free (step t-1's products are done)
     if (abort_flag) return;
 
-    // ---- 3. the workgroup's partial of slice j -> workgroup (x, r, j) ---------------
-    if (cell) {
-      float* const ib = p.inbox + (size_t)(t % kWidePSlots) * inbox_slot;
-#pragma unroll 2
-      for (int j = 0; j < kWideKBlocks; ++j) {
-        const int uo = S::SU * j + su;
-        const f4 s = ((red[(0 * U + uo) * 32 + cb] + red[(1 * U + uo) * 32 + cb]) +
-                      red[(2 * U + uo) * 32 + cb]) + red[(3 * U + uo) * 32 + cb];
-        const int dst = x + kWideXcds * (r * kWideKBlocks + j);
-        if (cb < B) quad_put<FAST>(ib + (size_t)dst * S::IW, pofs, s);
+    // ---- 2. products over the workgroup's k block; the accumulators are the partial
+    //         of the wave's 16 units, sent to the two slices' cell workgroups -----------
+    f16v acc[4] = {f16v{}, f16v{}, f16v{}, f16v{}};
+    {
+      // the operands of group i4 + 1 are read from LDS while group i4 multiplies (volatile
+      // reads stay in program order with the asm, so only two groups' operands are live)
+      typedef __attribute__((address_space(3))) const volatile f4 lds_vf4;
+      lds_vf4* const hv = (lds_vf4*)(hsb);
+      f4 hcur = hv[lane];
+#pragma unroll
+      for (int i4 = 0; i4 < S::KS / 4; ++i4) {
+        const f4 hnext = i4 + 1 < S::KS / 4 ? hv[(i4 + 1) * 64 + lane] : hcur;
+        wide_ksteps4(acc, wreg[i4], hcur);
+        hcur = hnext;
       }
     }
-    lds_barrier();  // red is read; the next step may overwrite it
+    wide_ksteps_drain(acc);
+    {
+      // D layout: lane l, register 4 q + g -> gate row 8 q + 4 (l/32) + g of tile rt, batch
+      // l%32; with unit-interleaved rows that is gate g of unit U w / 4 + 8 rt + 2 q + l/32,
+      // i.e. unit 2 q + l/32 of slice 2 w + rt
+      float* const ib = p.inbox + (size_t)(t % kWidePSlots) * inbox_slot;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int dst = x + kWideXcds * (r * kWideKBlocks + 2 * w + rt);
+        const __amdgpu_buffer_rsrc_t d = wide_rsrc(ib + (size_t)dst * S::IW + (size_t)kb * S::PW, S::PW);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f4 v = f4{acc[rt][4 * q] + acc[rt + 2][4 * q], acc[rt][4 * q + 1] + acc[rt + 2][4 * q + 1],
+                          acc[rt][4 * q + 2] + acc[rt + 2][4 * q + 2], acc[rt][4 * q + 3] + acc[rt + 2][4 * q + 3]};
+          if (h_ok) quad_put<FAST>(d, 4u * ((2 * q + hb) * 32 + l32), v);
+        }
+      }
+    }
 
-    // ---- 4. the cell of slice kb: sum the 8 sources, activate, publish h_t ---------
+    // ---- 3. the cell of slice kb: sum the 8 sources, activate, publish h_t ---------
     if (cell) {
-      float* const ib = p.inbox + (size_t)(t % kWidePSlots) * inbox_slot + (size_t)me * S::IW;
+      const __amdgpu_buffer_rsrc_t ib =
+          wide_rsrc(p.inbox + (size_t)(t % kWidePSlots) * inbox_slot + (size_t)me * S::IW, S::IW);
       unsigned offs[kWideKBlocks];
 #pragma unroll
       for (int sidx = 0; sidx < kWideKBlocks; ++sidx) offs[sidx] = (unsigned)sidx * S::PW + 4u * (su * 32 + cb);
@@ -339,7 +341,7 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
       if (!quads_wait<kWideKBlocks>(ib, offs, c_ok, v, p.spin, &abort_flag, p.err)) return;
       if (c_ok) {
 #pragma unroll
-        for (int sidx = 0; sidx < kWideKBlocks; ++sidx) quad_clear<FAST>(ib, offs[sidx]);
+        for (int sidx = 0; sidx < kWideKBlocks; ++sidx) quad_store<FAST>(ib, offs[sidx], u4v{kEmpty, kEmpty, kEmpty, kEmpty});
         f4 z = v[0];
 #pragma unroll
         for (int sidx = 1; sidx < kWideKBlocks; ++sidx) z = z + v[sidx];
@@ -350,15 +352,23 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
         const float tc = tanh_f(c);
         const float h = act[3] * tc;
         c_reg = c;
-        word_put<false>(hown + (size_t)(t % kWideHSlots) * hslot, hpos, canon_nan(h));
+        hst[4 * (cb + 32 * (su & 1)) + (su >> 1)] = canon_nan(h);  // word 4 l + e of the group
         const size_t e = (size_t)cb * H + unit;
         __builtin_nontemporal_store(h, p.h_save + (size_t)(t + 1) * plane + e);
         __builtin_nontemporal_store(c, p.c_save + (size_t)(t + 1) * plane + e);
         __builtin_nontemporal_store(tc, p.tanh_c + (size_t)t * plane + e);
         __builtin_nontemporal_store(f4{act[0], act[1], act[2], act[3]},
                                     reinterpret_cast<f4*>(p.gact + ((size_t)t * plane + e) * 4));
-        word_put<false>(hown + (size_t)((t + 2) % kWideHSlots) * hslot, hpos, __uint_as_float(kEmpty));
       }
+    }
+    lds_barrier();  // the workgroup's h values are gathered
+    if (w == 0) {   // publish the 1 KB group, then clear it in the slot of two steps ago
+      const f4 hq = *reinterpret_cast<const f4*>(&hst[4 * lane]);
+      const __amdgpu_buffer_rsrc_t hp = wide_rsrc(hown + (size_t)(t % kWideHSlots) * hslot, 256);
+      quad_store<false>(hp, 4u * lane, u4v{__float_as_uint(hq[0]), __float_as_uint(hq[1]), __float_as_uint(hq[2]),
+                                           __float_as_uint(hq[3])});
+      const __amdgpu_buffer_rsrc_t hc = wide_rsrc(hown + (size_t)((t + 2) % kWideHSlots) * hslot, 256);
+      quad_store<false>(hc, 4u * lane, u4v{kEmpty, kEmpty, kEmpty, kEmpty});
     }
   }
 }
@@ -385,7 +395,7 @@ __device__ void poison_wide_fwd(const WFwdArgs& p, int x, int r, int kb) {
 
 template <int U>
 __global__ __launch_bounds__(256, 1) void rec_fwd_wide(WFwdArgs p) {
-  extern __shared__ f4 wide_red[];  // [4 waves][U units][32 batch] (keeps one workgroup per CU)
+  extern __shared__ f4 wide_hs[];  // the h blocks of two steps (sized to keep one workgroup per CU)
   __shared__ int abort_flag;
   const int x = blockIdx.x % kWideXcds, loc = blockIdx.x / kWideXcds;
   const int r = loc / kWideKBlocks, kb = loc % kWideKBlocks;
@@ -395,9 +405,9 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_wide(WFwdArgs p) {
                     !p.device_scope;
   if (!abort_flag) {
     if (fast)
-      rec_fwd_wide_body<U, true>(p, x, r, kb, wide_red, abort_flag);
+      rec_fwd_wide_body<U, true>(p, x, r, kb, wide_hs, abort_flag);
     else
-      rec_fwd_wide_body<U, false>(p, x, r, kb, wide_red, abort_flag);
+      rec_fwd_wide_body<U, false>(p, x, r, kb, wide_hs, abort_flag);
   }
   lds_barrier();
   if (abort_flag) poison_wide_fwd<U>(p, x, r, kb);

@@ -1651,7 +1651,9 @@ struct WidePlan {
   bool ok = false;
 };
 
-constexpr size_t kWideLdsBytes = WideShape<64>::RED_BYTES;  // 128 KB: one workgroup per CU
+// the double-buffered h blocks (64 KB), padded so that one workgroup fits per CU
+constexpr size_t kWideLdsBytes =
+    WideShape<64>::LDS_BYTES > (size_t)kPadLdsBytes ? WideShape<64>::LDS_BYTES : (size_t)kPadLdsBytes;
 
 int plan_wide(int B, int H, WidePlan* pl) {
   *pl = WidePlan{};

@@ -81,8 +81,8 @@ int hsl_set_exchange_scope(int mode);
 int hsl_set_split_products(int on);
 /* Which path the last hsl_rec_fwd / hsl_rec_bwd in this process (on any host
  * thread; autograd runs the backward on its own thread) used: 1 = per-step,
- * 2 = persistent, 3 = the persistent forward with W_hh held in the registers of
- * 256 workgroups (H = 2048, B <= 32; its backward is per-step). */
+ * 2 = persistent, 3 = the persistent kernels that hold W_hh in the registers of
+ * 256 workgroups (H = 2048, B <= 32). */
 int hsl_last_recurrent_path(void);
 /* Whether the last hsl_rec_bwd (in this process, on any thread) accumulated the
  * weight gradients inside the persistent kernel: 0 = no (separate GEMMs), 1 = dW_hh,

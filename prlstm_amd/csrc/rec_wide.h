@@ -412,3 +412,277 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_wide(WFwdArgs p) {
   lds_barrier();
   if (abort_flag) poison_wide_fwd<U>(p, x, r, kb);
 }
+
+// ---------------------------------------------------------------------------------
+// Persistent recurrent backward for H = 2048, B <= 32: the mirror of the wide
+// forward (_torch.py:133-150: dh_t = dout_t + dg_{t+1} W_s, then the cell backward).
+// Workgroup (x, c), blockIdx = x + 8 c, sits on XCD x and holds W_hh's 1024 gate rows of
+// units [256 x, +256) (unit-interleaved) for the output columns (units) [64 c, +64); wave w
+// takes rows [256 w, +256) (units [256 x + 64 w, +64)), 2 column tiles x 128 k-steps in the
+// accumulator registers.  The rows of XCD x are the gate rows of the units whose cells run
+// on XCD x, so the broadcast of a dg (4H values per batch row, four times h) stays inside
+// the XCD; the partial sums of dh (H per batch row) cross XCDs instead.  Per iteration:
+//   1. products: wave w reads a dg_{t+1} of its 256 rows from the XCD's broadcast buffer,
+//      8 groups at a time (the next 8 are requested before the current ones multiply);
+//   2. the four waves' partials [64 columns x 32 batch] are summed in LDS and sent to the
+//      reducing workgroups of the columns' XCD (c / 4): slice sl of 8 units goes to
+//      workgroup (c / 4, 8 (c % 4) + sl), whose inbox holds the 8 row XCDs' partials;
+//   3. reducer lane (unit su of slice s, batch b) sums them in XCD order, adds dout_t (and
+//      dh_n at t = T-1), runs the cell backward with the dc carry in a register, stores
+//      dgates_t and publishes a_g dg_t (the a-scaling of W_s moved to the operand) to the
+//      XCD's broadcast buffer: its 8 units x 4 gates x 32 batch are one contiguous 4 KB
+//      group, gathered in LDS and written in full cache lines.
+// One more product after t = 0 gives dh0.  Slots as in the forward: broadcast of iteration
+// k in slot k%4, its owner clears slot (k+2)%4 after publishing; partials of iteration k in
+// slot k%3, cleared by their one reader.
+constexpr int kWideBRows = 1024;             // gate rows held per XCD
+constexpr int kWideBInbox = 8 * 32 * 8;      // inbox words of a reducer per slot: [src x][batch][unit]
+constexpr int kWideBLdsBytes = 4 * 2048 * 4 + 1024 * 4;  // wave partials + the gathered dg group
+
+struct WBwdArgs {
+  const float* dout;    // [T][B][H]
+  const float* dh_n;    // [B][H] or null
+  const float* dc_n;    // [B][H] or null
+  const float* c_save;  // [T+1][B][H]
+  const float* gact;    // [T][B][H][4]
+  const float* tanh_c;  // [T][B][H]
+  const float* w_hh;
+  const float* a;
+  float* dgates;        // [T][B][4H]
+  float* dh0;           // [B][H] or null
+  float* dc0;           // [B][H] or null
+  float* dgbuf;         // [4 slots][8 XCDs][1024 rows x 32 batch]
+  float* inbox;         // [3 slots][256 workgroups][kWideBInbox]
+  unsigned long long* hello;  // [8][32]
+  int* err;
+  int T, B, H;
+  int device_scope;
+  long long spin;
+};
+
+// word of (local row rho, batch b) in an XCD's broadcast buffer: wave w = rho / 256 reads
+// group j (k-steps 4j .. 4j+3 of its rows) at 8192 w + 256 j + 4 l
+__device__ __forceinline__ unsigned wideb_pos(int rho, int b) {
+  const int w = rho >> 8, rl = rho & 255, i = rl >> 1, l = b + 32 * (rl & 1);
+  return 8192u * w + 256u * (i >> 2) + 4u * l + (i & 3);
+}
+
+template <bool FAST>
+__device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int c, float* red, float* gst,
+                                                  int& abort_flag) {
+  const int T = p.T, B = p.B, H = p.H;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hb = lane >> 5, l32 = lane & 31;
+  const int ubase = 256 * x;  // first unit of the XCD's rows
+
+  // W_hh^T block of this wave: column tile ct, k-step 4 i4 + e -> column m = l%32 of the
+  // tile (unit 64 c + 32 ct + m), row rho = 256 w + 2 (4 i4 + e) + l/32 (unit ubase + rho/4,
+  // gate rho % 4); unscaled, a multiplies the dg operand instead
+  float wreg[32][4][2];
+#pragma unroll
+  for (int i8 = 0; i8 < 32; i8 += 4) {
+#pragma unroll
+    for (int i4 = i8; i4 < i8 + 4; ++i4)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int rho = 256 * w + 2 * (4 * i4 + e) + hb;
+        const float* row = p.w_hh + ((size_t)(rho & 3) * H + ubase + (rho >> 2)) * H + 64 * c + l32;
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) wreg[i4][e][ct] = row[32 * ct];
+      }
+#pragma unroll
+    for (int i4 = i8; i4 < i8 + 4; ++i4)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) asm volatile("" : "+a"(wreg[i4][e][ct]));  // held in the accumulator file
+  }
+
+  // reducer lane: unit su of this workgroup's slice (slice s = c of XCD x: units ubase + 8 c
+  // + su), batch cb
+  const int su = tid >> 5, cb = tid & 31;
+  const bool c_ok = cb < B;
+  const int unit = ubase + 8 * c + su;
+  float ag[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) ag[g] = p.a[g];
+  float dc = 0.f;
+  if (c_ok && p.dc_n) dc = p.dc_n[(size_t)cb * H + unit];
+  const size_t plane = (size_t)B * H, plane4 = 4 * plane;
+  const bool h_ok = l32 < B;
+  // broadcast buffer of this XCD; this workgroup's 4 KB group in it
+  const size_t bslot = (size_t)kWideXcds * kWideBRows * 32;
+  float* const bx = p.dgbuf + (size_t)x * kWideBRows * 32;
+  // send: lane (c4 = tid / 32, batch sb = tid % 32) sends columns 8 c4 .. 8 c4 + 7 (slice c4)
+  // to reducer (c / 4, 8 (c % 4) + c4), inbox [src x][sb][8 units]
+  const int c4 = tid >> 5, sb = tid & 31;
+  const int dst = (c >> 2) + kWideXcds * (8 * (c & 3) + c4);
+  const size_t islot = (size_t)kWideWgs * kWideBInbox;
+  for (int k = 0; k <= T; ++k) {
+    const int t = T - 1 - k;  // the cell's step (-1 after the last product: dh0)
+    float dsum = 0.f;
+    if (k > 0) {
+      // ---- 1. products with a_g dg_{t+1} of the wave's rows ---------------------------
+      const __amdgpu_buffer_rsrc_t src =
+          wide_rsrc(bx + (size_t)((k - 1) % kWideHSlots) * bslot + 8192u * w, 8192);
+      f16v acc[4] = {f16v{}, f16v{}, f16v{}, f16v{}};
+      u4v qa[8], qb[8];
+      auto issue = [&](u4v (&q)[8], int jb) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = h_ok ? quad_load(src, 256u * (jb + j) + 4u * lane) : u4v{0u, 0u, 0u, 0u};
+      };
+      // waits for groups jb .. jb+7 (all eight reloaded while any word is kEmpty: the loop
+      // then keeps no state beyond the values)
+      auto settle = [&](u4v (&q)[8], int jb) -> bool {
+        const long long t0 = wall_clock64();
+        while (true) {
+          unsigned m = 0u;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) m = max(m, max(max(q[j][0], q[j][1]), max(q[j][2], q[j][3])));
+          if (__all(m != kEmpty)) return true;
+          if (wall_clock64() - t0 > p.spin) {
+            raise_abort(&abort_flag, p.err);
+            return false;
+          }
+          issue(q, jb);
+        }
+      };
+      auto mult = [&](const u4v (&q)[8], int jb) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          wide_ksteps4(acc, wreg[jb + j],
+                       f4{__uint_as_float(q[j][0]), __uint_as_float(q[j][1]), __uint_as_float(q[j][2]),
+                          __uint_as_float(q[j][3])});
+      };
+      issue(qa, 0);
+      if (!settle(qa, 0)) return;
+      issue(qb, 8);
+      mult(qa, 0);
+      if (!settle(qb, 8)) return;
+      issue(qa, 16);
+      mult(qb, 8);
+      if (!settle(qa, 16)) return;
+      issue(qb, 24);
+      mult(qa, 16);
+      if (!settle(qb, 24)) return;
+      mult(qb, 24);
+      wide_ksteps_drain(acc);
+      // ---- 2. the four waves' partials summed in LDS, sent to the reducers ------------
+      // D layout: lane l, register 4 q + e -> column 8 q + 4 (l/32) + e of tile ct, batch l%32
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<f4*>(&red[((w * 16 + 8 * ct + 2 * q + hb) * 32 + l32) * 4]) =
+              f4{acc[ct][4 * q] + acc[ct + 2][4 * q], acc[ct][4 * q + 1] + acc[ct + 2][4 * q + 1],
+                 acc[ct][4 * q + 2] + acc[ct + 2][4 * q + 2], acc[ct][4 * q + 3] + acc[ct + 2][4 * q + 3]};
+      lds_barrier();
+      if (abort_flag) return;
+      if (sb < B) {
+        f4 s0 = f4{0.f, 0.f, 0.f, 0.f}, s1 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+          s0 = s0 + *reinterpret_cast<const f4*>(&red[((ww * 16 + 2 * c4) * 32 + sb) * 4]);
+          s1 = s1 + *reinterpret_cast<const f4*>(&red[((ww * 16 + 2 * c4 + 1) * 32 + sb) * 4]);
+        }
+        const __amdgpu_buffer_rsrc_t d =
+            wide_rsrc(p.inbox + (size_t)((k - 1) % kWidePSlots) * islot + (size_t)dst * kWideBInbox, kWideBInbox);
+        quad_put<false>(d, (unsigned)(x * 256 + sb * 8), s0);
+        quad_put<false>(d, (unsigned)(x * 256 + sb * 8 + 4), s1);
+      }
+      // ---- 3a. the reducer's sum of the 8 row XCDs' partials --------------------------
+      if (c_ok) {
+        const __amdgpu_buffer_rsrc_t ib =
+            wide_rsrc(p.inbox + (size_t)((k - 1) % kWidePSlots) * islot + (size_t)blockIdx.x * kWideBInbox,
+                      kWideBInbox);
+        unsigned v[8];
+        const long long t0 = wall_clock64();
+        while (true) {
+          unsigned m = 0u;
+#pragma unroll
+          for (int sx = 0; sx < 8; ++sx) {
+            v[sx] = __builtin_amdgcn_raw_buffer_load_b32(ib, (int)(4u * (sx * 256 + cb * 8 + su)), 0, kCpolSc1);
+            m = max(m, v[sx]);
+          }
+          if (__all(m != kEmpty)) break;
+          if (wall_clock64() - t0 > p.spin) {
+            raise_abort(&abort_flag, p.err);
+            return;
+          }
+        }
+#pragma unroll
+        for (int sx = 0; sx < 8; ++sx)
+          __builtin_amdgcn_raw_buffer_store_b32(kEmpty, ib, (int)(4u * (sx * 256 + cb * 8 + su)), 0, kCpolSc1);
+        dsum = __uint_as_float(v[0]);
+#pragma unroll
+        for (int sx = 1; sx < 8; ++sx) dsum += __uint_as_float(v[sx]);
+      }
+    }
+    if (k == T) {  // dh of h0, and the carry into c0
+      if (c_ok) {
+        if (p.dh0) p.dh0[(size_t)cb * H + unit] = dsum;
+        if (p.dc0) p.dc0[(size_t)cb * H + unit] = dc;
+      }
+      break;
+    }
+    // ---- 3b. cell backward of step t, dgates_t, the broadcast of a_g dg_t ---------------
+    float d[4] = {0.f, 0.f, 0.f, 0.f};
+    if (c_ok) {
+      const size_t e = (size_t)cb * H + unit;
+      float dh = (k > 0 ? dsum : (p.dh_n ? p.dh_n[e] : 0.f)) + p.dout[(size_t)t * plane + e];
+      const f4 ga = *reinterpret_cast<const f4*>(p.gact + ((size_t)t * plane + e) * 4);
+      cell_bwd(dh, dc, p.c_save[(size_t)t * plane + e], ga[0], ga[1], ga[2], ga[3], p.tanh_c[(size_t)t * plane + e], d);
+      float* const dg = p.dgates + (size_t)t * plane4 + (size_t)cb * 4 * H + unit;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) __builtin_nontemporal_store(d[g], dg + (size_t)g * H);
+    }
+    // gather: rows 4 (8 c + su) + g of this XCD are word 1024 c + (wideb_pos - 1024 c) of the
+    // buffer; absent batch rows publish 0
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      gst[wideb_pos(4 * (8 * c + su) + g, cb) - 1024u * c] = c_ok ? canon_nan(ag[g] * d[g]) : 0.f;
+    lds_barrier();
+    if (abort_flag) return;
+    {
+      const f4 qv = *reinterpret_cast<const f4*>(&gst[4 * tid]);
+      const __amdgpu_buffer_rsrc_t bp = wide_rsrc(bx + (size_t)(k % kWideHSlots) * bslot + 1024u * c, 1024);
+      quad_store<FAST>(bp, 4u * tid, u4v{__float_as_uint(qv[0]), __float_as_uint(qv[1]), __float_as_uint(qv[2]),
+                                         __float_as_uint(qv[3])});
+      const __amdgpu_buffer_rsrc_t bc = wide_rsrc(bx + (size_t)((k + 2) % kWideHSlots) * bslot + 1024u * c, 1024);
+      quad_store<FAST>(bc, 4u * tid, u4v{kEmpty, kEmpty, kEmpty, kEmpty});
+    }
+  }
+}
+
+// After an abort the reducer lanes set what they own to NaN: dgates of their unit and batch
+// row at every step, and dh0 / dc0.
+__device__ void poison_wide_bwd(const WBwdArgs& p, int x, int c) {
+  const int tid = threadIdx.x, su = tid >> 5, cb = tid & 31;
+  if (cb >= p.B) return;
+  const int unit = 256 * x + 8 * c + su, H = p.H;
+  const float nan = __uint_as_float(0x7FC00000u);
+  const size_t e = (size_t)cb * H + unit;
+  if (p.dh0) p.dh0[e] = nan;
+  if (p.dc0) p.dc0[e] = nan;
+  for (int t = 0; t < p.T; ++t)
+    for (int g = 0; g < 4; ++g) p.dgates[((size_t)t * p.B + cb) * 4 * H + g * H + unit] = nan;
+}
+
+__global__ __launch_bounds__(256, 1) void rec_bwd_wide(WBwdArgs p) {
+  extern __shared__ float wide_lds[];  // wave partials, then the gathered dg group (padded: one workgroup per CU)
+  __shared__ int abort_flag;
+  const int x = blockIdx.x % kWideXcds, c = blockIdx.x / kWideXcds;
+  if (threadIdx.x == 0) abort_flag = 0;
+  const bool fast = agree_placement(p.hello + (size_t)x * (kWideRowSubs * kWideKBlocks), c,
+                                    kWideRowSubs * kWideKBlocks, p.spin, &abort_flag, p.err) &&
+                    !p.device_scope;
+  if (!abort_flag) {
+    if (fast)
+      rec_bwd_wide_body<true>(p, x, c, wide_lds, wide_lds + 4 * 2048, abort_flag);
+    else
+      rec_bwd_wide_body<false>(p, x, c, wide_lds, wide_lds + 4 * 2048, abort_flag);
+  }
+  lds_barrier();
+  if (abort_flag) poison_wide_bwd(p, x, c);
+}

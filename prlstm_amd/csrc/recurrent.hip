@@ -1655,14 +1655,20 @@ struct WidePlan {
 constexpr size_t kWideLdsBytes =
     WideShape<64>::LDS_BYTES > (size_t)kPadLdsBytes ? WideShape<64>::LDS_BYTES : (size_t)kPadLdsBytes;
 
-int plan_wide(int B, int H, WidePlan* pl) {
+constexpr size_t kWideBwdLdsBytes =
+    (size_t)kWideBLdsBytes > (size_t)kPadLdsBytes ? (size_t)kWideBLdsBytes : (size_t)kPadLdsBytes;
+
+int plan_wide(int B, int H, bool bwd, WidePlan* pl) {
   *pl = WidePlan{};
   if (recurrent_path_mode() == 1 || B < 1 || B > 32 || H != 2048) return HSL_OK;
   DeviceInfo di;
   HSL_CHECK(device_info(&di));
   if (di.num_xcds != kWideXcds || di.num_cus < kWideWgs) return HSL_OK;
   int occ = 0;
-  HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, rec_fwd_wide<64>, 256, kWideLdsBytes));
+  if (bwd)
+    HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, rec_bwd_wide, 256, kWideBwdLdsBytes));
+  else
+    HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, rec_fwd_wide<64>, 256, kWideLdsBytes));
   pl->ok = occ >= 1 && (long)occ * di.num_cus >= kWideWgs;
   return HSL_OK;
 }
@@ -1802,6 +1808,9 @@ struct BwdWs {
   float* gemm;               // shared by the weight-gradient GEMMs
   size_t gemm_bytes;
   float* dgates;             // [T*B*4H] (when they feed a product)
+  float* wbuf;               // dg broadcast slots, then partial inboxes (wide persistent)
+  size_t wfloats;
+  unsigned long long* whello; // [256] (wide persistent)
 };
 
 size_t gemm_region_bytes(int T, int B, int D, int H) {
@@ -1828,13 +1837,14 @@ size_t gemm_region_bytes(int T, int B, int D, int H) {
 // dW_ih when the persistent kernel does not accumulate it).  All when the path is not
 // known (no device).
 struct BwdNeeds {
-  bool xch = true, step = true, dgates = true;
+  bool xch = true, step = true, dgates = true, wide = true;
 };
 
-BwdNeeds bwd_needs(const PersistentPlan& pl, bool with_dx) {
+BwdNeeds bwd_needs(const PersistentPlan& pl, const WidePlan& wp, bool with_dx) {
   BwdNeeds nd;
   nd.xch = pl.ok;
-  nd.step = !pl.ok;
+  nd.wide = !pl.ok && wp.ok;
+  nd.step = !pl.ok && !wp.ok;
   nd.dgates = !(pl.ok && pl.XT > 0) || with_dx;
   return nd;
 }
@@ -1861,6 +1871,11 @@ size_t carve_bwd(void* ws, size_t cap, int T, int B, int D, int H, BwdNeeds nd, 
     o->pfloats = 3 * ng * nwmax * 4 * 64 * per;
     o->pbuf = c.take<float>(o->pfloats);
     o->hello = c.take<unsigned long long>(o->hwords);
+  }
+  if (nd.wide && H == 2048) {
+    o->wfloats = (size_t)kWideHSlots * kWideXcds * kWideBRows * 32 + (size_t)kWidePSlots * kWideWgs * kWideBInbox;
+    o->wbuf = c.take<float>(o->wfloats);
+    o->whello = c.take<unsigned long long>(kWideWgs);
   }
   o->gemm_bytes = gemm_region_bytes(T, B, D, H);
   o->gemm = c.take<float>(o->gemm_bytes / sizeof(float) + 1);
@@ -1965,7 +1980,7 @@ size_t hsl_rec_fwd_ws_bytes(int T, int B, int D, int H) {
   FwdNeeds nd;  // every part when the path cannot be planned (no device)
   PersistentPlan pl;
   WidePlan wp;
-  if (B > 0 && H > 0 && plan_persistent(B, H, D, false, &pl) == HSL_OK && plan_wide(B, H, &wp) == HSL_OK)
+  if (B > 0 && H > 0 && plan_persistent(B, H, D, false, &pl) == HSL_OK && plan_wide(B, H, false, &wp) == HSL_OK)
     nd = fwd_needs(pl, wp, true);
   return carve_fwd(nullptr, 0, T, B, H, nd, &w);
 }
@@ -1981,7 +1996,7 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
   PersistentPlan pl;
   HSL_CHECK(plan_persistent(B, H, D, false, &pl));
   WidePlan wp;
-  if (!pl.ok) HSL_CHECK(plan_wide(B, H, &wp));
+  if (!pl.ok) HSL_CHECK(plan_wide(B, H, false, &wp));
   if (recurrent_path_mode() == 2 && !pl.ok && !wp.ok)
     return fail(HSL_ERR_UNSUPPORTED, "persistent path does not fit (B=%d H=%d)", B, H);
   const bool x_aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0;
@@ -2085,7 +2100,7 @@ int hsl_rec_fwd_noalloc(const float* x, const float* h0, const float* c0, const 
   PersistentPlan pl;
   HSL_CHECK(plan_persistent(B, H, D, false, &pl));
   WidePlan wp;
-  if (!pl.ok) HSL_CHECK(plan_wide(B, H, &wp));
+  if (!pl.ok) HSL_CHECK(plan_wide(B, H, false, &wp));
   const bool x_aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0;
   if (pl.XP && !x_aligned) pl.XP = false;
   FwdWs w;
@@ -2109,7 +2124,9 @@ size_t hsl_rec_bwd_ws_bytes_for(int T, int B, int D, int H, int with_dx) {
   BwdWs w;
   BwdNeeds nd;  // every part when the path cannot be planned (no device)
   PersistentPlan pl;
-  if (B > 0 && H > 0 && plan_persistent(B, H, D, true, &pl) == HSL_OK) nd = bwd_needs(pl, with_dx != 0);
+  WidePlan wp;
+  if (B > 0 && H > 0 && plan_persistent(B, H, D, true, &pl) == HSL_OK && plan_wide(B, H, true, &wp) == HSL_OK)
+    nd = bwd_needs(pl, wp, with_dx != 0);
   return carve_bwd(nullptr, 0, T, B, D, H, nd, &w);
 }
 
@@ -2127,11 +2144,13 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
   if (T > 0 && B > 0 && H > 0 && (!dout || !x || !h_save || !c_save || !gact || !tanh_c))
     return fail(HSL_ERR_ARG, "hsl_rec_bwd: null pointer");
   PersistentPlan pl;
+  WidePlan wp;
   if (T > 0 && B > 0 && H > 0) HSL_CHECK(plan_persistent(B, H, D, true, &pl));
-  if (T > 0 && B > 0 && H > 0 && recurrent_path_mode() == 2 && !pl.ok)
+  if (T > 0 && B > 0 && H > 0 && !pl.ok) HSL_CHECK(plan_wide(B, H, true, &wp));
+  if (T > 0 && B > 0 && H > 0 && recurrent_path_mode() == 2 && !pl.ok && !wp.ok)
     return fail(HSL_ERR_UNSUPPORTED, "persistent path does not fit (B=%d H=%d)", B, H);
   BwdWs w;
-  const size_t need = carve_bwd(ws, ws_bytes, T, B, D, H, bwd_needs(pl, dx != nullptr), &w);
+  const size_t need = carve_bwd(ws, ws_bytes, T, B, D, H, bwd_needs(pl, wp, dx != nullptr), &w);
   if (!ws || ws_bytes < need) return fail(HSL_ERR_ARG, "hsl_rec_bwd: workspace %zu bytes, need %zu", ws_bytes, need);
   const int TB = T * B;
   const size_t plane = (size_t)B * H, plane4 = (size_t)B * 4 * H;
@@ -2162,6 +2181,8 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
   }
   if (pl.ok)
     HSL_CHECK(prepare_persistent(w.err, w.pbuf, w.pfloats, w.hello, w.hwords, s));
+  else if (wp.ok)
+    HSL_CHECK(prepare_persistent(w.err, w.wbuf, w.wfloats, w.whello, kWideWgs, s));
   else
     HSL_CHECK(zero_words(reinterpret_cast<unsigned long long*>(w.err), 32, s));
   if (pl.ok) {
@@ -2181,6 +2202,19 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     timing_end(slot, s);
     note_recurrent_path(2);
     note_backward_fused(fused_ih ? 2 : fused ? 1 : 0);
+  } else if (wp.ok) {
+    note_backward_fused(0);
+    WBwdArgs wa{dout, dh_n, dc_n, c_save, gact, tanh_c, w_hh, a, w.dgates, dh0, dc0, w.wbuf,
+                w.wbuf + (size_t)kWideHSlots * kWideXcds * kWideBRows * 32, w.whello, w.err, T, B, H,
+                exchange_scope_mode(), spin_timeout_ticks()};
+    const int slot = timing_begin(kTimeRecBwd, s);
+    hipLaunchKernelGGL(rec_bwd_wide, dim3(kWideWgs), dim3(256), kWideBwdLdsBytes, s, wa);
+    HSL_HIP(hipGetLastError());
+    timing_end(slot, s);
+    hipLaunchKernelGGL(colsum_time_kernel, dim3(grid_for(plane4)), dim3(256), 0, s, w.dgates, w.db_part, T,
+                       (int)plane4);
+    HSL_HIP(hipGetLastError());
+    note_recurrent_path(3);
   } else {
     note_backward_fused(0);
     hipLaunchKernelGGL(scale_whh_kernel, dim3(grid_for((size_t)4 * H * H)), dim3(256), 0, s, w_hh, b_hh, a, w.w_s,

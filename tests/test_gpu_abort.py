@@ -100,16 +100,17 @@ def test_timed_out_waits_in_graph_replay(dev, tiny_spin):
     assert _finite(out) and all(_finite(p.grad) for p in m.parameters())
 
 
-def test_timed_out_waits_wide_forward(dev, tiny_spin):
-    """The W_hh-resident forward for H = 2048 (rec_fwd_wide) bounds its waits the same way:
-    an aborting workgroup fills its cells' outputs with NaN and raises the device word."""
+def test_timed_out_waits_wide_kernels(dev, tiny_spin):
+    """The W_hh-resident kernels for H = 2048 (rec_fwd_wide, rec_bwd_wide) bound their waits
+    the same way: an aborting workgroup fills what it owns with NaN and raises the device
+    word.  The forward is checked alone, then forward + backward."""
     T, B, D, H = 4, 8, 32, 2048
     torch.manual_seed(0)
     m = prlstm_amd.HeadStartLSTM(D, H).to(dev)
     x = torch.randn(T, B, D, device=dev)
     aborted = 0
     for attempt in range(3):
-        print(f"wide abort attempt {attempt}", flush=True)
+        print(f"wide forward abort attempt {attempt}", flush=True)
         with torch.no_grad():
             out, (h_n, c_n) = m(x)
         torch.cuda.synchronize()
@@ -119,9 +120,17 @@ def test_timed_out_waits_wide_forward(dev, tiny_spin):
         assert bool(flags) != finite, (attempt, flags, finite)
         aborted += bool(flags)
     assert aborted >= 1, "a 1 us spin limit never made the wide forward give up a wait"
+    aborted = 0
+    for attempt in range(3):
+        print(f"wide step abort attempt {attempt}", flush=True)
+        out, grads = _step(m, x)
+        assert _lib.last_recurrent_path() == 3
+        flags = _lib.device_errors(clear=True)
+        finite = _finite(out) and all(_finite(g) for g in grads)
+        assert bool(flags) != finite, (attempt, flags, finite)
+        aborted += bool(flags)
+    assert aborted >= 1, "a 1 us spin limit never made the wide kernels give up a wait"
     prlstm_amd.set_spin_timeout_us(2_000_000)
-    with torch.no_grad():
-        out, (h_n, c_n) = m(x)
-    torch.cuda.synchronize()
+    out, grads = _step(m, x)
     prlstm_amd.check_errors()
-    assert _finite(out) and _finite(h_n) and _finite(c_n)
+    assert _finite(out) and all(_finite(g) for g in grads)

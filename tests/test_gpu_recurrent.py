@@ -174,9 +174,10 @@ def test_config3_large_hidden(dev):
 
 
 def test_config3_wide_forward(dev):
-    """configs[3] with the automatic path: the forward holds W_hh (64 MiB) in the registers
-    of 256 workgroups (rec_fwd_wide, path 3); the backward runs one launch per step."""
+    """configs[3] with the automatic path: forward and backward hold W_hh (64 MiB) in the
+    registers of 256 workgroups (rec_fwd_wide / rec_bwd_wide, path 3)."""
     check(64, 32, 1024, 2048, dev, 0, fwd_path=3)
+    assert prlstm_amd.last_recurrent_path() == 3
 
 
 @pytest.mark.parametrize("scope", [0, 1])
@@ -185,6 +186,7 @@ def test_wide_forward_partial_batch_hx(dev, scope):
     with device-scope stores for the partial exchange (scope 1)."""
     prlstm_amd.set_exchange_scope(scope)
     check(6, 20, 64, 2048, dev, 0, a=[0.3, 0.5, 0.1, 0.2], with_hx=True, fwd_path=3)
+    assert prlstm_amd.last_recurrent_path() == 3
 
 
 def test_sgd_training_step(dev):

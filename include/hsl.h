@@ -111,8 +111,10 @@ int hsl_poll_error(const void* ws, int* flag, void* stream);
  * _csrc/lstm_cell.cpp:38-43, RuntimeError at _metal.py:85-87). */
 int hsl_device_errors(int* flags, int clear, void* stream);
 /* Test hook (no reference counterpart): y[i] = f(x[i]) for n fp32 values with
- * the device math of the kernels, fn 0 = exp, 1 = sigmoid, 2 = tanh (the
- * reference computes them with torch.sigmoid / torch.tanh, _torch.py:29-34). */
+ * the device math of the kernels, fn 0 = exp, 1 = sigmoid, 2 = tanh, and
+ * fn 3 = sigmoid(x[i]) sigmoid(x[n-1-i]) as the scans form i*g (the reference
+ * computes them with torch.sigmoid / torch.tanh, _torch.py:29-34,
+ * _parallel.py:58-63). */
 int hsl_eval_math(int fn, const float* x, float* y, size_t n, void* stream);
 
 /* ---------------------------------------------------------------------------

@@ -97,7 +97,7 @@ namespace {
 __global__ void eval_math_kernel(int fn, const float* __restrict__ x, float* __restrict__ y, size_t n) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
     const float v = x[i];
-    y[i] = fn == 0 ? exp_f(v) : fn == 1 ? sigmoid_f(v) : tanh_f(v);
+    y[i] = fn == 0 ? exp_f(v) : fn == 1 ? sigmoid_f(v) : fn == 2 ? tanh_f(v) : sigmoid_prod_f(v, x[n - 1 - i]);
   }
 }
 }  // namespace
@@ -155,7 +155,9 @@ int hsl_timing_collect(int kind, double* total_ms, int* count) {
 }
 
 int hsl_eval_math(int fn, const float* x, float* y, size_t n, void* stream) {
-  if (fn < 0 || fn > 2) return hsl::fail(HSL_ERR_ARG, "hsl_eval_math: fn %d is not 0 (exp), 1 (sigmoid) or 2 (tanh)", fn);
+  if (fn < 0 || fn > 3)
+    return hsl::fail(HSL_ERR_ARG, "hsl_eval_math: fn %d is not 0 (exp), 1 (sigmoid), 2 (tanh) or 3 (sigmoid product)",
+                     fn);
   if (n == 0) return HSL_OK;
   if (!x || !y) return hsl::fail(HSL_ERR_ARG, "hsl_eval_math: null pointer");
   size_t blocks = (n + 255) / 256;

@@ -151,6 +151,12 @@ __device__ __forceinline__ float exp_f(float x) { return exp_scaled_f<1>(x); }
 // sigmoid(-large) -> 0 and sigmoid(+large) -> 1 without NaN.  Error: exp's, the rounding
 // of 1 + e and v_rcp_f32's (about 1 ulp each).
 __device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + exp_scaled_f<-1>(x)); }
+// sigmoid(x) sigmoid(y) = 1 / ((1 + e^-x)(1 + e^-y)) with one v_rcp_f32 for both.  The
+// denominators are >= 1 (or NaN), so their product is never 0 * inf; one that overflows
+// gives 0.  Error: the two exps', three roundings and the rcp's.
+__device__ __forceinline__ float sigmoid_prod_f(float x, float y) {
+  return __builtin_amdgcn_rcpf((1.0f + exp_scaled_f<-1>(x)) * (1.0f + exp_scaled_f<-1>(y)));
+}
 // tanh: for |x| < 1 the odd polynomial x + x^3 P(x^2), P of degree 6 fitted to
 // (tanh(x)/x - 1)/x^2 on [0, 1] by iteratively reweighted least squares in fp64 (relative
 // error of the model 4.6e-9); there 1 - 2/(1 + e^{2x}) would cancel (1.7e-4 relative error
@@ -180,6 +186,23 @@ __device__ __forceinline__ float tanh_impl(float x) {
 }
 __device__ __forceinline__ float tanh_f(float x) { return tanh_impl<false>(x); }
 __device__ __forceinline__ float tanh_pos_f(float x) { return tanh_impl<true>(x); }
+
+// Rows of floats addressed as a raw buffer: a uniform base and size in bytes, per-lane
+// byte offsets and a uniform byte offset.  A lane whose offset is at or beyond the size
+// reads 0 and its store is dropped, so lanes past the end (offset kOffNone) and rows
+// past the last step (size 0) need no branch and touch no memory.  Sizes < 2^31.
+constexpr unsigned kOffNone = 0x80000000u;
+constexpr int kCpolNt = 2;  // non-temporal: the stream is touched once
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const float* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)bytes, 0x00020000);
+}
+template <int CPOL = kCpolNt>
+__device__ __forceinline__ float row_load(__amdgpu_buffer_rsrc_t r, unsigned voff, int soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, soff, CPOL));
+}
+__device__ __forceinline__ void row_store_nt(float v, __amdgpu_buffer_rsrc_t r, unsigned voff, int soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)voff, soff, kCpolNt);
+}
 
 // Workgroup barrier that orders LDS accesses only.  __syncthreads() also waits for
 // the wave's outstanding global loads and stores; the persistent kernels and the scans

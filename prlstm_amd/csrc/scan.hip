@@ -23,7 +23,15 @@
 // next chunk's loads are issued before the current chunk is processed.  Every [T,...]
 // stream is read or written once, with non-temporal accesses (the streams bypass the
 // caches' retention; measured 9% faster forward on MI355X).
+//
+// The kernels are limited by their arithmetic and barriers as much as by HBM, so the
+// streams are raw buffer accesses with a uniform base per time step: rows past T are
+// given size 0 and lanes past the last channel an out-of-range offset, which reads 0 and
+// drops stores, so no lane computes a 64-bit address or branches around an access.
+// Chunks alternate between two register sets, and only the chunk that holds step T-1
+// carries the end-of-sequence conditions.
 #include <algorithm>
+#include <type_traits>
 
 #include "hsl_internal.h"
 
@@ -39,46 +47,51 @@ __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restri
                                                           int T, int B, int H) {
   __shared__ float2 sAV[NW][64];  // each wave's composed map (A, V) of the chunk
   __shared__ float sC[64];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int C = B * H;
   const int ch = blockIdx.x * 64 + lane;
   const bool ok = ch < C;
   const int b = ok ? ch / H : 0, j = ok ? ch % H : 0;
-  const size_t gstride = (size_t)B * 4 * H;  // per time step
-  const float* gbase = gates + (size_t)b * 4 * H + j;
-  const size_t ostride = (size_t)B * H;
+  const size_t gstride = (size_t)B * 4 * H, ostride = (size_t)C;  // per time step
+  const unsigned grow = (unsigned)(gstride * 4), orow = (unsigned)(ostride * 4);
+  const unsigned gv = ok ? (unsigned)(b * 4 * H + j) * 4u : kOffNone;  // lane offsets in a row
+  const unsigned ov = ok ? (unsigned)ch * 4u : kOffNone;
+  const int hb = 4 * H;  // bytes between gate planes
   if (w == 0) sC[lane] = ok ? fmaxf(c0 ? c0[ch] : 0.f, eps) : 0.f;
 
   constexpr int CH = NW * L;
-  const int nchunks = (T + CH - 1) / CH;
-  float cur[4][L], nxt[4][L];
-  auto load = [&](int chunk, float (&r)[4][L]) {
+  const int nchunks = (T + CH - 1) / CH, nfull = T / CH;
+  // the step loads: rows past T have size 0 (they read 0)
+  auto load = [&](int chunk, float(&r)[4][L]) {
 #pragma unroll
     for (int s = 0; s < L; ++s) {
       const int t = chunk * CH + w * L + s;
-      const bool v = ok && t < T;
-      const float* p = gbase + (size_t)t * gstride;
+      const auto rs = row_rsrc(gates + (size_t)t * gstride, t < T ? grow : 0u);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) r[g][s] = v ? __builtin_nontemporal_load(p + g * H) : 0.f;
+      for (int g = 0; g < 4; ++g) r[g][s] = row_load(rs, gv, g * hb);
     }
   };
-  if (nchunks > 0) load(0, cur);
-  for (int k = 0; k < nchunks; ++k) {
+  // one chunk from the registers cur, with the next chunk's loads issued into nxt first;
+  // TAIL: steps past T are identity maps (only the last chunk has any)
+  auto chunk = [&](auto tail, int k, float(&cur)[4][L], float(&nxt)[4][L]) {
+    constexpr bool TAIL = decltype(tail)::value;
     if (k + 1 < nchunks) load(k + 1, nxt);
-    float fv[L], bv[L], ov[L];
+    float fv[L], bv[L], ogv[L];
     float A = 1.f, V = 0.f;
 #pragma unroll
     for (int s = 0; s < L; ++s) {
-      const int t = k * CH + w * L + s;
-      const float ig = sigmoid_f(cur[0][s]), fg = sigmoid_f(cur[1][s]);
-      const float gg = sigmoid_f(cur[2][s]), og = sigmoid_f(cur[3][s]);
-      fv[s] = fmaxf(fg, eps);
-      bv[s] = fmaxf(ig * gg, eps);
-      ov[s] = og;
-      if (t < T) {
-        A = fv[s] * A;
-        V = fv[s] * V + bv[s];
+      float f = fmaxf(sigmoid_f(cur[1][s]), eps);
+      float bb = fmaxf(sigmoid_prod_f(cur[0][s], cur[2][s]), eps);
+      if (TAIL && k * CH + w * L + s >= T) {
+        f = 1.f;
+        bb = 0.f;
       }
+      fv[s] = f;
+      bv[s] = bb;
+      ogv[s] = sigmoid_f(cur[3][s]);
+      A = f * A;
+      V = f * V + bb;
     }
     sAV[w][lane] = float2{A, V};
     lds_barrier();
@@ -98,21 +111,25 @@ __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restri
 #pragma unroll
     for (int s = 0; s < L; ++s) {
       const int t = k * CH + w * L + s;
-      if (t < T) {
-        c = fv[s] * c + bv[s];
-        if (ok) {  // c >= eps > 0 (a positive combination of positive terms)
-          __builtin_nontemporal_store(ov[s] * tanh_pos_f(c), out + (size_t)t * ostride + ch);
-          __builtin_nontemporal_store(c, cseq + (size_t)t * ostride + ch);
-        }
-      }
+      const unsigned obytes = (!TAIL || t < T) ? orow : 0u;
+      c = fv[s] * c + bv[s];
+      // c >= eps > 0 (a positive combination of positive terms)
+      row_store_nt(ogv[s] * tanh_pos_f(c), row_rsrc(out + (size_t)t * ostride, obytes), ov, 0);
+      row_store_nt(c, row_rsrc(cseq + (size_t)t * ostride, obytes), ov, 0);
     }
     lds_barrier();
     if (w == NW - 1) sC[lane] = c;
-#pragma unroll
-    for (int s = 0; s < L; ++s)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) cur[g][s] = nxt[g][s];
+  };
+  // chunks alternate between two register sets, so no copies between them
+  float ra[4][L], rb[4][L];
+  if (nchunks > 0) load(0, ra);
+  int k = 0;
+  for (; k + 1 < nfull; k += 2) {
+    chunk(std::false_type{}, k, ra, rb);
+    chunk(std::false_type{}, k + 1, rb, ra);
   }
+  if (k < nchunks) chunk(std::true_type{}, k++, ra, rb);
+  if (k < nchunks) chunk(std::true_type{}, k, rb, ra);
 }
 
 // Reverse scan.  For wave steps [ws, we] and G_in = G_{we+1}:
@@ -127,15 +144,17 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
   __shared__ float2 sAV[NW][64];  // each wave's composed reverse map (A, V) of the chunk
   __shared__ float sG[64];
   __shared__ double sdb[NW][4][64];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int C = B * H;
   const int ch = blockIdx.x * 64 + lane;
   const bool ok = ch < C;
   const int b = ok ? ch / H : 0, j = ok ? ch % H : 0;
-  const size_t gstride = (size_t)B * 4 * H;
-  const float* gbase = gates + (size_t)b * 4 * H + j;
-  float* dgbase = dgates + (size_t)b * 4 * H + j;
-  const size_t ostride = (size_t)B * H;
+  const size_t gstride = (size_t)B * 4 * H, ostride = (size_t)C;
+  const unsigned grow = (unsigned)(gstride * 4), orow = (unsigned)(ostride * 4);
+  const unsigned gv = ok ? (unsigned)(b * 4 * H + j) * 4u : kOffNone;
+  const unsigned ov = ok ? (unsigned)ch * 4u : kOffNone;
+  const int hb = 4 * H;
   const float c0v = (ok && c0) ? c0[ch] : 0.f;
   const float c0c = ok ? fmaxf(c0v, eps) : 0.f;
   const bool c0_pass = ok && c0v >= eps;
@@ -144,29 +163,32 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
 
   constexpr int CH = NW * L;
   const int nchunks = (T + CH - 1) / CH;
-  // per step: zi zf zg zo c dout; plus zf at we+1 and c at ws-1
-  float cur[6][L], nxt[6][L];
-  float cur_fn, nxt_fn, cur_cp, nxt_cp;
-  auto load = [&](int chunk, float (&r)[6][L], float& fnext, float& cprev) {
+  // per step: zi zf zg zo c dout; plus zf at we+1 (fnext) and c at ws-1 (cprev); rows past
+  // T read 0
+  auto load = [&](int chunk, float(&r)[6][L], float& fnext, float& cprev) {
     const int ws = chunk * CH + w * L;
 #pragma unroll
     for (int s = 0; s < L; ++s) {
       const int t = ws + s;
-      const bool v = ok && t < T;
-      const float* p = gbase + (size_t)t * gstride;
+      const auto rg = row_rsrc(gates + (size_t)t * gstride, t < T ? grow : 0u);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) r[g][s] = v ? __builtin_nontemporal_load(p + g * H) : 0.f;
-      r[4][s] = v ? __builtin_nontemporal_load(cseq + (size_t)t * ostride + ch) : 0.f;
-      r[5][s] = v ? __builtin_nontemporal_load(dout + (size_t)t * ostride + ch) : 0.f;
+      for (int g = 0; g < 4; ++g) r[g][s] = row_load(rg, gv, g * hb);
+      r[4][s] = row_load(row_rsrc(cseq + (size_t)t * ostride, t < T ? orow : 0u), ov, 0);
+      r[5][s] = row_load(row_rsrc(dout + (size_t)t * ostride, t < T ? orow : 0u), ov, 0);
     }
     const int tn = ws + L;
-    fnext = (ok && tn < T) ? gbase[(size_t)tn * gstride + H] : 0.f;
-    cprev = ws == 0 ? c0c : ((ok && ws - 1 < T) ? cseq[(size_t)(ws - 1) * ostride + ch] : 0.f);
+    fnext = row_load<0>(row_rsrc(gates + (size_t)tn * gstride, tn < T ? grow : 0u), gv, hb);
+    const int tp = ws > 0 ? ws - 1 : 0;
+    const float cp = row_load<0>(row_rsrc(cseq + (size_t)tp * ostride, (ws > 0 && tp < T) ? orow : 0u), ov, 0);
+    cprev = ws == 0 ? c0c : cp;
   };
-  if (nchunks > 0) load(nchunks - 1, cur, cur_fn, cur_cp);
   double dbacc[4] = {0.0, 0.0, 0.0, 0.0};
   float g_first = 0.f, f_first = 0.f;  // G and f~ at this wave's first step (for dc0)
-  for (int k = nchunks - 1; k >= 0; --k) {
+  // one chunk (reverse); LAST: the chunk holding step T-1, the only one with steps at or
+  // past T-1 (dh_n, dc_n, f~_T = 0, identity maps past T)
+  auto chunk = [&](auto last, int k, float(&cur)[6][L], float cur_fn, float cur_cp, float(&nxt)[6][L],
+                   float& nxt_fn, float& nxt_cp) {
+    constexpr bool LAST = decltype(last)::value;
     if (k > 0) load(k - 1, nxt, nxt_fn, nxt_cp);
     const int ws = k * CH + w * L;
     // sigma(z_f), sigma(z_o) and tanh(c) of each step, computed once and used by both
@@ -176,80 +198,92 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
     for (int s = 0; s < L; ++s) {
       fgv[s] = sigmoid_f(cur[1][s]);
       ogv[s] = sigmoid_f(cur[3][s]);
-      tcv[s] = tanh_f(cur[4][s]);
+      tcv[s] = tanh_pos_f(cur[4][s]);  // c >= eps > 0
     }
     const float fg_after = sigmoid_f(cur_fn);
 #pragma unroll
     for (int s = 0; s < L; ++s) {
       const int t = ws + s;
-      fn[s] = (t + 1 < T) ? fmaxf(s + 1 < L ? fgv[s + 1] : fg_after, eps) : 0.f;
+      fn[s] = (!LAST || t + 1 < T) ? fmaxf(s + 1 < L ? fgv[s + 1] : fg_after, eps) : 0.f;
       float d = cur[5][s];
-      if (t == T - 1) d = d + dhn;
+      if (LAST && t == T - 1) d = d + dhn;
       float e = d * ogv[s] * (1.0f - tcv[s] * tcv[s]);
-      if (t == T - 1) e = e + dcn;
-      ev[s] = (t < T) ? e : 0.f;
+      if (LAST && t == T - 1) e = e + dcn;
+      ev[s] = (!LAST || t < T) ? e : 0.f;
     }
     float A = 1.f, V = 0.f;
 #pragma unroll
     for (int s = L - 1; s >= 0; --s) {
-      if (ws + s < T) {
+      if (!LAST || ws + s < T) {
         V = ev[s] + fn[s] * V;
         A = fn[s] * A;
       }
     }
     sAV[w][lane] = float2{A, V};
     lds_barrier();
-    // carry-in from the later waves NW-1 .. w+1, applied in order; with 8 waves all maps
-    // fit in registers and are read at once (one LDS latency instead of one per map)
+    // carry-in from the later waves NW-1 .. w+1, applied in order; the maps are read four
+    // at a time (one LDS latency per four)
     float G = sG[lane];
-    float2 m[NW - 1];
+#pragma unroll 1
+    for (int u0 = NW - 1; u0 > w; u0 -= 4) {
+      float2 m[4];
 #pragma unroll
-    for (int u = 1; u < NW; ++u) m[u - 1] = sAV[u][lane];
+      for (int i = 0; i < 4; ++i) m[i] = sAV[max(u0 - i, 0)][lane];
 #pragma unroll
-    for (int u = NW - 1; u >= 1; --u)
-      if (u > w) G = m[u - 1].x * G + m[u - 1].y;
+      for (int i = 0; i < 4; ++i)
+        if (u0 - i > w) G = m[i].x * G + m[i].y;
+    }
+    float dsum[4] = {0.f, 0.f, 0.f, 0.f};  // the chunk's dgates sums, added into fp64 below
 #pragma unroll
     for (int s = L - 1; s >= 0; --s) {
       const int t = ws + s;
-      if (t < T) {
+      if (!LAST || t < T) {
         G = ev[s] + fn[s] * G;
         const float ig = sigmoid_f(cur[0][s]), gg = sigmoid_f(cur[2][s]);
         const float fg = fgv[s], og = ogv[s], tc = tcv[s];
         const float cprev = s > 0 ? cur[4][s - 1] : cur_cp;
         float d = cur[5][s];
-        if (t == T - 1) d = d + dhn;
+        if (LAST && t == T - 1) d = d + dhn;
         const float bb = ig * gg;
         const float dbb = bb >= eps ? G : 0.f;
         const float dfp = fg >= eps ? (G * cprev) * fg * (1.0f - fg) : 0.f;
-        const float dip = (dbb * gg) * ig * (1.0f - ig);
-        const float dgp = (dbb * ig) * gg * (1.0f - gg);
+        const float dbq = dbb * bb;
+        const float dip = dbq * (1.0f - ig);
+        const float dgp = dbq * (1.0f - gg);
         const float dop = (d * tc) * og * (1.0f - og);
-        if (ok) {
-          float* q = dgbase + (size_t)t * gstride;
-          __builtin_nontemporal_store(dip, q);
-          __builtin_nontemporal_store(dfp, q + H);
-          __builtin_nontemporal_store(dgp, q + 2 * H);
-          __builtin_nontemporal_store(dop, q + 3 * H);
-        }
-        dbacc[0] += (double)dip;
-        dbacc[1] += (double)dfp;
-        dbacc[2] += (double)dgp;
-        dbacc[3] += (double)dop;
+        const auto rq = row_rsrc(dgates + (size_t)t * gstride, grow);
+        row_store_nt(dip, rq, gv, 0);
+        row_store_nt(dfp, rq, gv, hb);
+        row_store_nt(dgp, rq, gv, 2 * hb);
+        row_store_nt(dop, rq, gv, 3 * hb);
+        dsum[0] += dip;
+        dsum[1] += dfp;
+        dsum[2] += dgp;
+        dsum[3] += dop;
         if (s == 0) {
           g_first = G;
           f_first = fmaxf(fg, eps);
         }
       }
     }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) dbacc[g] += (double)dsum[g];
     lds_barrier();
     if (w == 0) sG[lane] = G;
-#pragma unroll
-    for (int s = 0; s < L; ++s)
-#pragma unroll
-      for (int r = 0; r < 6; ++r) cur[r][s] = nxt[r][s];
-    cur_fn = nxt_fn;
-    cur_cp = nxt_cp;
+  };
+  // chunks alternate between two register sets, so no copies between them
+  float ra[6][L], rb[6][L];
+  float fa = 0.f, pa = 0.f, fb = 0.f, pb = 0.f;
+  if (nchunks > 0) {
+    load(nchunks - 1, ra, fa, pa);
+    chunk(std::true_type{}, nchunks - 1, ra, fa, pa, rb, fb, pb);
   }
+  int k = nchunks - 2;
+  for (; k >= 1; k -= 2) {
+    chunk(std::false_type{}, k, rb, fb, pb, ra, fa, pa);
+    chunk(std::false_type{}, k - 1, ra, fa, pa, rb, fb, pb);
+  }
+  if (k == 0) chunk(std::false_type{}, 0, rb, fb, pb, ra, fa, pa);
   // dc0 = G_0 f~_0 where the clamp of c0 passes gradient
   if (w == 0 && ok && dc0) dc0[ch] = (c0_pass && T > 0) ? g_first * f_first : 0.f;
   if (db_part) {
@@ -269,8 +303,9 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
 
 int check_scan_dims(int T, int B, int H) {
   if (T < 0 || B < 0 || H < 0) return fail(HSL_ERR_ARG, "negative dimension (T=%d B=%d H=%d)", T, B, H);
-  if ((long long)B * H >= (1ll << 31) || (long long)T * B * 4 * H > (1ll << 40))
-    return fail(HSL_ERR_UNSUPPORTED, "problem too large");
+  // one time step of gates (16 B H bytes) is addressed as a buffer of < 2^31 bytes
+  if ((long long)B * H * 16 >= (1ll << 31) || (long long)T * B * 4 * H > (1ll << 40))
+    return fail(HSL_ERR_UNSUPPORTED, "problem too large (B*H = %lld; at most 2^27 - 1 channels)", (long long)B * H);
   return HSL_OK;
 }
 

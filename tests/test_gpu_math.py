@@ -10,6 +10,9 @@ result (ulp of the fp64 value, 2^-149 below the normal range):
            own fp32 CPU sigmoid 2.47);
   tanh     <= 1.5 ulp (below |x| = 1 an odd polynomial, measured 0.53 near zero; above
            it 1 - 2/(1 + e^{2|x|}), whose cancellation is bounded there; measured 1.02).
+  sigmoid(x) sigmoid(y), the scans' i*g (_parallel.py:63), with one rcp of the product of
+           the two denominators: <= 5 ulp (two exps, three roundings, v_rcp_f32;
+           measured 4.44, torch's fp32 CPU product of two sigmoids 3.45).
 Results below the normal range (exp(x < -87.3), sigmoid(x < -87.3)) may be flushed:
 their absolute error must stay below 2^-126.  Special values: exp(+-inf) = inf / 0,
 sigmoid(+-inf) = 1 / 0, tanh(+-inf) = +-1, NaN in gives NaN out.
@@ -24,8 +27,8 @@ from prlstm_amd import _lib
 
 pytestmark = pytest.mark.gpu
 
-FN = {"exp": 0, "sigmoid": 1, "tanh": 2}
-BOUND = {"exp": 1.5, "sigmoid": 3.5, "tanh": 1.5}
+FN = {"exp": 0, "sigmoid": 1, "tanh": 2, "sigmoid_prod": 3}
+BOUND = {"exp": 1.5, "sigmoid": 3.5, "tanh": 1.5, "sigmoid_prod": 5.0}
 TORCH64 = {"exp": torch.exp, "sigmoid": torch.sigmoid, "tanh": torch.tanh}
 
 
@@ -54,9 +57,20 @@ def _sweep():
     return x[torch.isfinite(x)]
 
 
-@pytest.mark.parametrize("name", ["exp", "sigmoid", "tanh"])
+def _sigmoid_prod(x):
+    """sigmoid(x[i]) sigmoid(x[n-1-i]), the pairing of hsl_eval_math fn 3."""
+    return torch.sigmoid(x) * torch.sigmoid(x.flip(0))
+
+
+TORCH64["sigmoid_prod"] = _sigmoid_prod
+
+
+@pytest.mark.parametrize("name", ["exp", "sigmoid", "tanh", "sigmoid_prod"])
 def test_device_math_ulp(dev, name):
     x = _sweep()
+    if name == "sigmoid_prod":  # pair every sweep value with a shuffled partner too
+        g = torch.Generator().manual_seed(0)
+        x = torch.cat([x, x[torch.randperm(x.numel(), generator=g)]])
     y = _dev_eval(name, x, dev).double()
     ref = TORCH64[name](x.double())
     cpu32 = TORCH64[name](x).double()
@@ -88,13 +102,15 @@ def test_device_math_small_arguments_relative(dev):
     assert rel < 2 * 2.0 ** -24, rel
 
 
-@pytest.mark.parametrize("name", ["exp", "sigmoid", "tanh"])
+@pytest.mark.parametrize("name", ["exp", "sigmoid", "tanh", "sigmoid_prod"])
 def test_device_math_special_values(dev, name):
     x = torch.tensor([math.inf, -math.inf, math.nan, 0.0, -0.0], dtype=torch.float32)
     y = _dev_eval(name, x, dev)
+    # sigmoid_prod pairs x[i] with x[4-i]: (inf, -0), (-inf, 0), (nan, nan), (0, -inf), (-0, inf)
     want = {"exp": [math.inf, 0.0, math.nan, 1.0, 1.0],
             "sigmoid": [1.0, 0.0, math.nan, 0.5, 0.5],
-            "tanh": [1.0, -1.0, math.nan, 0.0, 0.0]}[name]
+            "tanh": [1.0, -1.0, math.nan, 0.0, 0.0],
+            "sigmoid_prod": [0.5, 0.0, math.nan, 0.0, 0.5]}[name]
     for got, w, xi in zip(y.tolist(), want, x.tolist()):
         if math.isnan(w):
             assert math.isnan(got), (name, xi, got)

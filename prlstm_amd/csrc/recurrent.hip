@@ -28,6 +28,7 @@
 #include <type_traits>
 
 #include "gemm_core.h"
+#include "split_bf16.h"
 
 namespace hsl {
 
@@ -569,6 +570,10 @@ __device__ __forceinline__ lds_vint* step_flags() { return (lds_vint*)(s_step_fl
 // for the 8 steps of a block.  Rows are padded to 36 floats.
 constexpr int kXinSteps = 8;
 constexpr bool kXprojAfterPublish = true;  // projection products wait for the step's publish
+#ifndef HSL_XPROJ_SPLIT
+#define HSL_XPROJ_SPLIT 1
+#endif
+constexpr bool kXprojSplit = HSL_XPROJ_SPLIT;  // split bf16 projection products when enabled
 typedef float XinBuf[2][4][64][kXinSteps * 4 + 4];
 // With the projection waves present, recurrent wave q's cell lanes do not store the
 // step's saved activations themselves: they leave them in LDS and projection wave q
@@ -807,7 +812,7 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
 // 8m-1).  Its x operands are loaded two blocks ahead.  Block 0 is computed and written
 // before one extra barrier ahead of the first step.  The waves take part in every
 // workgroup barrier of the recurrent waves and leave when the group aborts, as they do.
-template <int KQ>
+template <int KQ, bool XS>
 __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg, XinBuf* xin, int& abort_flag) {
   const int T = p.T, B = p.B, H = p.H, D = p.D, Bg = p.Bg;
   const int lane = threadIdx.x & 63;
@@ -825,6 +830,16 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
       const int k = kb + i;
       wa[rt][i] = (ok && k < D) ? wrow[k] : 0.f;
     }
+  }
+  // XS: W_ih's rows as their three bf16 pieces for the four 16-deep k-steps (the fp32
+  // rows are not kept)
+  u32x4 wp[XS ? 2 : 1][XS ? 4 : 1][3];
+  if constexpr (XS) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) split8(&wa[rt][8 * i], wp[rt][i]);
+    __builtin_amdgcn_sched_barrier(0);  // the fp32 rows die before the x rows arrive
   }
   // column l32 = t%8 * 4 + batch slot; absent slots read batch 0 (their column is unused)
   const int bsl = l32 & 3, tl = l32 >> 2, cb = grp * Bg + bsl;
@@ -845,12 +860,36 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
     }
   };
   f16v acc[2] = {f16v{}, f16v{}};
-  auto products = [&](const float (&xo)[32], int i0, int i1) {  // k-steps i0 .. i1-1
+  // part `sub` of `of` parts of a block's products
+  auto products = [&](const float (&xo)[32], int sub, int of) {
+    if constexpr (XS) {
+      // 16-deep k-steps on the exact bf16 split (split_bf16.h): k-step i multiplies the
+      // lane's values 8i .. 8i+7 (A: W_ih row l%32, B: column l%32 of x; lanes 0-31 hold k
+      // kb0 + 8i .., lanes 32-63 kb0 + 32 + 8i ..), six piece products each.  16-bit
+      // products leave the recurrent wave on the same SIMD its issue slots, where the
+      // fp32 instruction holds them off.
 #pragma unroll
-    for (int i = i0; i < i1; ++i)
+      for (int i = 4 * sub / of; i < 4 * (sub + 1) / of; ++i) {
+        float xv[8];
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-        acc[rt] = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[rt][i], xo[i], acc[rt], 0, 0, 0);
+        for (int e = 0; e < 8; ++e) {
+          xv[e] = xo[8 * i + e];
+          asm volatile("" : "+v"(xv[e]));  // split here, next to the products
+        }
+        u32x4 pb[3];
+        split8(xv, pb);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+          for (int pp = 0; pp < 6; ++pp) acc[rt] = mfma_bf16(wp[rt][i][kPa[pp]], pb[kPb[pp]], acc[rt]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 32 * sub / of; i < 32 * (sub + 1) / of; ++i)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+          acc[rt] = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[rt][i], xo[i], acc[rt], 0, 0, 0);
+    }
   };
   auto write_blk = [&](int m) {  // D layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column l%32
 #pragma unroll
@@ -864,12 +903,19 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
     }
   };
 
-  float xa[32], xb[32];  // x operands of even / odd blocks
+  // x operands of even / odd blocks, loaded two blocks ahead; XS: one set, loaded one
+  // block ahead (its products start in the second step of a block, three steps after the
+  // load, and the registers go to W_ih's pieces)
+  constexpr int LA = XS ? 2 : 3;
+  float xa[32], xb[XS ? 1 : 32];
   load_blk(0, xa);
-  load_blk(1, xb);
-  products(xa, 0, 32);
+  if constexpr (!XS) load_blk(1, xb);
+  products(xa, 0, 1);
   write_blk(0);
-  load_blk(2, xa);
+  if constexpr (XS)
+    load_blk(1, xa);
+  else
+    load_blk(2, xa);
   lds_barrier();  // the recurrent waves' barrier ahead of their first step
   // window j: the 8 steps of block j, computing block j+1 from its operand set in steps
   // 0-5 (k-steps 32 sub / 6 .. 32 (sub+1) / 6 in step sub) and writing it in step 6, when
@@ -886,7 +932,7 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
       if (t > 0) store_saves(p, grp, wg, save_buf(xin), w, t - 1);  // staged before this barrier
       if (next && sub == 6) {  // block j+1, whose products ended a step ago, to xin
         write_blk(j + 1);
-        load_blk(j + 3, xu);
+        load_blk(j + LA, xu);
       } else if (next && sub < 6) {
         if constexpr (kXprojAfterPublish) {  // after the recurrent waves' publish of h_t
           const long long t0 = wall_clock64();
@@ -902,14 +948,19 @@ __device__ __forceinline__ void rec_fwd_xproj(const PFwdArgs& p, int grp, int wg
             __builtin_amdgcn_s_sleep(1);
           }
         }
-        products(xu, 32 * sub / 6, 32 * (sub + 1) / 6);
+        products(xu, sub, 6);
       }
     }
     return true;
   };
-  for (int j = 0;; j += 2) {
-    if (!window(j, xb)) break;
-    if (!window(j + 1, xa)) break;
+  if constexpr (XS) {
+    for (int j = 0;; ++j)
+      if (!window(j, xa)) break;
+  } else {
+    for (int j = 0;; j += 2) {
+      if (!window(j, xb)) break;
+      if (!window(j + 1, xa)) break;
+    }
   }
 }
 
@@ -937,7 +988,9 @@ __device__ void poison_fwd(const PFwdArgs& p, int grp, int wg) {
 // is not read from gih, and store the saved activations.  Every wave ends with one more workgroup barrier: a wave that
 // gave up a wait has set abort_flag before it (waves that left early have terminated
 // and are not waited for), so all waves agree on whether to poison their outputs.
-template <int KQ, bool XP>
+// XP: 0 = no projection waves, 1 = projection products on the fp32 instruction, 2 = on
+// split bf16 pieces (hsl_set_split_products).
+template <int KQ, int XP>
 __global__ __launch_bounds__(XP ? 512 : 256, 1) void rec_fwd_persistent(PFwdArgs p) {
   constexpr int HP = 4 * KQ;
   __shared__ f4 red[2][4][64];  // [step parity][batch slot][gate row] -> 4 wave partials
@@ -954,15 +1007,15 @@ __global__ __launch_bounds__(XP ? 512 : 256, 1) void rec_fwd_persistent(PFwdArgs
     bool proj = false;
     if constexpr (XP) {
       if (threadIdx.x >= 256) {
-        rec_fwd_xproj<KQ>(p, grp, wg, xin, abort_flag);
+        rec_fwd_xproj<KQ, XP == 2>(p, grp, wg, xin, abort_flag);
         proj = true;
       }
     }
     if (!proj) {
       if (fast)
-        rec_fwd_body<KQ, true, XP>(p, grp, wg, red, xin, abort_flag);
+        rec_fwd_body<KQ, true, (XP > 0)>(p, grp, wg, red, xin, abort_flag);
       else
-        rec_fwd_body<KQ, false, XP>(p, grp, wg, red, xin, abort_flag);
+        rec_fwd_body<KQ, false, (XP > 0)>(p, grp, wg, red, xin, abort_flag);
     }
   }
   // The projection waves' save stores complete before the barrier (workgroup-scope
@@ -1544,6 +1597,7 @@ struct PersistentPlan {
   int KQ = 0, Hp = 0, NG = 0, NGX = 0, Bg = 0, NW = 0, grid = 0;
   int XT = -1;  // backward: -1 no weight-gradient waves, 0 dW_hh only, 2 dW_hh and dW_ih
   bool XP = false;  // forward: input projection inside the kernel (512 threads)
+  bool XS = false;  // with XP: its products on split bf16 pieces
 };
 
 int pick_kq(int H) {
@@ -1578,6 +1632,15 @@ bool fused_wgrad_enabled() {
     return !(e && e[0] == '0');
   }();
   return on;
+}
+
+template <int KQ>
+int fwd_resident(int xp, int* occ) {
+  switch (xp) {
+    case 0: return max_resident(rec_fwd_persistent<KQ, 0>, 256, occ);
+    case 1: return max_resident(rec_fwd_persistent<KQ, 1>, 512, occ);
+    default: return max_resident(rec_fwd_persistent<KQ, 2>, 512, occ);
+  }
 }
 
 template <int KQ>
@@ -1617,6 +1680,7 @@ int plan_persistent(int B, int H, int D, bool bwd, PersistentPlan* pl) {
   // the forward's projection waves hold W_ih rows for a quarter of D <= 256 each and read
   // x rows with 16-byte loads
   if (!bwd && fused_xproj_enabled()) p.XP = D > 0 && D <= 256 && D % 4 == 0;
+  p.XS = kXprojSplit && split_products_mode();
   int occ = 0;
   for (;;) {
     if (bwd) {
@@ -1627,12 +1691,12 @@ int plan_persistent(int B, int H, int D, bool bwd, PersistentPlan* pl) {
         default: HSL_CHECK(bwd_resident<128>(p.XT, &occ)); break;
       }
     } else {
-      const int th = p.XP ? 512 : 256;
+      const int xp = p.XP ? (p.XS ? 2 : 1) : 0;
       switch (kq) {
-        case 16: HSL_CHECK(p.XP ? max_resident(rec_fwd_persistent<16, true>, th, &occ) : max_resident(rec_fwd_persistent<16, false>, th, &occ)); break;
-        case 32: HSL_CHECK(p.XP ? max_resident(rec_fwd_persistent<32, true>, th, &occ) : max_resident(rec_fwd_persistent<32, false>, th, &occ)); break;
-        case 64: HSL_CHECK(p.XP ? max_resident(rec_fwd_persistent<64, true>, th, &occ) : max_resident(rec_fwd_persistent<64, false>, th, &occ)); break;
-        default: HSL_CHECK(p.XP ? max_resident(rec_fwd_persistent<128, true>, th, &occ) : max_resident(rec_fwd_persistent<128, false>, th, &occ)); break;
+        case 16: HSL_CHECK(fwd_resident<16>(xp, &occ)); break;
+        case 32: HSL_CHECK(fwd_resident<32>(xp, &occ)); break;
+        case 64: HSL_CHECK(fwd_resident<64>(xp, &occ)); break;
+        default: HSL_CHECK(fwd_resident<128>(xp, &occ)); break;
       }
     }
     // every workgroup must be resident at once: the waits are between workgroups
@@ -1891,12 +1955,13 @@ int check_dims(int T, int B, int D, int H) {
 }
 
 template <int KQ>
-void launch_fwd_persistent(const PFwdArgs& a, int grid, bool xp, hipStream_t s) {
+void launch_fwd_persistent(const PFwdArgs& a, int grid, int xp, hipStream_t s) {
   static_assert(sizeof(XinBuf) + sizeof(SaveBuf) <= (size_t)kPadLdsBytes, "xin and the staged saves live in the padding LDS");
-  if (xp)
-    hipLaunchKernelGGL((rec_fwd_persistent<KQ, true>), dim3(grid), dim3(512), kPadLdsBytes, s, a);
-  else
-    hipLaunchKernelGGL((rec_fwd_persistent<KQ, false>), dim3(grid), dim3(256), kPadLdsBytes, s, a);
+  switch (xp) {
+    case 0: hipLaunchKernelGGL((rec_fwd_persistent<KQ, 0>), dim3(grid), dim3(256), kPadLdsBytes, s, a); break;
+    case 1: hipLaunchKernelGGL((rec_fwd_persistent<KQ, 1>), dim3(grid), dim3(512), kPadLdsBytes, s, a); break;
+    default: hipLaunchKernelGGL((rec_fwd_persistent<KQ, 2>), dim3(grid), dim3(512), kPadLdsBytes, s, a); break;
+  }
 }
 template <int KQ>
 void launch_bwd_persistent(const PBwdArgs& a, int grid, int xt, hipStream_t s) {
@@ -2030,12 +2095,13 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
     PFwdArgs pa{w.gih, w_hh, b_hh, a, h0, c0, h_save, c_save, gact, tanh_c, w.xbuf, w.hello, w.err,
                 T, B, H, pl.Hp, pl.NG, pl.NGX, pl.Bg, pl.NW, exchange_scope_mode(), spin_timeout_ticks(),
                 x, w_ih, b_ih, D};
+    const int xp = pl.XP ? (pl.XS ? 2 : 1) : 0;
     const int slot = timing_begin(kTimeRecFwd, s);
     switch (pl.KQ) {
-      case 16: launch_fwd_persistent<16>(pa, pl.grid, pl.XP, s); break;
-      case 32: launch_fwd_persistent<32>(pa, pl.grid, pl.XP, s); break;
-      case 64: launch_fwd_persistent<64>(pa, pl.grid, pl.XP, s); break;
-      default: launch_fwd_persistent<128>(pa, pl.grid, pl.XP, s); break;
+      case 16: launch_fwd_persistent<16>(pa, pl.grid, xp, s); break;
+      case 32: launch_fwd_persistent<32>(pa, pl.grid, xp, s); break;
+      case 64: launch_fwd_persistent<64>(pa, pl.grid, xp, s); break;
+      default: launch_fwd_persistent<128>(pa, pl.grid, xp, s); break;
     }
     HSL_HIP(hipGetLastError());
     timing_end(slot, s);

@@ -1288,70 +1288,77 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
 // in registers while they wait.  Per step, the dgates of the four batch slots are read
 // from the LDS copy the recurrent waves already make (dgl, valid between the step's
 // barrier and the next), h_{t-1} and x_t rows are loaded one step ahead, and the
-// products are v_mfma_f32_32x32x2_f32 with the batch as the reduction index (two
-// instructions per 32x32 tile).  The products start only after the recurrent waves
-// have issued theirs (s_step_flag), so they fill the idle part of the step.  Wave w owns the
-// 32-column tiles w, w+4, ... of h (HT of them) and of x (XT).
+// batch is the reduction index of the products.  The products start only after the
+// recurrent waves have issued theirs (s_step_flag), so they fill the idle part of the step.
 //
 // Accuracy: no fp32 running sum spans more than a few hundred products.  dW_hh_s is
 // written as an fp32 partial plane every TS steps (its gradient dW_hh = a dW_hh_s is
 // a-scaled); dW_ih goes into an fp64 accumulator in LDS (64 rows x D, written once as
-// an fp64 plane per group): at the start of each step one of the wave's 2*XT
-// accumulator tiles is added to it with ds_add_f64 (no returned value) and restarted,
-// so an fp32 run covers 2*XT steps.  The planes are summed in fp64 afterwards.
+// an fp64 plane per group): at the start of each step one of the wave's 4*XT
+// accumulator sets (two 16x16 tiles) is added to it with ds_add_f64 (no returned value)
+// and restarted, so an fp32 run covers 4*XT steps.  The planes are summed in fp64
+// afterwards.
 //
 // The wave takes part in every workgroup barrier of the recurrent waves (one per step)
 // and leaves when the group aborts, as they do.
 constexpr int kXaccLdsBytes = 64 * 256 * 8;  // fp64 dW_ih accumulator for D <= 256
 
+// The products are v_mfma_f32_16x16x4_f32, one instruction per 16x16 tile and step (k =
+// the four batch slots): the matrix-core time of two 32x32x2 per 32x32 tile in
+// half-length instructions.  A second wave streaming 32x32x2 f32 products holds off the
+// recurrent wave on its SIMD about twice as long as one streaming 16x16x4 (a same-XCD
+// hand-off measured 1.52 against 0.89 us beside them, 0.42 us alone); 16-bit products
+// would not hold it off at all, but their four-step operand staging does not fit the
+// registers and LDS the two waves per SIMD leave.  Wave w owns the 32-column groups w,
+// w+4, ... of h and of x, each two 16-column tiles, and the four 16-row tiles.
 template <int KQ, int XT>
 __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg, float (&dgl)[2][4][68],
-                                              double* xacc, int& abort_flag) {
-  constexpr int HT = KQ >= 32 ? KQ / 32 : 1;  // h column tiles per wave (4*KQ >= H)
+                                                double* xacc, int& abort_flag) {
+  constexpr int HT = KQ >= 32 ? KQ / 32 : 1;  // h column groups of 32 per wave (4*KQ >= H)
   constexpr int XA = XT > 0 ? XT : 1;
   const int T = p.T, B = p.B, H = p.H, D = p.D, Bg = p.Bg, NG = p.NG, TS = p.TS;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) - 4);
-  const int half = lane >> 5, l32 = lane & 31;
-  // k index of the products = batch slot 2*ks + half
-  bool bok[2];
-  int brow[2];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const int b = 2 * ks + half, cb = grp * Bg + b;
-    bok[ks] = b < Bg && cb < B;
-    brow[ks] = bok[ks] ? cb : 0;
-  }
+  const int kb = lane >> 4, l16 = lane & 15;  // k index of the products = batch slot kb
+  const int cb = grp * Bg + kb;
+  const bool bok = kb < Bg && cb < B;
+  const int brow = bok ? cb : 0;
   const int nth = (H + 31) / 32, ntx = (D + 31) / 32;
-  // operand columns: clamped in range, so that the loads need no condition (a column
-  // past H or D only feeds an output column that is never written)
-  auto hcol = [&](int i) { return min((w + 4 * i) * 32 + l32, H - 1); };
-  auto xcol = [&](int i) { return min((w + 4 * i) * 32 + l32, D - 1); };
-  f16v acch[HT][2], accx[XA][2];
+  // operand column of group g, half sub: clamped in range (a column past H or D only feeds
+  // an output column that is never written)
+  auto hcol = [&](int g, int sub) { return min((w + 4 * g) * 32 + 16 * sub + l16, H - 1); };
+  auto xcol = [&](int g, int sub) { return min((w + 4 * g) * 32 + 16 * sub + l16, D - 1); };
+  f4 acch[HT][2][4], accx[XA][2][4];  // [column group][half][row tile]
   auto zero_h = [&]() {
 #pragma unroll
-    for (int i = 0; i < HT; ++i)
+    for (int g = 0; g < HT; ++g)
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) acch[i][rt] = f16v{};
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) acch[g][sub][rt] = f4{0.f, 0.f, 0.f, 0.f};
   };
   auto zero_x = [&]() {
 #pragma unroll
-    for (int i = 0; i < XA; ++i)
+    for (int g = 0; g < XA; ++g)
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) accx[i][rt] = f16v{};
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) accx[g][sub][rt] = f4{0.f, 0.f, 0.f, 0.f};
   };
   zero_h();
   zero_x();
-  // D-layout of a 32x32 tile: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column l%32
-  auto tile_row = [&](int rt, int r) { return rt * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
+  // D-layout of a 16x16 tile: lane l, register r -> row 4(l/16) + r, column l%16
+  auto tile_row = [&](int rt, int r) { return rt * 16 + 4 * kb + r; };
   if constexpr (XT > 0) {
 #pragma unroll
-    for (int i = 0; i < XT; ++i) {
-      if (w + 4 * i >= ntx) continue;
+    for (int g = 0; g < XT; ++g) {
+      if (w + 4 * g >= ntx) continue;
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) xacc[tile_row(rt, r) * 256 + (w + 4 * i) * 32 + l32] = 0.0;
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xacc[tile_row(rt, r) * 256 + (w + 4 * g) * 32 + 16 * sub + l16] = 0.0;
     }
   }
 
@@ -1361,82 +1368,81 @@ __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg
     float x[XA][2];
   };
   auto load_ops = [&](int t, Ops& o) {
+    const float* hr = p.h_save + ((size_t)t * B + brow) * H;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const float* hr = p.h_save + ((size_t)t * B + brow[ks]) * H;
+    for (int g = 0; g < HT; ++g)
 #pragma unroll
-      for (int i = 0; i < HT; ++i) o.h[i][ks] = hr[hcol(i)];
-      if constexpr (XT > 0) {
-        const float* xr = p.x + ((size_t)t * B + brow[ks]) * D;
+      for (int sub = 0; sub < 2; ++sub) o.h[g][sub] = hr[hcol(g, sub)];
+    if constexpr (XT > 0) {
+      const float* xr = p.x + ((size_t)t * B + brow) * D;
 #pragma unroll
-        for (int i = 0; i < XT; ++i) o.x[i][ks] = xr[xcol(i)];
-      }
+      for (int g = 0; g < XT; ++g)
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) o.x[g][sub] = xr[xcol(g, sub)];
     }
   };
-  // Row r64 = R0 + 4*half of a tile register (R0 = rt*32 + 8(r/4) + r%4) is gate R0/16,
-  // unit wg*16 + R0%16 + 4*half: the store address splits into a uniform part (R0) and
-  // a 32-bit lane part shared by all registers.
-  const int ulane = wg * kUnits + 4 * half;
+  // Row r64 = rt*16 + 4*kb + r of a tile is gate rt, unit wg*16 + 4*kb + r.
+  const int ulane = wg * kUnits + 4 * kb;
   auto dump_h = [&](int chunk) {
     float* const plane = p.wph + ((size_t)chunk * NG + grp) * 4 * H * H;
 #pragma unroll
-    for (int i = 0; i < HT; ++i) {
-      const int c = (w + 4 * i) * 32 + l32;
-      if (w + 4 * i >= nth) continue;
-      const unsigned lo = 4u * ((unsigned)ulane * H + c);
+    for (int g = 0; g < HT; ++g) {
+      if (w + 4 * g >= nth) continue;
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int sub = 0; sub < 2; ++sub) {
+        const int c = (w + 4 * g) * 32 + 16 * sub + l16;
+        const unsigned lo = 4u * ((unsigned)ulane * H + c);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int R0 = rt * 32 + 8 * (r >> 2) + (r & 3);
-          float* const rb = plane + (size_t)((R0 >> 4) * H + (R0 & 15)) * H;
-          if (ulane + (R0 & 15) < H && c < H) *byte_at(rb, lo) = acch[i][rt][r];
-        }
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float* const rb = plane + (size_t)(rt * H + r) * H;
+            if (ulane + r < H && c < H) *byte_at(rb, lo) = acch[g][sub][rt][r];
+          }
+      }
     }
     zero_h();
   };
-  // adds accumulator tile f = 2*i + rt of every wave whose flag is set to the fp64 copy
+  // adds accumulator tile sel = 2*(g*2 + sub) ... of every wave's x groups to the fp64
+  // copy: selection f in [0, 4 XT) picks (g, sub, row-tile pair)
   auto fold_x = [&](int sel) {
 #pragma unroll
-    for (int i = 0; i < XT; ++i) {
-      if (w + 4 * i >= ntx) continue;
+    for (int g = 0; g < XT; ++g) {
+      if (w + 4 * g >= ntx) continue;
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        if (sel >= 0 && sel != 2 * i + rt) continue;
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          __hip_atomic_fetch_add(&xacc[tile_row(rt, r) * 256 + (w + 4 * i) * 32 + l32], (double)accx[i][rt][r],
-                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        accx[i][rt] = f16v{};
-      }
+        for (int rp = 0; rp < 2; ++rp) {
+          if (sel >= 0 && sel != 4 * g + 2 * sub + rp) continue;
+#pragma unroll
+          for (int rt = 2 * rp; rt < 2 * rp + 2; ++rt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              __hip_atomic_fetch_add(&xacc[tile_row(rt, r) * 256 + (w + 4 * g) * 32 + 16 * sub + l16],
+                                     (double)accx[g][sub][rt][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            accx[g][sub][rt] = f4{0.f, 0.f, 0.f, 0.f};
+          }
+        }
     }
   };
 
-  // One operand set: the next step's rows are requested right after this step's
-  // products are issued, and have arrived long before the next barrier ends.
   auto step = [&](int s, Ops& cur) __attribute__((always_inline)) -> bool {
     lds_barrier();  // the recurrent waves' barrier of step s: dgl[s&1] is complete
     if (abort_flag) return false;
-    float a[2][2];  // [row tile][ks]
+    float a[4];  // [row tile]
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int rt = 0; rt < 4; ++rt) a[rt] = dgl[s & 1][kb][rt * 16 + l16];
+    if (!bok) {  // operand rows of absent batch slots are zero (their dgates are zero too)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) a[rt][ks] = dgl[s & 1][2 * ks + half][rt * 32 + l32];
+      for (int g = 0; g < HT; ++g) cur.h[g][0] = cur.h[g][1] = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      if (!bok[ks]) {  // operand rows of absent batch slots are zero (their dgates are zero too)
-#pragma unroll
-        for (int i = 0; i < HT; ++i) cur.h[i][ks] = 0.f;
-#pragma unroll
-        for (int i = 0; i < XA; ++i) cur.x[i][ks] = 0.f;
-      }
+      for (int g = 0; g < XA; ++g) cur.x[g][0] = cur.x[g][1] = 0.f;
     }
-    // one accumulator tile goes to the fp64 copy while the recurrent waves still issue
-    // their products (its last products were issued a step ago)
+    // one accumulator set goes to the fp64 copy while the recurrent waves still issue
+    // their products (its last products were issued a step ago); an fp32 run covers 4 XT
+    // steps
     if constexpr (XT > 0)
-      if (s > 0) fold_x((s - 1) % (2 * XT));
-    // wait until every recurrent wave has issued this step's products (bounded like
-    // every other wait of the persistent kernels)
+      if (s > 0) fold_x((s - 1) % (4 * XT));
     const long long t0 = wall_clock64();
     while (true) {
       lds_vint* const f = step_flags();
@@ -1450,22 +1456,22 @@ __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg
       __builtin_amdgcn_s_sleep(1);
     }
 #pragma unroll
-    for (int i = 0; i < HT; ++i) {
-      if (w + 4 * i >= nth) continue;
+    for (int g = 0; g < HT; ++g) {
+      if (w + 4 * g >= nth) continue;
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-          acch[i][rt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[rt][ks], cur.h[i][ks], acch[i][rt], 0, 0, 0);
+        for (int rt = 0; rt < 4; ++rt)
+          acch[g][sub][rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[rt], cur.h[g][sub], acch[g][sub][rt], 0, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < XT; ++i) {
-      if (w + 4 * i >= ntx) continue;
+    for (int g = 0; g < XT; ++g) {
+      if (w + 4 * g >= ntx) continue;
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-          accx[i][rt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[rt][ks], cur.x[i][ks], accx[i][rt], 0, 0, 0);
+        for (int rt = 0; rt < 4; ++rt)
+          accx[g][sub][rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[rt], cur.x[g][sub], accx[g][sub][rt], 0, 0, 0);
     }
     if (s + 1 < T) load_ops(T - 2 - s, cur);
     if (s % TS == TS - 1 || s == T - 1) dump_h(s / TS);
@@ -1482,16 +1488,19 @@ __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the wave's own LDS adds
     double* const plane = p.wpx + (size_t)grp * 4 * H * D;
 #pragma unroll
-    for (int i = 0; i < XT; ++i) {
-      const int c = (w + 4 * i) * 32 + l32;
-      if (w + 4 * i >= ntx) continue;
+    for (int g = 0; g < XT; ++g) {
+      if (w + 4 * g >= ntx) continue;
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int sub = 0; sub < 2; ++sub) {
+        const int c = (w + 4 * g) * 32 + 16 * sub + l16;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int r64 = tile_row(rt, r), u = wg * kUnits + (r64 & 15);
-          if (u < H && c < D) plane[((size_t)(r64 >> 4) * H + u) * D + c] = xacc[r64 * 256 + c];
-        }
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int r64 = tile_row(rt, r), u = wg * kUnits + (r64 & 15);
+            if (u < H && c < D) plane[((size_t)(r64 >> 4) * H + u) * D + c] = xacc[r64 * 256 + c];
+          }
+      }
     }
   }
 }

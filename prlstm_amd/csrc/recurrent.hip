@@ -1302,15 +1302,20 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
 // The wave takes part in every workgroup barrier of the recurrent waves (one per step)
 // and leaves when the group aborts, as they do.
 constexpr int kXaccLdsBytes = 64 * 256 * 8;  // fp64 dW_ih accumulator for D <= 256
+// 1: the weight-gradient waves run split bf16 products over 8-step windows
+// (rec_bwd_wgrad_win); 0: fp32 16x16x4 products every step (rec_bwd_wgrad)
+#ifndef HSL_WGRAD_WIN
+#define HSL_WGRAD_WIN 1
+#endif
+constexpr bool kWgradWin = HSL_WGRAD_WIN;
 
 // The products are v_mfma_f32_16x16x4_f32, one instruction per 16x16 tile and step (k =
 // the four batch slots): the matrix-core time of two 32x32x2 per 32x32 tile in
 // half-length instructions.  A second wave streaming 32x32x2 f32 products holds off the
 // recurrent wave on its SIMD about twice as long as one streaming 16x16x4 (a same-XCD
-// hand-off measured 1.52 against 0.89 us beside them, 0.42 us alone); 16-bit products
-// would not hold it off at all, but their four-step operand staging does not fit the
-// registers and LDS the two waves per SIMD leave.  Wave w owns the 32-column groups w,
-// w+4, ... of h and of x, each two 16-column tiles, and the four 16-row tiles.
+// hand-off measured 1.52 against 0.89 us beside them, 0.42 us alone).  Wave w owns the
+// 32-column groups w, w+4, ... of h and of x, each two 16-column tiles, and the four
+// 16-row tiles.  rec_bwd_wgrad_win below does the same sums on 16-bit products.
 template <int KQ, int XT>
 __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg, float (&dgl)[2][4][68],
                                                 double* xacc, int& abort_flag) {
@@ -1505,6 +1510,300 @@ __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg
   }
 }
 
+// Weight gradients on split bf16 products over windows of eight steps (the default;
+// HSL_WGRAD_WIN=0 at build time selects rec_bwd_wgrad).  v_mfma_f32_16x16x32_bf16 needs
+// a 32-deep k, here the 8 steps x 4 batch slots of a window: lane l holds k = 8 (l/16) + i
+// of its row (A) or column (B), i.e. batch slot l/16 and step i of the window, in both
+// operands.
+//  - A (dgates, 64 rows = four 16-row tiles): after the barrier of each step, wave w
+//    splits row tile w of the step's dgates (the recurrent waves' LDS copy) into three
+//    bf16 pieces and writes them into element i of the lanes' 16-byte operands in LDS
+//    (two window buffers, 24 KB).  Each wave reads a window's pieces into registers once,
+//    at the first slot that uses them.
+//  - B (h_{t-1} and x_t columns): read from memory a slot before the products that use
+//    them, eight values per lane and tile, split in registers (split8).
+//  - The products of window m run during the eight steps of window m+1 (slots), column
+//    tile c at slot c % 8 (one or two tiles per slot), once the recurrent waves have
+//    issued theirs.  The last window (and what a short last window leaves of the one
+//    before) runs in slots after the final barrier.
+//  - dW_hh_s accumulates in registers and goes out as an fp32 plane per chunk of TS
+//    steps (TS a multiple of 8); each dW_ih tile accumulates one window in registers and
+//    is then added to the fp64 LDS copy (ds_add_f64).
+// Six piece products per tile and window (split_bf16.h), smallest first.  Against the
+// fp32 16x16x4 stage the recurrent waves lose less time to the products (a 16-bit stream
+// holds off the other wave on the SIMD less than an fp32 one).  Returns true when the
+// wave has taken part in the workgroup's final barrier (always, except after an abort
+// inside the loop).
+constexpr int kWin = 8;
+constexpr unsigned kApieceBytes = 2u * 4u * 3u * 64u * 16u;  // [window parity][row tile][piece][lane]
+constexpr int kBwdXLdsBytes = kXaccLdsBytes + (int)kApieceBytes;
+constexpr int kBwdWgLdsBytes = kWgradWin ? kBwdXLdsBytes : kXaccLdsBytes;  // dynamic LDS with dW_ih fused
+static_assert(kApieceBytes <= (unsigned)kPadLdsBytes, "the A operands fit the padding LDS without dW_ih");
+
+__device__ __forceinline__ f4 mfma16_bf16(u32x4 a, u32x4 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+
+template <int J, int N, class F>
+__device__ __forceinline__ bool for_steps(F&& f) {
+  if constexpr (J == N) {
+    return true;
+  } else {
+    if (!f(std::integral_constant<int, J>{})) return false;
+    return for_steps<J + 1, N>(f);
+  }
+}
+
+template <int KQ, int XT>
+__device__ __forceinline__ bool rec_bwd_wgrad_win(const PBwdArgs& p, int grp, int wg, float (&dgl)[2][4][68],
+                                                  char* lds, int& abort_flag) {
+  constexpr int HT = KQ >= 32 ? KQ / 32 : 1;  // h column groups of 32 per wave (4*KQ >= H)
+  constexpr int NH = 2 * HT;                   // h column tiles per wave
+  constexpr int NX = XT > 0 ? 2 * XT : 0;      // x column tiles per wave
+  constexpr int C = NH + NX;
+  const int T = p.T, B = p.B, H = p.H, D = p.D, Bg = p.Bg, NG = p.NG, TS = p.TS;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) - 4);
+  const int kb = lane >> 4, l16 = lane & 15;  // batch slot of the lane's k values
+  const int cb = grp * Bg + kb;
+  const bool bok = kb < Bg && cb < B;
+  const int brow = bok ? cb : 0;
+  const int nth = (H + 31) / 32, ntx = (D + 31) / 32;
+  double* const xacc = reinterpret_cast<double*>(lds);
+  const unsigned abase = XT > 0 ? (unsigned)kXaccLdsBytes : 0u;
+  // the fields used inside the loop, as locals (the lambdas below capture these, not p)
+  const float* const h_save = p.h_save;
+  const float* const xin = p.x;
+  float* const wph = p.wph;
+  const long long spin = p.spin;
+  int* const err = p.err;
+
+  // The lane's index as a value the compiler cannot see through: addresses derived from
+  // it inside the loop are recomputed where they are used instead of being kept in
+  // registers for the whole loop (which the 128 dW_hh accumulators do not leave room for).
+  auto opaque_lane = [&]() {
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    return l;
+  };
+  // column tile c: h tiles (group c/2, half c%2) then x tiles
+  auto tile_g = [](int c) { return c < NH ? c / 2 : (c - NH) / 2; };
+  auto tile_sub = [](int c) { return c < NH ? c % 2 : (c - NH) % 2; };
+  auto tile_on = [&](int c) { return w + 4 * tile_g(c) < (c < NH ? nth : ntx); };  // wave-uniform
+  auto tile_col = [&](int c) { return (w + 4 * tile_g(c)) * 32 + 16 * tile_sub(c) + l16; };
+
+  f4 acch[HT][2][4];  // [column group][half][row tile]
+  auto zero_h = [&]() {
+#pragma unroll
+    for (int g = 0; g < HT; ++g)
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) acch[g][sub][rt] = f4{0.f, 0.f, 0.f, 0.f};
+  };
+  zero_h();
+  // D-layout of a 16x16 tile: lane l, register r -> row 4(l/16) + r, column l%16
+  auto tile_row = [&](int rt, int r) { return rt * 16 + 4 * kb + r; };
+  if constexpr (XT > 0) {
+#pragma unroll
+    for (int c = NH; c < C; ++c) {
+      if (!tile_on(c)) continue;
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xacc[tile_row(rt, r) * 256 + tile_col(c)] = 0.0;
+    }
+  }
+
+  // B of tile c for the eight steps of window win (clamped rows past T; zeroed at use).
+  // No branch around the loads (a tile that is off loads clamped addresses it never
+  // uses): the waits before the products count outstanding loads exactly only when every
+  // path issues the same loads.
+  auto load_b = [&](int c, int win, float (&v)[kWin]) {
+    const int ol = opaque_lane();
+    const int cl = (w + 4 * tile_g(c)) * 32 + 16 * tile_sub(c) + (ol & 15);
+    const int col = c < NH ? min(cl, H - 1) : min(cl, D - 1);
+    const int okb = ol >> 4;
+    const int orow = okb < Bg && grp * Bg + okb < B ? grp * Bg + okb : 0;
+#pragma unroll
+    for (int i = 0; i < kWin; ++i) {
+      const int s = kWin * win + i;
+      const int t = s < T ? T - 1 - s : 0;
+      if (c < NH)
+        v[i] = *byte_at(h_save + (size_t)t * B * H, 4u * (unsigned)(orow * H + col));
+      else
+        v[i] = *byte_at(xin + (size_t)t * B * D, 4u * (unsigned)(orow * D + col));
+    }
+  };
+  // the A pieces of window win's four row tiles
+  auto read_a = [&](int win, u32x4 (&a)[4][3]) {
+    const char* const ab = lds + abase + (unsigned)(win & 1) * (4u * 3u * 1024u) + 16u * opaque_lane();
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int pc = 0; pc < 3; ++pc) a[rt][pc] = *reinterpret_cast<const u32x4*>(ab + (rt * 3 + pc) * 1024);
+  };
+  // the products of tile c for window win; steps i >= nvalid of the window do not exist
+  auto products = [&](int c, int win, const float (&v)[kWin], int nvalid, const u32x4 (&a)[4][3]) {
+    if (!tile_on(c)) return;
+    float vv[kWin];
+#pragma unroll
+    for (int i = 0; i < kWin; ++i) vv[i] = (bok && i < nvalid) ? v[i] : 0.f;
+    u32x4 bp[3];
+    split8(vv, bp);
+    const int ol = opaque_lane();
+    const int g = tile_g(c), sub = tile_sub(c);
+    f4 xa[4] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+    // piece product i of the four row tiles in turn: four independent accumulators
+    // between dependent products
+#pragma unroll
+    for (int i = 5; i >= 0; --i)
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        if (c < NH)
+          acch[g][sub][rt] = mfma16_bf16(a[rt][kPa[i]], bp[kPb[i]], acch[g][sub][rt]);
+        else
+          xa[rt] = mfma16_bf16(a[rt][kPa[i]], bp[kPb[i]], xa[rt]);
+      }
+    if (c >= NH) {  // the window's dW_ih tile into the fp64 copy
+      double* const xl = xacc + (4 * (ol >> 4)) * 256 + (w + 4 * g) * 32 + 16 * sub + (ol & 15);
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          __hip_atomic_fetch_add(xl + (rt * 16 + r) * 256, (double)xa[rt][r], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  };
+  // Row r64 = rt*16 + 4*kb + r of a tile is gate rt, unit wg*16 + 4*kb + r.
+  // (addresses from opaque_lane: the several call sites share no address registers)
+  auto dump_h = [&](int chunk) {
+    __builtin_amdgcn_sched_barrier(0);
+    float* const plane = wph + ((size_t)chunk * NG + grp) * 4 * H * H;
+    const int ol = opaque_lane();
+    const int ul = wg * kUnits + 4 * (ol >> 4);
+#pragma unroll
+    for (int g = 0; g < HT; ++g) {
+      if (w + 4 * g >= nth) continue;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        const int c = (w + 4 * g) * 32 + 16 * sub + (ol & 15);
+        const unsigned lo = 4u * ((unsigned)ul * H + c);
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float* const rb = plane + (size_t)(rt * H + r) * H;
+            if (ul + r < H && c < H) *byte_at(rb, lo) = acch[g][sub][rt][r];
+          }
+      }
+    }
+    zero_h();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // element j of the lanes' A operands of row tile w in window buffer m&1: the three pieces
+  // of v
+  auto put_pieces = [&](int m, int j, float v) {
+    const __bf16 p0 = (__bf16)v;
+    const float r1 = v - (float)p0;
+    const __bf16 p1 = (__bf16)r1;
+    const __bf16 p2 = (__bf16)(r1 - (float)p1);
+    char* const dst =
+        lds + abase + (unsigned)(m & 1) * (4u * 3u * 1024u) + (unsigned)w * 3072u + 16u * opaque_lane() + 2u * j;
+    *reinterpret_cast<__bf16*>(dst) = p0;
+    *reinterpret_cast<__bf16*>(dst + 1024) = p1;
+    *reinterpret_cast<__bf16*>(dst + 2048) = p2;
+  };
+
+  // Slot (m, j), m = 0..M (M windows): step s = 8m + j when s < T, and runs tiles j and
+  // j + 8 of window m-1.  Slots with s >= T come after the loop's last step: the first
+  // of them (s == T) zeroes the A elements of the missing steps of the last window and
+  // takes part in the final barrier, and they run the rest of the products without
+  // waiting for anything.
+  const int M = (T + kWin - 1) / kWin;
+  const int last = M - 1, nvalid = T - kWin * last;  // steps of the last window
+  float nb[2][kWin];  // B of the next slot's tiles (j and j + 8)
+  u32x4 apc[4][3];    // A pieces of the window whose products the slots run
+  bool final_done = false;
+  auto slot = [&](int m, auto jc) __attribute__((always_inline)) -> bool {
+    constexpr int j = decltype(jc)::value;
+    const int s = kWin * m + j;
+    __builtin_amdgcn_sched_barrier(0);  // nothing of another slot moves into this one
+    if (s < T) {
+      lds_barrier();  // the recurrent waves' barrier of step s: dgl[s&1] is complete
+      if (abort_flag) return false;
+      {
+        const int ol = opaque_lane();
+        put_pieces(m, j, dgl[s & 1][ol >> 4][w * 16 + (ol & 15)]);
+      }
+      // the window's A pieces, once per window (they serve its eight slots); the reads
+      // complete while the recurrent waves issue their products
+      if constexpr (j == 0) read_a(max(m - 1, 0), apc);
+      const long long t0 = wall_clock64();
+      while (true) {
+        lds_vint* const f = step_flags();
+        const int m0 = f[0], m1 = f[1], m2 = f[2], m3 = f[3];
+        if (min(min(m0, m1), min(m2, m3)) > s) break;
+        if (abort_flag) return false;
+        if (wall_clock64() - t0 > spin) {
+          raise_abort(&abort_flag, err);
+          return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    } else {
+      if (s == T) {
+        for (int jj = nvalid; jj < kWin; ++jj) put_pieces(last, jj, 0.f);
+        lds_barrier();  // the workgroup's final barrier (the recurrent waves' last one)
+        final_done = true;
+        if (abort_flag) return false;
+      }
+      if (j == 0 || s == T) read_a(max(m - 1, 0), apc);
+    }
+    if (m > 0) {  // window m-1's tiles j and j + 8
+      const int nv = m - 1 == last ? nvalid : kWin;
+      if constexpr (j < C) products(j, m - 1, nb[0], nv, apc);
+      if constexpr (j + kWin < C) products(j + kWin, m - 1, nb[1], nv, apc);
+      if constexpr (j == kWin - 1)
+        if (m == M || (kWin * m) % TS == 0) dump_h(kWin * (m - 1) / TS);
+    }
+    {  // B of the next slot's tiles: window m-1, or window m after j = 7 (clamped: a
+       // slot without products loads window 0 or M-1 and does not use it)
+      constexpr int jn = (j + 1) % kWin;
+      const int wn = min(max(j + 1 < kWin ? m - 1 : m, 0), M - 1);
+      if constexpr (jn < C) load_b(jn, wn, nb[0]);
+      if constexpr (jn + kWin < C) load_b(jn + kWin, wn, nb[1]);
+      // the loads stay here, a slot ahead of their use: without this the compiler sinks
+      // them past the next barrier to the products, and each slot waits for memory twice
+      asm volatile("" ::: "memory");
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    return true;
+  };
+  for (int m = 0; m <= M; ++m)
+    if (!for_steps<0, kWin>([&](auto jc) { return slot(m, jc); })) return final_done;
+
+  if constexpr (XT > 0) {  // this group's dW_ih rows as an fp64 plane
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the wave's own LDS adds
+    double* const plane = p.wpx + (size_t)grp * 4 * H * D;
+#pragma unroll
+    for (int c = NH; c < C; ++c) {
+      if (!tile_on(c)) continue;
+      const int col = tile_col(c);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int r64 = tile_row(rt, r), u = wg * kUnits + (r64 & 15);
+          if (u < H && col < D) plane[((size_t)(r64 >> 4) * H + u) * D + col] = xacc[r64 * 256 + col];
+        }
+    }
+  }
+  return true;
+}
+
 // After an abort, a recurrent wave sets what its cell lanes own to NaN: dh0/dc0, the
 // bias partials and (when they are stored) the dgates of its batch slot and the
 // workgroup's units.
@@ -1568,11 +1867,18 @@ __global__ __launch_bounds__(XT >= 0 ? 512 : 256, 1) void rec_bwd_persistent(PBw
   const bool fast = agree_placement(p.hello + (size_t)grp * NWMAX, wg, p.NW, p.spin, &abort_flag, p.err) &&
                     !p.device_scope;
   const bool wgrad_wave = GW && threadIdx.x >= 256;
+  bool passed_final = false;  // the wave has taken part in the final barrier below
   if (!abort_flag) {
     if constexpr (GW) {
       if (wgrad_wave) {
-        extern __shared__ double xacc[];  // [64][256] fp64 dW_ih accumulator (dynamic LDS)
-        rec_bwd_wgrad<KQ, (XT > 0 ? XT : 0)>(p, grp, wg, dgl, xacc, abort_flag);
+        // [64][256] fp64 dW_ih accumulator (XT > 0), then the bf16 A operands of two
+        // windows (dynamic LDS)
+        extern __shared__ double xacc[];
+        if constexpr (kWgradWin)
+          passed_final =
+              rec_bwd_wgrad_win<KQ, (XT > 0 ? XT : 0)>(p, grp, wg, dgl, reinterpret_cast<char*>(xacc), abort_flag);
+        else
+          rec_bwd_wgrad<KQ, (XT > 0 ? XT : 0)>(p, grp, wg, dgl, xacc, abort_flag);
       } else {
         __builtin_amdgcn_s_setprio(2);  // the recurrent chain first when both waves can issue
       }
@@ -1584,7 +1890,7 @@ __global__ __launch_bounds__(XT >= 0 ? 512 : 256, 1) void rec_bwd_persistent(PBw
         rec_bwd_body<KQ, false, GW>(p, grp, wg, dgl, abort_flag);
     }
   }
-  lds_barrier();
+  if (!passed_final) lds_barrier();
   if (abort_flag) {
     if constexpr (GW) {
       if (wgrad_wave) {
@@ -1659,7 +1965,7 @@ int bwd_resident(int xt, int* occ) {
     case 0: return max_resident(rec_bwd_persistent<KQ, 0>, 512, occ);
     default: {
       int o = 0;
-      HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, rec_bwd_persistent<KQ, 2>, 512, kXaccLdsBytes));
+      HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, rec_bwd_persistent<KQ, 2>, 512, kBwdWgLdsBytes));
       *occ = o;
       return HSL_OK;
     }
@@ -1977,7 +2283,7 @@ void launch_bwd_persistent(const PBwdArgs& a, int grid, int xt, hipStream_t s) {
   switch (xt) {
     case -1: hipLaunchKernelGGL((rec_bwd_persistent<KQ, -1>), dim3(grid), dim3(256), kPadLdsBytes, s, a); break;
     case 0: hipLaunchKernelGGL((rec_bwd_persistent<KQ, 0>), dim3(grid), dim3(512), kPadLdsBytes, s, a); break;
-    default: hipLaunchKernelGGL((rec_bwd_persistent<KQ, 2>), dim3(grid), dim3(512), kXaccLdsBytes, s, a); break;
+    default: hipLaunchKernelGGL((rec_bwd_persistent<KQ, 2>), dim3(grid), dim3(512), kBwdWgLdsBytes, s, a); break;
   }
 }
 
@@ -2250,7 +2556,7 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
   double* wpx = nullptr;
   if (fused) {
     const int nch = wgrad_chunks(T);
-    wts = (T + nch - 1) / nch;
+    wts = ((T + nch - 1) / nch + 7) / 8 * 8;  // whole 8-step windows per plane
     nsplit = (T + wts - 1) / wts * pl.NG;
     wpx = reinterpret_cast<double*>(wph + (size_t)nsplit * 4 * H * H);
   }

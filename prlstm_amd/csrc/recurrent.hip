@@ -50,19 +50,18 @@ __global__ void fill_u64_kernel(unsigned long long* p, size_t n, unsigned long l
     p[i] = v;
 }
 
-// Fills three word ranges in one launch (error flag, hand-off slots, placement words).
+// Fills three word ranges in one launch (error flag, hand-off slots, placement words);
+// the slots, the bulk, with 16-byte stores when they are 16-byte aligned.
 __global__ void fill3_u64_kernel(unsigned long long* a, size_t na, unsigned long long va, unsigned long long* b,
                                  size_t nb, unsigned long long vb, unsigned long long* c, size_t nc,
                                  unsigned long long vc) {
-  const size_t n = na + nb + nc;
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-    if (i < na)
-      a[i] = va;
-    else if (i < na + nb)
-      b[i - na] = vb;
-    else
-      c[i - na - nb] = vc;
-  }
+  const size_t tid = blockIdx.x * (size_t)blockDim.x + threadIdx.x, nth = (size_t)gridDim.x * blockDim.x;
+  const size_t n16 = reinterpret_cast<uintptr_t>(b) % 16 == 0 ? nb / 2 : 0;
+  ulonglong2* const b2 = reinterpret_cast<ulonglong2*>(b);
+  for (size_t i = tid; i < n16; i += nth) b2[i] = make_ulonglong2(vb, vb);
+  for (size_t i = 2 * n16 + tid; i < nb; i += nth) b[i] = vb;
+  for (size_t i = tid; i < na; i += nth) a[i] = va;
+  for (size_t i = tid; i < nc; i += nth) c[i] = vc;
 }
 
 __global__ void copy_f32_kernel(float* dst, const float* src, size_t n) {
@@ -99,13 +98,13 @@ __global__ void colsum_time_kernel(const float* __restrict__ dg, double* __restr
 }
 
 // dW_hh_s = sum of split-K partials (fp64); dW_hh = a * dW_hh_s; rowdot[n] = sum_k W_hh[n][k] dW_hh_s[n][k].
-// Blocks past the 4H rows (when X is non-null) add the fp64 dW_ih planes X[xplanes][xn]
+// Blocks past the 4H rows (when X is non-null) add the dW_ih planes X[xplanes][xn] in fp64
 // of the fused backward into dw_ih, in the same launch.
 __global__ __launch_bounds__(256) void whh_grad_finalize_kernel(const float* __restrict__ P, int splits,
                                                                 const float* __restrict__ w_hh,
                                                                 const float* __restrict__ a, float* __restrict__ dw_hh,
                                                                 double* __restrict__ rowdot, int H,
-                                                                const double* __restrict__ X, int xplanes,
+                                                                const float* __restrict__ X, int xplanes,
                                                                 float* __restrict__ dw_ih, size_t xn) {
   __shared__ double red[256];
   const int n = blockIdx.x;
@@ -114,7 +113,7 @@ __global__ __launch_bounds__(256) void whh_grad_finalize_kernel(const float* __r
     for (size_t e = (size_t)(n - 4 * H) * blockDim.x + threadIdx.x; e < xn; e += nb * blockDim.x) {
       double v = 0.0;
 #pragma unroll 4
-      for (int z = 0; z < xplanes; ++z) v += X[(size_t)z * xn + e];
+      for (int z = 0; z < xplanes; ++z) v += (double)X[(size_t)z * xn + e];
       dw_ih[e] = (float)v;
     }
     return;
@@ -1064,7 +1063,7 @@ struct PBwdArgs {
   const float* h_save;  // [T+1][B][H]
   const float* x;       // [T][B][D]
   float* wph;           // [chunks*NG][4H][H] fp32
-  double* wpx;          // [NG][4H][D] fp64 (when dW_ih is fused)
+  float* wpx;           // [NG][4H][D] (when dW_ih is fused): each group's fp64 sums rounded once
   int D, TS;
   int store_dg;  // 0: dgates are not needed after the kernel (not written)
 };
@@ -1293,8 +1292,8 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
 //
 // Accuracy: no fp32 running sum spans more than a few hundred products.  dW_hh_s is
 // written as an fp32 partial plane every TS steps (its gradient dW_hh = a dW_hh_s is
-// a-scaled); dW_ih goes into an fp64 accumulator in LDS (64 rows x D, written once as
-// an fp64 plane per group): at the start of each step one of the wave's 4*XT
+// a-scaled); dW_ih goes into an fp64 accumulator in LDS (64 rows x D, written once per
+// group as a plane, rounded to fp32 once): at the start of each step one of the wave's 4*XT
 // accumulator sets (two 16x16 tiles) is added to it with ds_add_f64 (no returned value)
 // and restarted, so an fp32 run covers 4*XT steps.  The planes are summed in fp64
 // afterwards.
@@ -1488,10 +1487,10 @@ __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg
   for (int s = 0; s < T; ++s)
     if (!step(s, op)) return;
 
-  if constexpr (XT > 0) {  // this group's dW_ih rows as an fp64 plane
+  if constexpr (XT > 0) {  // this group's dW_ih rows (fp64 sums, rounded once) as a plane
     fold_x(-1);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the wave's own LDS adds
-    double* const plane = p.wpx + (size_t)grp * 4 * H * D;
+    float* const plane = p.wpx + (size_t)grp * 4 * H * D;
 #pragma unroll
     for (int g = 0; g < XT; ++g) {
       if (w + 4 * g >= ntx) continue;
@@ -1503,7 +1502,7 @@ __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int r64 = tile_row(rt, r), u = wg * kUnits + (r64 & 15);
-            if (u < H && c < D) plane[((size_t)(r64 >> 4) * H + u) * D + c] = xacc[r64 * 256 + c];
+            if (u < H && c < D) plane[((size_t)(r64 >> 4) * H + u) * D + c] = (float)xacc[r64 * 256 + c];
           }
       }
     }
@@ -1784,9 +1783,9 @@ __device__ __forceinline__ bool rec_bwd_wgrad_win(const PBwdArgs& p, int grp, in
   for (int m = 0; m <= M; ++m)
     if (!for_steps<0, kWin>([&](auto jc) { return slot(m, jc); })) return final_done;
 
-  if constexpr (XT > 0) {  // this group's dW_ih rows as an fp64 plane
+  if constexpr (XT > 0) {  // this group's dW_ih rows (fp64 sums, rounded once) as a plane
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the wave's own LDS adds
-    double* const plane = p.wpx + (size_t)grp * 4 * H * D;
+    float* const plane = p.wpx + (size_t)grp * 4 * H * D;
 #pragma unroll
     for (int c = NH; c < C; ++c) {
       if (!tile_on(c)) continue;
@@ -1797,7 +1796,7 @@ __device__ __forceinline__ bool rec_bwd_wgrad_win(const PBwdArgs& p, int grp, in
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int r64 = tile_row(rt, r), u = wg * kUnits + (r64 & 15);
-          if (u < H && col < D) plane[((size_t)(r64 >> 4) * H + u) * D + col] = xacc[r64 * 256 + col];
+          if (u < H && col < D) plane[((size_t)(r64 >> 4) * H + u) * D + col] = (float)xacc[r64 * 256 + col];
         }
     }
   }
@@ -1824,7 +1823,7 @@ __device__ void poison_bwd(const PBwdArgs& p, int grp, int wg) {
 
 // ... and a weight-gradient wave sets every element of the planes it writes to NaN: its
 // 32-column tiles of the workgroup's 64 rows in the group's dW_hh_s plane of every chunk
-// and, with XT > 0, in the group's fp64 dW_ih plane.
+// and, with XT > 0, in the group's dW_ih plane.
 template <int KQ, int XT>
 __device__ void poison_wgrad(const PBwdArgs& p, int grp, int wg) {
   constexpr int HT = KQ >= 32 ? KQ / 32 : 1;
@@ -1844,7 +1843,7 @@ __device__ void poison_wgrad(const PBwdArgs& p, int grp, int wg) {
     if constexpr (XT > 0) {
       for (int i = 0; i < XT; ++i) {
         const int c = (w + 4 * i) * 32 + (lane & 31);
-        if (c < D) p.wpx[((size_t)grp * 4 * H + row) * D + c] = (double)nan;
+        if (c < D) p.wpx[((size_t)grp * 4 * H + row) * D + c] = nan;
       }
     }
   }
@@ -2052,11 +2051,13 @@ int plan_wide(int B, int H, bool bwd, WidePlan* pl) {
   return HSL_OK;
 }
 
-// Steps per fp32 partial plane of the fused weight gradients: at most 128 steps
-// (512 products per running sum at four batch slots) while there are at most 8 planes
-// per group.
+// Chunks of the fused weight gradients' fp32 partial planes (at most 8 per group).  A
+// chunk spans at most 256 steps with the window products (each running sum takes six
+// 32-term products per 8-step window, 192 additions per chunk) and at most 128 steps with
+// the fp32 products (512 single products per running sum).
 int wgrad_chunks(int T) {
-  const int c = (T + 127) / 128;
+  const int span = kWgradWin ? 256 : 128;
+  const int c = (T + span - 1) / span;
   return c < 1 ? 1 : (c > 8 ? 8 : c);
 }
 
@@ -2095,7 +2096,7 @@ int fill_words(unsigned long long* p, size_t n, unsigned long long v, hipStream_
 int prepare_persistent(int* err, float* slots, size_t slot_floats, unsigned long long* hello, size_t hwords,
                        hipStream_t s) {
   const size_t n1 = 32, n2 = (slot_floats + 1) / 2;
-  hipLaunchKernelGGL(fill3_u64_kernel, dim3(grid_for(n1 + n2 + hwords)), dim3(256), 0, s,
+  hipLaunchKernelGGL(fill3_u64_kernel, dim3(grid_for(n1 + (n2 + 1) / 2 + hwords)), dim3(256), 0, s,
                      reinterpret_cast<unsigned long long*>(err), n1, 0ull,
                      reinterpret_cast<unsigned long long*>(slots), n2, kEmpty2, hello, hwords, 0ull);
   HSL_HIP(hipGetLastError());
@@ -2205,7 +2206,7 @@ size_t gemm_region_bytes(int T, int B, int D, int H) {
   if (pick_kq(H) && fused_wgrad_enabled()) {  // planes of the fused weight gradients
     const size_t ng = (B + 3) / 4;
     const size_t wg = sizeof(float) * wgrad_chunks(T) * ng * 4 * H * H +
-                      (D <= 256 ? sizeof(double) * ng * 4 * H * D : 0);
+                      (D <= 256 ? sizeof(float) * ng * 4 * H * D : 0);
     if (wg > need) need = wg;
   }
   return need;
@@ -2553,12 +2554,12 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
   const bool fused_ih = fused && pl.XT > 0;
   int wts = T, nsplit = 0;
   float* const wph = w.gemm;
-  double* wpx = nullptr;
+  float* wpx = nullptr;
   if (fused) {
     const int nch = wgrad_chunks(T);
     wts = ((T + nch - 1) / nch + 7) / 8 * 8;  // whole 8-step windows per plane
     nsplit = (T + wts - 1) / wts * pl.NG;
-    wpx = reinterpret_cast<double*>(wph + (size_t)nsplit * 4 * H * H);
+    wpx = wph + (size_t)nsplit * 4 * H * H;
   }
   if (pl.ok)
     HSL_CHECK(prepare_persistent(w.err, w.pbuf, w.pfloats, w.hello, w.hwords, s));
@@ -2657,7 +2658,7 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     const size_t xn = fused_ih ? (size_t)4 * H * D : 0;
     const int xblocks = fused_ih ? grid_for(xn) : 0;
     hipLaunchKernelGGL(whh_grad_finalize_kernel, dim3(4 * H + xblocks), dim3(256), 0, s, wph, splits, w_hh, a,
-                       dw_hh, w.rowdot, H, (const double*)wpx, pl.NG, dw_ih, xn);
+                       dw_hh, w.rowdot, H, (const float*)wpx, pl.NG, dw_ih, xn);
     HSL_HIP(hipGetLastError());
   }
   HSL_CHECK(bias_grads_from_parts(w.db_part, B, w.rowdot, b_hh, a, db_ih, db_hh, da, H, s));

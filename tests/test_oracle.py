@@ -18,6 +18,9 @@ formula:
 * parallel_forward     -- a=0 equivalence with the recurrent path
                           (test_parallel.py:47-60, :84-122) and the divergence
                           sweep (test_parallel.py:63-81); its backward by gradcheck.
+* RefHeadStartLSTM     -- batch_first and hx plumbing against batch rows run one
+                          at a time (B=1, time-major, (B,H) state): no transpose
+                          shared with the code under test.
 * The last test plants mistakes in copies of the oracle and checks that the
   pins above catch them.
 """
@@ -278,6 +281,33 @@ def test_parallel_gradcheck():
 
 
 # ---------------------------------------------------------------------------
+@pytest.mark.parametrize("parallel", [False, True])
+def test_module_batch_first_and_hx_against_single_rows(parallel):
+    """batch_first / hx handling of RefHeadStartLSTM (__init__.py:169-233 of the reference):
+    each batch row run alone through the time-major path with a (B,H) = (1,H) state gives
+    that row of the batch_first output and of h_n / c_n ((1,B,H))."""
+    T, B, D, H = 5, 3, 4, 6
+    m = _model(D, H, seed=3, a=0.3 if not parallel else 0.0, parallel=parallel)
+    mb = _model(D, H, seed=3, a=0.3 if not parallel else 0.0, parallel=parallel)
+    mb.batch_first = True
+    g = torch.Generator().manual_seed(7)
+    xb = torch.randn(B, T, D, generator=g, dtype=torch.float64)
+    h0 = torch.randn(1, B, H, generator=g, dtype=torch.float64) * 0.5
+    c0 = torch.rand(1, B, H, generator=g, dtype=torch.float64) + 0.1
+    out, (hn, cn) = mb(xb, (h0, c0))
+    assert out.shape == (B, T, H) and hn.shape == (1, B, H) and cn.shape == (1, B, H)
+    for b in range(B):
+        xr = torch.stack([xb[b, t] for t in range(T)]).unsqueeze(1)  # [T, 1, D]
+        o1, (h1, c1) = m(xr, (h0[0, b:b + 1], c0[0, b:b + 1]))
+        assert torch.allclose(out[b], o1[:, 0], rtol=0, atol=1e-13)
+        assert torch.allclose(hn[0, b], h1[0, 0], rtol=0, atol=1e-13)
+        assert torch.allclose(cn[0, b], c1[0, 0], rtol=0, atol=1e-13)
+    # hx=None is the zero state
+    o0, _ = mb(xb)
+    oz, _ = mb(xb, (torch.zeros(1, B, H, dtype=torch.float64), torch.zeros(1, B, H, dtype=torch.float64)))
+    assert torch.equal(o0, oz)
+
+
 def test_pins_detect_planted_mistakes(monkeypatch):
     """Each plausible slip in the oracle is caught by one of the pins above."""
     good_bwd = O.cell_backward

@@ -71,7 +71,9 @@ int hsl_set_exchange_scope(int mode);
  *  - C = A^T B and C = A B of at least 8 GFLOP with M >= 256, N >= 128: the weight
  *    gradients and dx (_torch.py:157-162), as fp32 runs of 64 k folded into a second
  *    fp32 sum, split along K into planes of at most 2048 k added in fp64 (workspace
- *    permitting; otherwise the fp32 kernel runs).
+ *    permitting; otherwise the fp32 kernel runs);
+ *  - the products the persistent recurrent kernels fuse (H <= 512): the forward's input
+ *    projection and the backward's weight gradients (k = 8 steps x 4 batch rows).
  * on = 0 uses the fp32 MFMA instruction for every product.  With
  * on = 1 a non-finite element of A (or one beyond the bf16 range, 3.3895e38) makes
  * its row of C NaN and one of B its column, where the fp32 instruction would give

@@ -103,7 +103,7 @@ def set_recurrent_path(mode):
 
 
 def set_split_products(on):
-    """Large ``A B^T`` products (the input projection) on split-bf16 MFMA (1, default)
+    """Large products and the persistent kernels' fused ones on split-bf16 MFMA (1, default)
     or on the fp32 instruction (0); returns the previous setting."""
     return load().hsl_set_split_products(1 if on else 0)
 

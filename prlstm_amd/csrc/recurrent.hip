@@ -1325,12 +1325,6 @@ __device__ __forceinline__ void rec_bwd_body(const PBwdArgs& p, int grp, int wg,
 // The wave takes part in every workgroup barrier of the recurrent waves (one per step)
 // and leaves when the group aborts, as they do.
 constexpr int kXaccLdsBytes = 64 * 256 * 8;  // fp64 dW_ih accumulator for D <= 256
-// 1: the weight-gradient waves run split bf16 products over 8-step windows
-// (rec_bwd_wgrad_win); 0: fp32 16x16x4 products every step (rec_bwd_wgrad)
-#ifndef HSL_WGRAD_WIN
-#define HSL_WGRAD_WIN 1
-#endif
-constexpr bool kWgradWin = HSL_WGRAD_WIN;
 
 // The products are v_mfma_f32_16x16x4_f32, one instruction per 16x16 tile and step (k =
 // the four batch slots): the matrix-core time of two 32x32x2 per 32x32 tile in
@@ -1534,7 +1528,7 @@ __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg
 }
 
 // Weight gradients on split bf16 products over windows of eight steps (the default;
-// HSL_WGRAD_WIN=0 at build time selects rec_bwd_wgrad).  v_mfma_f32_16x16x32_bf16 needs
+// hsl_set_split_products(0) selects rec_bwd_wgrad).  v_mfma_f32_16x16x32_bf16 needs
 // a 32-deep k, here the 8 steps x 4 batch slots of a window: lane l holds k = 8 (l/16) + i
 // of its row (A) or column (B), i.e. batch slot l/16 and step i of the window, in both
 // operands.
@@ -1560,7 +1554,11 @@ __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg
 constexpr int kWin = 8;
 constexpr unsigned kApieceBytes = 2u * 4u * 3u * 64u * 16u;  // [window parity][row tile][piece][lane]
 constexpr int kBwdXLdsBytes = kXaccLdsBytes + (int)kApieceBytes;
-constexpr int kBwdWgLdsBytes = kWgradWin ? kBwdXLdsBytes : kXaccLdsBytes;  // dynamic LDS with dW_ih fused
+// dynamic LDS of a backward with weight-gradient waves (XT >= 0), products on split bf16
+// pieces (WS) or on the fp32 instruction
+constexpr int bwd_lds_bytes(int xt, bool ws) {
+  return xt > 0 ? (ws ? kBwdXLdsBytes : kXaccLdsBytes) : kPadLdsBytes;
+}
 static_assert(kApieceBytes <= (unsigned)kPadLdsBytes, "the A operands fit the padding LDS without dW_ih");
 
 __device__ __forceinline__ f4 mfma16_bf16(u32x4 a, u32x4 b, f4 c) {
@@ -1874,10 +1872,12 @@ __device__ void poison_wgrad(const PBwdArgs& p, int grp, int wg) {
 }
 
 // XT < 0: 256 threads, recurrent waves only (weight gradients by separate GEMMs).
-// XT >= 0: 512 threads; waves 4-7 accumulate dW_hh_s and, when XT > 0, dW_ih.
+// XT >= 0: 512 threads; waves 4-7 accumulate dW_hh_s and, when XT > 0, dW_ih, on split
+// bf16 products (WS, rec_bwd_wgrad_win) or on the fp32 instruction (rec_bwd_wgrad), as
+// hsl_set_split_products selects.
 // As in the forward, every wave ends with one more workgroup barrier and then poisons
 // its outputs if any wave of the workgroup gave up a wait.
-template <int KQ, int XT>
+template <int KQ, int XT, bool WS>
 __global__ __launch_bounds__(XT >= 0 ? 512 : 256, 1) void rec_bwd_persistent(PBwdArgs p) {
   constexpr int NWMAX = 4 * KQ / kUnits;
   constexpr bool GW = XT >= 0;
@@ -1897,7 +1897,7 @@ __global__ __launch_bounds__(XT >= 0 ? 512 : 256, 1) void rec_bwd_persistent(PBw
         // [64][256] fp64 dW_ih accumulator (XT > 0), then the bf16 A operands of two
         // windows (dynamic LDS)
         extern __shared__ double xacc[];
-        if constexpr (kWgradWin)
+        if constexpr (WS)
           passed_final =
               rec_bwd_wgrad_win<KQ, (XT > 0 ? XT : 0)>(p, grp, wg, dgl, reinterpret_cast<char*>(xacc), abort_flag);
         else
@@ -1936,6 +1936,7 @@ struct PersistentPlan {
   int XT = -1;  // backward: -1 no weight-gradient waves, 0 dW_hh only, 2 dW_hh and dW_ih
   bool XP = false;  // forward: input projection inside the kernel (512 threads)
   bool XS = false;  // with XP: its products on split bf16 pieces
+  bool WS = true;   // backward with XT >= 0: weight-gradient products on split bf16 pieces
 };
 
 int pick_kq(int H) {
@@ -1981,18 +1982,29 @@ int fwd_resident(int xp, int* occ) {
   }
 }
 
-template <int KQ>
-int bwd_resident(int xt, int* occ) {
+template <int KQ, bool WS>
+int bwd_resident_ws(int xt, int* occ) {
+  int o = 0;
   switch (xt) {
-    case -1: return max_resident(rec_bwd_persistent<KQ, -1>, 256, occ);
-    case 0: return max_resident(rec_bwd_persistent<KQ, 0>, 512, occ);
-    default: {
-      int o = 0;
-      HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, rec_bwd_persistent<KQ, 2>, 512, kBwdWgLdsBytes));
-      *occ = o;
-      return HSL_OK;
-    }
+    case -1:
+      HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, rec_bwd_persistent<KQ, -1, true>, 256,
+                                                           bwd_lds_bytes(-1, true)));
+      break;
+    case 0:
+      HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, rec_bwd_persistent<KQ, 0, WS>, 512,
+                                                           bwd_lds_bytes(0, WS)));
+      break;
+    default:
+      HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, rec_bwd_persistent<KQ, 2, WS>, 512,
+                                                           bwd_lds_bytes(2, WS)));
+      break;
   }
+  *occ = o;
+  return HSL_OK;
+}
+template <int KQ>
+int bwd_resident(int xt, bool ws, int* occ) {
+  return ws ? bwd_resident_ws<KQ, true>(xt, occ) : bwd_resident_ws<KQ, false>(xt, occ);
 }
 
 int plan_persistent(int B, int H, int D, bool bwd, PersistentPlan* pl) {
@@ -2019,14 +2031,15 @@ int plan_persistent(int B, int H, int D, bool bwd, PersistentPlan* pl) {
   // x rows with 16-byte loads
   if (!bwd && fused_xproj_enabled()) p.XP = D > 0 && D <= 256 && D % 4 == 0;
   p.XS = kXprojSplit && split_products_mode();
+  p.WS = split_products_mode() != 0;
   int occ = 0;
   for (;;) {
     if (bwd) {
       switch (kq) {
-        case 16: HSL_CHECK(bwd_resident<16>(p.XT, &occ)); break;
-        case 32: HSL_CHECK(bwd_resident<32>(p.XT, &occ)); break;
-        case 64: HSL_CHECK(bwd_resident<64>(p.XT, &occ)); break;
-        default: HSL_CHECK(bwd_resident<128>(p.XT, &occ)); break;
+        case 16: HSL_CHECK(bwd_resident<16>(p.XT, p.WS, &occ)); break;
+        case 32: HSL_CHECK(bwd_resident<32>(p.XT, p.WS, &occ)); break;
+        case 64: HSL_CHECK(bwd_resident<64>(p.XT, p.WS, &occ)); break;
+        default: HSL_CHECK(bwd_resident<128>(p.XT, p.WS, &occ)); break;
       }
     } else {
       const int xp = p.XP ? (p.XS ? 2 : 1) : 0;
@@ -2079,8 +2092,8 @@ int plan_wide(int B, int H, bool bwd, WidePlan* pl) {
 // chunk spans at most 256 steps with the window products (each running sum takes six
 // 32-term products per 8-step window, 192 additions per chunk) and at most 128 steps with
 // the fp32 products (512 single products per running sum).
-int wgrad_chunks(int T) {
-  const int span = kWgradWin ? 256 : 128;
+int wgrad_chunks(int T, bool ws) {
+  const int span = ws ? 256 : 128;
   const int c = (T + span - 1) / span;
   return c < 1 ? 1 : (c > 8 ? 8 : c);
 }
@@ -2229,7 +2242,8 @@ size_t gemm_region_bytes(int T, int B, int D, int H) {
   if (g7 > need) need = g7;
   if (pick_kq(H) && fused_wgrad_enabled()) {  // planes of the fused weight gradients
     const size_t ng = (B + 3) / 4;
-    const size_t wg = sizeof(float) * wgrad_chunks(T) * ng * 4 * H * H +
+    // sized for the fp32 products' shorter chunks, whatever the mode is now
+    const size_t wg = sizeof(float) * wgrad_chunks(T, false) * ng * 4 * H * H +
                       (D <= 256 ? sizeof(float) * ng * 4 * H * D : 0);
     if (wg > need) need = wg;
   }
@@ -2303,13 +2317,26 @@ void launch_fwd_persistent(const PFwdArgs& a, int grid, int xp, hipStream_t s) {
     default: hipLaunchKernelGGL((rec_fwd_persistent<KQ, 2>), dim3(grid), dim3(512), kPadLdsBytes, s, a); break;
   }
 }
-template <int KQ>
-void launch_bwd_persistent(const PBwdArgs& a, int grid, int xt, hipStream_t s) {
+template <int KQ, bool WS>
+void launch_bwd_persistent_ws(const PBwdArgs& a, int grid, int xt, hipStream_t s) {
   switch (xt) {
-    case -1: hipLaunchKernelGGL((rec_bwd_persistent<KQ, -1>), dim3(grid), dim3(256), kPadLdsBytes, s, a); break;
-    case 0: hipLaunchKernelGGL((rec_bwd_persistent<KQ, 0>), dim3(grid), dim3(512), kPadLdsBytes, s, a); break;
-    default: hipLaunchKernelGGL((rec_bwd_persistent<KQ, 2>), dim3(grid), dim3(512), kBwdWgLdsBytes, s, a); break;
+    case -1:
+      hipLaunchKernelGGL((rec_bwd_persistent<KQ, -1, true>), dim3(grid), dim3(256), bwd_lds_bytes(-1, true), s, a);
+      break;
+    case 0:
+      hipLaunchKernelGGL((rec_bwd_persistent<KQ, 0, WS>), dim3(grid), dim3(512), bwd_lds_bytes(0, WS), s, a);
+      break;
+    default:
+      hipLaunchKernelGGL((rec_bwd_persistent<KQ, 2, WS>), dim3(grid), dim3(512), bwd_lds_bytes(2, WS), s, a);
+      break;
   }
+}
+template <int KQ>
+void launch_bwd_persistent(const PBwdArgs& a, int grid, int xt, bool ws, hipStream_t s) {
+  if (ws)
+    launch_bwd_persistent_ws<KQ, true>(a, grid, xt, s);
+  else
+    launch_bwd_persistent_ws<KQ, false>(a, grid, xt, s);
 }
 
 }  // namespace
@@ -2580,7 +2607,7 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
   float* const wph = w.gemm;
   float* wpx = nullptr;
   if (fused) {
-    const int nch = wgrad_chunks(T);
+    const int nch = wgrad_chunks(T, pl.WS);
     wts = ((T + nch - 1) / nch + 7) / 8 * 8;  // whole 8-step windows per plane
     nsplit = (T + wts - 1) / wts * pl.NG;
     wpx = wph + (size_t)nsplit * 4 * H * H;
@@ -2599,10 +2626,10 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
                 (!fused_ih || dx != nullptr) ? 1 : 0};
     const int slot = timing_begin(kTimeRecBwd, s);
     switch (pl.KQ) {
-      case 16: launch_bwd_persistent<16>(pa, pl.grid, pl.XT, s); break;
-      case 32: launch_bwd_persistent<32>(pa, pl.grid, pl.XT, s); break;
-      case 64: launch_bwd_persistent<64>(pa, pl.grid, pl.XT, s); break;
-      default: launch_bwd_persistent<128>(pa, pl.grid, pl.XT, s); break;
+      case 16: launch_bwd_persistent<16>(pa, pl.grid, pl.XT, pl.WS, s); break;
+      case 32: launch_bwd_persistent<32>(pa, pl.grid, pl.XT, pl.WS, s); break;
+      case 64: launch_bwd_persistent<64>(pa, pl.grid, pl.XT, pl.WS, s); break;
+      default: launch_bwd_persistent<128>(pa, pl.grid, pl.XT, pl.WS, s); break;
     }
     HSL_HIP(hipGetLastError());
     timing_end(slot, s);

@@ -268,12 +268,20 @@ def test_null_states_equal_explicit_zeros(dev, mode):
             assert torch.equal(v, runs[1][k]), k
 
 
-@pytest.mark.parametrize("shape,fused", [((12, 5, 16, 40), 2), ((12, 5, 300, 40), 1), ((130, 6, 32, 72), 2)])
-def test_fused_weight_gradients(dev, shape, fused):
-    """The persistent backward accumulates dW_hh (and dW_ih when D <= 256) itself; the
-    parity bar is the same as for the separate GEMMs.  (130 steps: two dW_hh planes.)"""
-    check(*shape, dev, 2, a=[0.4, 0.3, 0.2, 0.1])
-    assert prlstm_amd._lib.last_backward_fused() == fused
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("shape,fused", [((12, 5, 16, 40), 2), ((12, 5, 300, 40), 1), ((130, 6, 32, 72), 2),
+                                         ((300, 6, 32, 72), 2)])
+def test_fused_weight_gradients(dev, shape, fused, split):
+    """The persistent backward accumulates dW_hh (and dW_ih when D <= 256) itself, on split
+    bf16 products over 8-step windows (split products on) or on the fp32 instruction; the
+    parity bar is the same as for the separate GEMMs.  (130 steps: two dW_hh planes with
+    the fp32 products; 300 steps: two planes either way and a last window of 4 steps.)"""
+    prlstm_amd.set_split_products(split)
+    try:
+        check(*shape, dev, 2, a=[0.4, 0.3, 0.2, 0.1])
+        assert prlstm_amd._lib.last_backward_fused() == fused
+    finally:
+        prlstm_amd.set_split_products(True)
 
 
 def test_workspaces_sized_by_path(dev):

@@ -1540,9 +1540,9 @@ __device__ __forceinline__ void rec_bwd_wgrad(const PBwdArgs& p, int grp, int wg
 //  - B (h_{t-1} and x_t columns): read from memory a slot before the products that use
 //    them, eight values per lane and tile, split in registers (split8).
 //  - The products of window m run during the eight steps of window m+1 (slots), column
-//    tile c at slot c % 8 (one or two tiles per slot), once the recurrent waves have
-//    issued theirs.  The last window (and what a short last window leaves of the one
-//    before) runs in slots after the final barrier.
+//    tile c at slot c % 8 (one or two tiles per slot), from the step's barrier on, beside
+//    the recurrent waves' own products.  The last window (and what a short last window
+//    leaves of the one before) runs in slots after the final barrier.
 //  - dW_hh_s accumulates in registers and goes out as an fp32 plane per chunk of TS
 //    steps (TS a multiple of 8); each dW_ih tile accumulates one window in registers and
 //    is then added to the fp64 LDS copy (ds_add_f64).
@@ -1597,8 +1597,6 @@ __device__ __forceinline__ bool rec_bwd_wgrad_win(const PBwdArgs& p, int grp, in
   const float* const h_save = p.h_save;
   const float* const xin = p.x;
   float* const wph = p.wph;
-  const long long spin = p.spin;
-  int* const err = p.err;
 
   // The lane's index as a value the compiler cannot see through: addresses derived from
   // it inside the loop are recomputed where they are used instead of being kept in
@@ -1758,21 +1756,11 @@ __device__ __forceinline__ bool rec_bwd_wgrad_win(const PBwdArgs& p, int grp, in
         const int ol = opaque_lane();
         put_pieces(m, j, dgl[s & 1][ol >> 4][w * 16 + (ol & 15)]);
       }
-      // the window's A pieces, once per window (they serve its eight slots); the reads
-      // complete while the recurrent waves issue their products
+      // the window's A pieces, once per window (they serve its eight slots)
       if constexpr (j == 0) read_a(max(m - 1, 0), apc);
-      const long long t0 = wall_clock64();
-      while (true) {
-        lds_vint* const f = step_flags();
-        const int m0 = f[0], m1 = f[1], m2 = f[2], m3 = f[3];
-        if (min(min(m0, m1), min(m2, m3)) > s) break;
-        if (abort_flag) return false;
-        if (wall_clock64() - t0 > spin) {
-          raise_abort(&abort_flag, err);
-          return false;
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
+      // The products start at once, beside the recurrent waves' own: a slot that waited
+      // for those (an LDS flag) reached the next barrier after the recurrent waves in
+      // most steps (launch-phase stamps), and the step took its length.
     } else {
       if (s == T) {
         for (int jj = nvalid; jj < kWin; ++jj) put_pieces(last, jj, 0.f);

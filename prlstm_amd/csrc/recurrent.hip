@@ -568,7 +568,10 @@ __device__ __forceinline__ lds_vint* step_flags() { return (lds_vint*)(s_step_fl
 // holds projection wave w's partial sum (over the w-th quarter of D) of x_t[b] . W_ih[row]
 // for the 8 steps of a block.  Rows are padded to 36 floats.
 constexpr int kXinSteps = 8;
-constexpr bool kXprojAfterPublish = true;  // projection products wait for the step's publish
+// true: the projection products of a step wait for the recurrent waves' publish (an LDS
+// flag).  With the products on 16-bit instructions, starting them at the step's barrier
+// is faster (configs[2] forward 430-436 -> 412-415 us).
+constexpr bool kXprojAfterPublish = false;
 #ifndef HSL_XPROJ_SPLIT
 #define HSL_XPROJ_SPLIT 1
 #endif

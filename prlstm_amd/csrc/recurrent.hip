@@ -1592,13 +1592,12 @@ __device__ __forceinline__ bool rec_bwd_wgrad_win(const PBwdArgs& p, int grp, in
   const int kb = lane >> 4, l16 = lane & 15;  // batch slot of the lane's k values
   const int cb = grp * Bg + kb;
   const bool bok = kb < Bg && cb < B;
-  const int brow = bok ? cb : 0;
   const int nth = (H + 31) / 32, ntx = (D + 31) / 32;
   double* const xacc = reinterpret_cast<double*>(lds);
   const unsigned abase = XT > 0 ? (unsigned)kXaccLdsBytes : 0u;
   // the fields used inside the loop, as locals (the lambdas below capture these, not p)
   const float* const h_save = p.h_save;
-  const float* const xin = p.x;
+  const float* const xrows = p.x;
   float* const wph = p.wph;
 
   // The lane's index as a value the compiler cannot see through: addresses derived from
@@ -1655,7 +1654,7 @@ __device__ __forceinline__ bool rec_bwd_wgrad_win(const PBwdArgs& p, int grp, in
       if (c < NH)
         v[i] = *byte_at(h_save + (size_t)t * B * H, 4u * (unsigned)(orow * H + col));
       else
-        v[i] = *byte_at(xin + (size_t)t * B * D, 4u * (unsigned)(orow * D + col));
+        v[i] = *byte_at(xrows + (size_t)t * B * D, 4u * (unsigned)(orow * D + col));
     }
   };
   // the A pieces of window win's four row tiles

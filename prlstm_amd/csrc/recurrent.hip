@@ -139,26 +139,39 @@ __global__ __launch_bounds__(256) void whh_grad_finalize_kernel(const float* __r
   if (threadIdx.x == 0) rowdot[n] = red[0];
 }
 
+// Adds column entries p[b * stride] for b = b0, b0 + 1, ... in chunks of C into ps[b % 8]
+// (b0 a multiple of 8); a chunk's C loads are all issued before the first addition.
+template <int C>
+__device__ __forceinline__ void add_parts(const double* __restrict__ p, size_t stride, int& b, int B, double (&ps)[8]) {
+  for (; b + C <= B; b += C) {
+    double v[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) v[i] = p[(size_t)(b + i) * stride];
+#pragma unroll
+    for (int i = 0; i < C; ++i) ps[i & 7] += v[i];
+  }
+}
+
 // db_ih = db_hh_s = sum_b db_part[b][n]; db_hh = a * db; da[g] = sum_{n in g} rowdot[n] + b_hh[n] db[n].
-// One workgroup per gate.
-__global__ __launch_bounds__(256) void bias_da_finalize_kernel(const double* __restrict__ db_part, int B,
-                                                               const double* __restrict__ rowdot,
-                                                               const float* __restrict__ b_hh,
-                                                               const float* __restrict__ a, float* __restrict__ db_ih,
-                                                               float* __restrict__ db_hh, float* __restrict__ da, int H) {
-  __shared__ double red[256];
+// One workgroup per gate, one unit per thread while H <= 1024: the kernel is a handful of
+// memory round trips, so every thread keeps all of its unit's partial loads in flight.
+__global__ __launch_bounds__(1024) void bias_da_finalize_kernel(const double* __restrict__ db_part, int B,
+                                                                const double* __restrict__ rowdot,
+                                                                const float* __restrict__ b_hh,
+                                                                const float* __restrict__ a, float* __restrict__ db_ih,
+                                                                float* __restrict__ db_hh, float* __restrict__ da, int H) {
+  __shared__ double red[1024];
   const int g = blockIdx.x;
   const float ag = a ? a[g] : 1.0f;
   double acc = 0.0;
   for (int u = threadIdx.x; u < H; u += blockDim.x) {
     const int n = g * H + u;
-    // eight independent partial sums keep eight loads in flight (fixed order: deterministic)
+    // eight independent partial sums, b % 8 each, in increasing b (fixed order: deterministic)
     double ps[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
     int b = 0;
-    for (; b + 8 <= B; b += 8) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ps[i] += db_part[(size_t)(b + i) * 4 * H + n];
-    }
+    add_parts<32>(db_part + n, (size_t)4 * H, b, B, ps);
+    add_parts<16>(db_part + n, (size_t)4 * H, b, B, ps);
+    add_parts<8>(db_part + n, (size_t)4 * H, b, B, ps);
     for (; b < B; ++b) ps[0] += db_part[(size_t)b * 4 * H + n];
     const double s = ((ps[0] + ps[1]) + (ps[2] + ps[3])) + ((ps[4] + ps[5]) + (ps[6] + ps[7]));
     const float db = (float)s;
@@ -168,7 +181,7 @@ __global__ __launch_bounds__(256) void bias_da_finalize_kernel(const double* __r
   }
   red[threadIdx.x] = acc;
   __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
     if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
     __syncthreads();
   }
@@ -2337,7 +2350,7 @@ int copy_f32(float* dst, const float* src, size_t n, hipStream_t s) { return cop
 int bias_grads_from_parts(const double* db_part, int B, const double* rowdot, const float* b_hh, const float* a,
                           float* db_ih, float* db_hh, float* da, int H, hipStream_t s) {
   if (H == 0) return HSL_OK;
-  hipLaunchKernelGGL(bias_da_finalize_kernel, dim3(4), dim3(256), 0, s, db_part, B, rowdot, b_hh, a, db_ih, db_hh,
+  hipLaunchKernelGGL(bias_da_finalize_kernel, dim3(4), dim3(1024), 0, s, db_part, B, rowdot, b_hh, a, db_ih, db_hh,
                      da, H);
   HSL_HIP(hipGetLastError());
   return HSL_OK;

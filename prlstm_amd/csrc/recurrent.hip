@@ -139,6 +139,69 @@ __global__ __launch_bounds__(256) void whh_grad_finalize_kernel(const float* __r
   if (threadIdx.x == 0) rowdot[n] = red[0];
 }
 
+// whh_grad_finalize_kernel on 16-byte groups (H % 4 == 0, every pointer 16-byte aligned):
+// one wave per row n of dW_hh, each lane's planes requested in batches of 8 before they
+// are added, and the row's da term reduced across the wave without LDS or barriers.
+// Each element's planes are added in plane order from 0.0 in fp64, as in the kernel
+// above, so dW_hh and dW_ih come out bit for bit the same; only the order of rowdot's
+// fp64 sum differs.  Blocks past the 4H/4 row blocks sum the dW_ih planes.
+__global__ __launch_bounds__(256) void whh_grad_finalize4_kernel(const float4* __restrict__ P, int splits,
+                                                                 const float4* __restrict__ w_hh,
+                                                                 const float* __restrict__ a,
+                                                                 float4* __restrict__ dw_hh,
+                                                                 double* __restrict__ rowdot, int H,
+                                                                 const float4* __restrict__ X, int xplanes,
+                                                                 float4* __restrict__ dw_ih, size_t xn4) {
+  constexpr int kBatch = 8;
+  const int rblocks = H;  // 4H rows, four per block
+  auto add4 = [](double (&v)[4], const float4 q) {
+    v[0] += (double)q.x;
+    v[1] += (double)q.y;
+    v[2] += (double)q.z;
+    v[3] += (double)q.w;
+  };
+  auto sum_planes = [&](const float4* base, size_t stride, int nplanes, double (&v)[4]) {
+    for (int z0 = 0; z0 < nplanes; z0 += kBatch) {
+      float4 q[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i)
+        q[i] = z0 + i < nplanes ? base[(size_t)(z0 + i) * stride] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) add4(v, q[i]);  // adding +0.0 past the last plane is exact
+    }
+  };
+  if ((int)blockIdx.x >= rblocks) {
+    const size_t nb = gridDim.x - rblocks;
+    for (size_t e = (size_t)(blockIdx.x - rblocks) * blockDim.x + threadIdx.x; e < xn4; e += nb * blockDim.x) {
+      double v[4] = {0.0, 0.0, 0.0, 0.0};
+      sum_planes(X + e, xn4, xplanes, v);
+      dw_ih[e] = make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+    }
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);  // < 4H: rblocks * 4 rows
+  const int H4 = H / 4;
+  const size_t plane4 = (size_t)H * H;  // 4H * H floats
+  const float ag = a[n / H];
+  double acc = 0.0;
+  for (int k = lane; k < H4; k += 64) {
+    const size_t e = (size_t)n * H4 + k;
+    double v[4] = {0.0, 0.0, 0.0, 0.0};
+    sum_planes(P + e, plane4, splits, v);
+    const float4 s = make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+    dw_hh[e] = make_float4(ag * s.x, ag * s.y, ag * s.z, ag * s.w);
+    const float4 w = w_hh[e];
+    acc += (double)w.x * (double)s.x;
+    acc += (double)w.y * (double)s.y;
+    acc += (double)w.z * (double)s.z;
+    acc += (double)w.w * (double)s.w;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+  if (lane == 0) rowdot[n] = acc;
+}
+
 // Adds column entries p[b * stride] for b = b0, b0 + 1, ... in chunks of C into ps[b % 8]
 // (b0 a multiple of 8); a chunk's C loads are all issued before the first addition.
 template <int C>
@@ -2710,9 +2773,20 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
   }
   {  // dW_hh (and the fused dW_ih planes in extra blocks of the same launch)
     const size_t xn = fused_ih ? (size_t)4 * H * D : 0;
-    const int xblocks = fused_ih ? grid_for(xn) : 0;
-    hipLaunchKernelGGL(whh_grad_finalize_kernel, dim3(4 * H + xblocks), dim3(256), 0, s, wph, splits, w_hh, a,
-                       dw_hh, w.rowdot, H, (const float*)wpx, pl.NG, dw_ih, xn);
+    auto al16 = [](const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+    const bool vec = H % 4 == 0 && al16(wph) && al16(w_hh) && al16(dw_hh) &&
+                     (!fused_ih || (al16(wpx) && al16(dw_ih)));
+    if (vec) {
+      const int xblocks = fused_ih ? grid_for(xn / 4) : 0;
+      hipLaunchKernelGGL(whh_grad_finalize4_kernel, dim3(H + xblocks), dim3(256), 0, s,
+                         reinterpret_cast<const float4*>(wph), splits, reinterpret_cast<const float4*>(w_hh), a,
+                         reinterpret_cast<float4*>(dw_hh), w.rowdot, H, reinterpret_cast<const float4*>(wpx), pl.NG,
+                         reinterpret_cast<float4*>(dw_ih), xn / 4);
+    } else {
+      const int xblocks = fused_ih ? grid_for(xn) : 0;
+      hipLaunchKernelGGL(whh_grad_finalize_kernel, dim3(4 * H + xblocks), dim3(256), 0, s, wph, splits, w_hh, a,
+                         dw_hh, w.rowdot, H, (const float*)wpx, pl.NG, dw_ih, xn);
+    }
     HSL_HIP(hipGetLastError());
   }
   HSL_CHECK(bias_grads_from_parts(w.db_part, B, w.rowdot, b_hh, a, db_ih, db_hh, da, H, s));

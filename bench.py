@@ -24,7 +24,12 @@ Prints ONE JSON line:
               configs[4] beside it
   scan        configs[4] parallel scan (T=4096 B=16 H=1024) forward and
               backward kernels: algorithmic HBM bytes / launch time
-  modes       every configured shape (configs[0..4], configs[1] in both modes)
+  fused_products  the arithmetic of the products fused into the headline step's
+              persistent kernels (split_bf16x6 by default, fp32 with
+              hsl_set_split_products(0)); split_products_off: the same step and its
+              kernel times with every product on the fp32 instruction
+  modes       every configured shape (configs[0..4], configs[1] in both modes, and
+              the reference's published T64 B32 (D128 H256) and (D512 H1024) shapes)
               as one graph-replayed fwd+bwd step each; TFLOP/s counts the products
               the step executes: 16*T*B*H*D + 24*T*B*H^2 (recurrent: projection,
               recurrence both ways, dW_ih, dW_hh) or 2*2*T*B*D*4H (parallel:
@@ -82,46 +87,72 @@ def make_inputs():
     return m, x
 
 
-def bench_gpu(args):
-    from prlstm_amd import _lib
+def _graph_step_ms(m, x, steps, warmup):
+    """(ms per step, wall ms per step): `steps` replays of the captured fwd+bwd step after
+    `warmup` replays, bracketed by events on the replay stream."""
     from prlstm_amd.graph import GraphedTrainStep
-    dev = torch.device("cuda", 0)
-    m_cpu, x_cpu = make_inputs()
-    m = m_cpu.to(dev)
-    x = x_cpu.to(dev)
     step = GraphedTrainStep(m, x)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step.step()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     w0 = time.perf_counter()
     e0.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step.step()
     e1.record()
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - w0) * 1e3 / args.steps
-    ms = e0.elapsed_time(e1) / args.steps
-    path = _lib.last_recurrent_path()
+    wall_ms = (time.perf_counter() - w0) * 1e3 / steps
+    return e0.elapsed_time(e1) / steps, wall_ms
 
-    # per-kernel launch times: the same step run eagerly with the library's event hooks
+
+def _kernel_ms(m, x, steps):
+    """Mean launch time (ms) of each library kernel kind over `steps` eager steps, from the
+    HIP events the library records on the launch stream (hsl_set_timing)."""
+    from prlstm_amd import _lib
+    kinds = ("rec_fwd", "rec_bwd", "input_proj", "step_fwd", "step_bwd")
     _lib.set_timing(True)
-    for k in ("rec_fwd", "rec_bwd", "input_proj", "step_fwd", "step_bwd"):
+    for k in kinds:
         _lib.timing_collect(k)
-    for _ in range(args.steps):
+    for _ in range(steps):
         m.zero_grad(set_to_none=True)
         out, _ = m(x)
         out.sum().backward()
     torch.cuda.synchronize()
     kern = {}
-    for k in ("rec_fwd", "rec_bwd", "input_proj", "step_fwd", "step_bwd"):
+    for k in kinds:
         tot, n = _lib.timing_collect(k)
         if n:
             kern[k] = tot / n
     _lib.set_timing(False)
+    return kern
+
+
+def bench_gpu(args):
+    from prlstm_amd import _lib
+    dev = torch.device("cuda", 0)
+    m_cpu, x_cpu = make_inputs()
+    m = m_cpu.to(dev)
+    x = x_cpu.to(dev)
+    ms, wall_ms = _graph_step_ms(m, x, args.steps, args.warmup)
+    path = _lib.last_recurrent_path()
+    kern = _kernel_ms(m, x, args.steps)
     fused = _lib.last_backward_fused()
     log(f"graph step {ms:.4f} ms (wall {wall_ms:.4f} ms), path {path}, fused wgrad {fused}, kernels(ms) {kern}")
-    return ms, wall_ms, kern, path, fused
+    off = None
+    if not args.no_split_off:
+        # the same step with every fused and separate product on the fp32 instruction
+        prev = _lib.set_split_products(0)
+        try:
+            off_ms, _ = _graph_step_ms(m, x, args.steps, args.warmup)
+            off_kern = _kernel_ms(m, x, args.steps)
+        finally:
+            _lib.set_split_products(prev)
+        off = {"arithmetic": "fp32", "ms_per_step": round(off_ms, 5),
+               "timesteps_batch_per_s": round(T * B / off_ms * 1e3, 1),
+               "kernels_ms": {k: round(v, 5) for k, v in off_kern.items()}}
+        log(f"split products off: graph step {off_ms:.4f} ms, kernels(ms) {off_kern}")
+    return ms, wall_ms, kern, path, fused, off
 
 
 def bench_scan(args):
@@ -183,14 +214,17 @@ def bench_scan(args):
     return res
 
 
-# configs[0..4] of BASELINE.json (configs[1] in both modes), and configs[4] with the
-# module in bf16 (16-bit input projection): (name, T, B, D, H, parallel, a, dtype)
+# configs[0..4] of BASELINE.json (configs[1] in both modes), the two shapes of the
+# reference's published table (README.md:73-79) that no config covers, and configs[4]
+# with the module in bf16 (16-bit input projection): (name, T, B, D, H, parallel, a, dtype)
 MODE_CONFIGS = [
     ("configs[0]", 32, 16, 64, 128, False, 1e-4, torch.float32),
     ("configs[1]", 128, 32, 256, 256, False, 1e-4, torch.float32),
     ("configs[1]", 128, 32, 256, 256, True, 1e-4, torch.float32),
     ("configs[2] a~U(0,0.5)", 256, 32, 256, 512, False, None, torch.float32),
     ("configs[3]", 64, 32, 1024, 2048, False, 1e-4, torch.float32),
+    ("README.md:75 shape", 64, 32, 128, 256, False, 1e-4, torch.float32),
+    ("README.md:78 shape", 64, 32, 512, 1024, False, 1e-4, torch.float32),
     ("configs[4]", 4096, 16, 256, 1024, True, 0.0, torch.float32),
     ("configs[4] bf16 module", 4096, 16, 256, 1024, True, 0.0, torch.bfloat16),
 ]
@@ -325,6 +359,8 @@ def main():
     ap.add_argument("--no-cpu-parallel", action="store_true", help="skip the parallel-mode CPU baseline")
     ap.add_argument("--no-scan", action="store_true")
     ap.add_argument("--no-modes", action="store_true", help="skip the per-config table of both modes")
+    ap.add_argument("--no-split-off", action="store_true",
+                    help="skip the headline step with the split products switched off")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -334,7 +370,7 @@ def main():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
 
-    ms, wall_ms, kern, path, fused = bench_gpu(args)
+    ms, wall_ms, kern, path, fused, split_off = bench_gpu(args)
     scan = None if args.no_scan else bench_scan(args)
     modes = None if args.no_modes else bench_modes(args)
     cpu = None if args.no_cpu else bench_cpu(args)
@@ -393,11 +429,20 @@ def main():
         "wall_ms_per_step": round(wall_ms, 5),
         "scan": scan,
         "modes": modes,
-        # products of the modes table: with this switch on (the library default), input
-        # projections of >= 256 tiles of 256x256 and weight-gradient / dx products of >= 8
-        # GFLOP run as exact three-piece bf16 splits (six piece products, fp32 accuracy);
-        # the headline step's products are fused into its persistent kernels (fp32 MFMA)
+        # hsl_set_split_products during the run (the library default is on).  On, the
+        # headline step's input projection (inside rec_fwd) and its dW_hh / dW_ih products
+        # (inside rec_bwd) run as exact three-piece bf16 splits, six piece products with
+        # fp32 accumulation, and so do the modes table's large separate products; the
+        # recurrent h W_hh^T and dg W_hh products stay on the fp32 instruction.  The same
+        # step with the switch off (every product on the fp32 instruction) is beside it.
         "split_products": bool(_split_products_state()),
+        "fused_products": {
+            "arithmetic": "split_bf16x6" if _split_products_state() else "fp32",
+            "note": "input projection (rec_fwd) and dW_hh/dW_ih (rec_bwd) of the headline step; "
+                    "split_bf16x6 = each fp32 operand split exactly into three bf16 pieces, the six "
+                    "largest piece products on bf16 MFMA with fp32 accumulation; the recurrent "
+                    "products are fp32 MFMA either way"},
+        "split_products_off": split_off,
         "cpu_baseline": cpu,
     }
     if cpu:

@@ -30,6 +30,24 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+// The kernels and GEMMs hold these in 32-bit integers: the GEMM rows and reduction
+// length T*B, the elements of a [4H, max(D, H)] weight, and the bytes of one time step of
+// a [B, 4H] or [B, D] row block (addressed as a raw buffer of < 2^31 bytes).  Whole
+// [T, B, max(4H, D)] buffers are sized in size_t, bounded at 2^40 elements.
+int check_shape(const char* who, int T, int B, int D, int H) {
+  if (T < 0 || B < 0 || D < 0 || H < 0)
+    return fail(HSL_ERR_ARG, "%s: negative dimension (T=%d B=%d D=%d H=%d)", who, T, B, D, H);
+  const long long t = T, b = B, d = D, g = 4ll * H, lim = 1ll << 31;
+  const long long row = g > d ? g : d;      // widest per-(t, b) row in floats
+  const long long wcols = d > H ? d : H;    // columns of the widest weight
+  if (t * b >= lim || g * wcols >= lim || 4 * b * row >= lim || t >= (1ll << 30) || t * b * row > (1ll << 40))
+    return fail(HSL_ERR_UNSUPPORTED,
+                "%s: T=%d B=%d D=%d H=%d is beyond the library's 32-bit index range (needs T*B < 2^31, "
+                "4H*max(D,H) < 2^31 and a time step's [B, max(4H,D)] row block < 2^31 bytes)",
+                who, T, B, D, H);
+  return HSL_OK;
+}
+
 int hip_fail(hipError_t e, const char* what) {
   return fail(HSL_ERR_HIP, "%s failed: %s", what, hipGetErrorString(e));
 }

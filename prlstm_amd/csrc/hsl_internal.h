@@ -24,6 +24,11 @@ int hip_fail(hipError_t e, const char* what);    // HSL_ERR_HIP with the HIP tex
     if (hsl_rc_ != HSL_OK) return hsl_rc_; \
   } while (0)
 
+// Shape check shared by every entry point that takes (T, B, D, H) (D = 0 where there is
+// none): negative sizes are HSL_ERR_ARG, shapes beyond the 32-bit index math of the
+// kernels and GEMMs are HSL_ERR_UNSUPPORTED.  `who` names the entry point in the text.
+int check_shape(const char* who, int T, int B, int D, int H);
+
 // Per-device facts queried once.
 struct DeviceInfo {
   int device = -1;

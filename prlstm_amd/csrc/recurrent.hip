@@ -2154,10 +2154,12 @@ int plan_wide(int B, int H, bool bwd, WidePlan* pl) {
   return HSL_OK;
 }
 
-// Chunks of the fused weight gradients' fp32 partial planes (at most 8 per group).  A
-// chunk spans at most 256 steps with the window products (each running sum takes six
-// 32-term products per 8-step window, 192 additions per chunk) and at most 128 steps with
-// the fp32 products (512 single products per running sum).
+// Chunks of the fused weight gradients' fp32 partial planes, at most 8 per group (the
+// workspace holds 8).  Up to T = 2048 (window products) or T = 1024 (fp32 products) a
+// chunk spans at most 256 or 128 steps: each running sum then takes at most 32 windows of
+// six 32-term products, or 512 single products.  Longer sequences share the 8 chunks, so
+// a chunk spans ceil(T / 8) steps (at T = 2048 with the fp32 products: 1024 single
+// products per running sum, which the long-sequence test checks against the parity bar).
 int wgrad_chunks(int T, bool ws) {
   const int span = ws ? 256 : 128;
   const int c = (T + span - 1) / span;
@@ -2367,12 +2369,7 @@ size_t carve_bwd(void* ws, size_t cap, int T, int B, int D, int H, BwdNeeds nd, 
   return c.off;
 }
 
-int check_dims(int T, int B, int D, int H) {
-  if (T < 0 || B < 0 || D < 0 || H < 0) return fail(HSL_ERR_ARG, "negative dimension (T=%d B=%d D=%d H=%d)", T, B, D, H);
-  if ((long long)T * B * 4 * H > (1ll << 40)) return fail(HSL_ERR_UNSUPPORTED, "problem too large");
-  if (T >= (1 << 30)) return fail(HSL_ERR_UNSUPPORTED, "T too large");
-  return HSL_OK;
-}
+int check_dims(int T, int B, int D, int H) { return check_shape("recurrent mode", T, B, D, H); }
 
 template <int KQ>
 void launch_fwd_persistent(const PFwdArgs& a, int grid, int xp, hipStream_t s) {

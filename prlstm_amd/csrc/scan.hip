@@ -302,13 +302,8 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
   }
 }
 
-int check_scan_dims(int T, int B, int H) {
-  if (T < 0 || B < 0 || H < 0) return fail(HSL_ERR_ARG, "negative dimension (T=%d B=%d H=%d)", T, B, H);
-  // one time step of gates (16 B H bytes) is addressed as a buffer of < 2^31 bytes
-  if ((long long)B * H * 16 >= (1ll << 31) || (long long)T * B * 4 * H > (1ll << 40))
-    return fail(HSL_ERR_UNSUPPORTED, "problem too large (B*H = %lld; at most 2^27 - 1 channels)", (long long)B * H);
-  return HSL_OK;
-}
+// one time step of gates (16 B H bytes) is addressed as a buffer of < 2^31 bytes
+int check_scan_dims(int T, int B, int H, int D = 0) { return check_shape("parallel mode", T, B, D, H); }
 
 int scan_fwd(const float* gates, const float* c0, float eps, float* out, float* cseq, int T, int B, int H,
              hipStream_t s) {
@@ -377,8 +372,7 @@ int par_bwd_impl(const float* dout, const float* dh_n, const float* dc_n, const 
                  float* db_ih, float* dc0, void* ws, size_t ws_bytes, int T, int B, int D, int H, int fmt,
                  hipStream_t s) {
   const char* fn = fmt < 0 ? "hsl_par_bwd" : "hsl_par_bwd_b16";
-  HSL_CHECK(check_scan_dims(T, B, H));
-  if (D < 0) return fail(HSL_ERR_ARG, "negative D");
+  HSL_CHECK(check_scan_dims(T, B, H, D));
   if (H == 0) return HSL_OK;
   if (!dw_ih || !db_ih || !w_ih) return fail(HSL_ERR_ARG, "%s: null pointer", fn);
   ParWs w;
@@ -440,8 +434,7 @@ int hsl_scan_bwd(const float* gates, const float* c0, const float* c_seq, const 
 
 int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float* b_ih, float eps, float* gates,
                 float* out, float* c_seq, int T, int B, int D, int H, void* stream) {
-  HSL_CHECK(check_scan_dims(T, B, H));
-  if (D < 0) return fail(HSL_ERR_ARG, "negative D");
+  HSL_CHECK(check_scan_dims(T, B, H, D));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (T == 0 || B == 0 || H == 0) return HSL_OK;
   if (!x || !w_ih || !b_ih || !gates || !out || !c_seq) return fail(HSL_ERR_ARG, "hsl_par_fwd: null pointer");
@@ -454,8 +447,7 @@ int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float*
 
 int hsl_par_fwd_b16(const void* x, const float* c0, const void* w_ih, const float* b_ih, float eps, float* gates,
                     float* out, float* c_seq, int T, int B, int D, int H, int fmt, void* stream) {
-  HSL_CHECK(check_scan_dims(T, B, H));
-  if (D < 0) return fail(HSL_ERR_ARG, "negative D");
+  HSL_CHECK(check_scan_dims(T, B, H, D));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (T == 0 || B == 0 || H == 0) return HSL_OK;
   if (!x || !w_ih || !b_ih || !gates || !out || !c_seq) return fail(HSL_ERR_ARG, "hsl_par_fwd_b16: null pointer");

@@ -149,14 +149,13 @@ def test_head_start_schedule_matches_oracle_twin(dev, shape):
         torch.cuda.synchronize()
         r32 = _oracle_step(ref32, x)
         r64 = _oracle_step(ref64, x.double())
-        got = {"out": out}
+        got = {"out": out, "h_n": step.static_h_n, "c_n": step.static_c_n}
         got.update({"d" + n: p.grad for n, p in m.named_parameters()})
         for n, p in ref32.named_parameters():
             assert (got["d" + n] is None) == (p.grad is None), (i, n)
         mode = "parallel" if parallel else "recurrent"
+        assert set(r32) <= set(got), (set(r32) - set(got))
         for k in r32:
-            if k in ("h_n", "c_n"):
-                continue
             if parallel:  # fp64 is the bar in parallel mode (the fp32 log-domain scan drifts)
                 assert_close64(f"step {i} {mode} {k}", got[k].reshape(r64[k].shape), r64[k], RTOL, ATOL)
             else:

@@ -144,8 +144,11 @@ def _par_fwd(x, c0, w_ih, b_ih, T, B, D, H):
     return gates, out, c_seq
 
 
-def test_config4_full_size_subsets(dev):
-    """T4096 B16 D256 H1024, a=0, checked on channel / row subsets."""
+def test_config4_full_size_all_channels(dev):
+    """T4096 B16 D256 H1024, a=0.  The input projection on sampled rows; the
+    scan forward (c, out) and backward (dgates, db partials) on every one of the 16384
+    channels, against the reference formula (_parallel.py:21-74) evaluated in fp64 on the
+    GPU's gates, in chunks of channels."""
     T, B, D, H = 4096, 16, 256, 1024
     print(f"parallel configs[4] T={T} B={B} D={D} H={H}", flush=True)
     torch.manual_seed(0)
@@ -163,21 +166,7 @@ def test_config4_full_size_subsets(dev):
     want = xr @ ref.weight_ih_l0.detach().double().t() + ref.bias_ih_l0.detach().double()
     got = gates.view(T * B, 4 * H)[rows.to(dev)].cpu().double()
     assert lim_ratio(got, want, RTOL, ATOL) <= 1.0
-    # scan: random channels over all T, fp64 reference formula from the GPU gates
-    ch = torch.randperm(B * H, generator=g)[:48]
-    bb, jj = ch // H, ch % H
-    gv = gates.cpu().view(T, B, 4, H).permute(1, 3, 0, 2)          # [B, H, T, 4]
-    gsub = gv[bb, jj].permute(1, 0, 2).double().contiguous().requires_grad_(True)  # [T, n, 4]
-    i, f, gg, o = (torch.sigmoid(gsub[..., k]) for k in range(4))
-    c0_sub = torch.zeros(len(ch), 1, 1, dtype=torch.float64)
-    c_ref = O.heinsen_scan(f.t().unsqueeze(-1), c0_sub, (i * gg).t().unsqueeze(-1))[..., 0].t()
-    out_ref = o * torch.tanh(c_ref)
-    c_got = c_seq.cpu()[:, bb, jj].double()
-    out_got = out.cpu()[:, bb, jj].double()
-    print(f"  c   {lim_ratio(c_got, c_ref, RTOL, ATOL):.3g}x  out {lim_ratio(out_got, out_ref, RTOL, ATOL):.3g}x")
-    assert lim_ratio(c_got, c_ref, RTOL, ATOL) <= 1.0
-    assert lim_ratio(out_got, out_ref, RTOL, ATOL) <= 1.0
-    # backward of the scan on the same channels: autograd of the fp64 reference formula
+    # backward of the scan (same gates), for the loss out . dout + h_n . dh_n + c_n . dc_n
     dout = torch.randn(T, B, H, generator=g)
     dh_n = torch.randn(B, H, generator=g)
     dc_n = torch.randn(B, H, generator=g)
@@ -191,18 +180,36 @@ def test_config4_full_size_subsets(dev):
     _lib.call("hsl_scan_bwd", P(gates), P(c0), P(c_seq), P(dout_d), P(dh_d), P(dc_d), 1e-6,
               P(dgates), P(db_part), P(dc0), T, B, H, _lib.stream_of(dev))
     torch.cuda.synchronize()
-    dsub = dout[:, bb, jj].double()
-    loss = (out_ref * dsub).sum() + (out_ref[-1] * dh_n[bb, jj].double()).sum() \
-        + (c_ref[-1] * dc_n[bb, jj].double()).sum()
-    loss.backward()
-    dg_ref = gsub.grad                                    # [T, n, 4]
-    dg_got = dgates.cpu().view(T, B, 4, H).permute(1, 3, 0, 2)[bb, jj].permute(1, 0, 2).double()
-    print(f"  dgates {lim_ratio(dg_got, dg_ref, RTOL, ATOL):.3g}x")
-    assert lim_ratio(dg_got, dg_ref, RTOL, ATOL) <= 1.0
-    # column sums of dgates (the db_ih partials) for those channels
-    dbp = db_part.cpu().view(B, 4, H).permute(0, 2, 1)[bb, jj]      # [n, 4]
-    want_db = dg_got.sum(0)
-    assert (dbp - want_db).abs().max().item() < 1e-6 * (1 + want_db.abs().max().item())
+    # channel-major copies: [B*H, T, 4] gates and gradients, [B*H, T] states
+    n = B * H
+    gv = gates.view(T, B, 4, H).permute(1, 3, 0, 2).reshape(n, T, 4).cpu()
+    dgv = dgates.view(T, B, 4, H).permute(1, 3, 0, 2).reshape(n, T, 4).cpu()
+    cv = c_seq.permute(1, 2, 0).reshape(n, T).cpu()
+    ov = out.permute(1, 2, 0).reshape(n, T).cpu()
+    dv = dout.permute(1, 2, 0).reshape(n, T)
+    dbp = db_part.cpu().view(B, 4, H).permute(0, 2, 1).reshape(n, 4)
+    dhv, dcv = dh_n.reshape(n), dc_n.reshape(n)
+    worst = {"c": 0.0, "out": 0.0, "dgates": 0.0}
+    CH = 2048
+    for c_lo in range(0, n, CH):
+        sl = slice(c_lo, c_lo + CH)
+        gsub = gv[sl].double().requires_grad_(True)                          # [ch, T, 4]
+        i, f, gg, o = (torch.sigmoid(gsub[..., k]) for k in range(4))
+        c0_sub = torch.zeros(gsub.shape[0], 1, 1, dtype=torch.float64)
+        c_ref = O.heinsen_scan(f.unsqueeze(-1), c0_sub, (i * gg).unsqueeze(-1))[..., 0]  # [ch, T]
+        out_ref = o * torch.tanh(c_ref)
+        worst["c"] = max(worst["c"], lim_ratio(cv[sl], c_ref, RTOL, ATOL))
+        worst["out"] = max(worst["out"], lim_ratio(ov[sl], out_ref, RTOL, ATOL))
+        loss = (out_ref * dv[sl].double()).sum() + (out_ref[:, -1] * dhv[sl].double()).sum() \
+            + (c_ref[:, -1] * dcv[sl].double()).sum()
+        loss.backward()
+        worst["dgates"] = max(worst["dgates"], lim_ratio(dgv[sl], gsub.grad, RTOL, ATOL))
+        # column sums of dgates (the db_ih partials) of these channels
+        want_db = dgv[sl].double().sum(1)
+        assert (dbp[sl] - want_db).abs().max().item() < 1e-6 * (1 + want_db.abs().max().item())
+    print("  all channels: " + ", ".join(f"{k} {v:.3g}x" for k, v in worst.items()), flush=True)
+    for k, v in worst.items():
+        assert v <= 1.0, (k, v)
 
 
 def test_config4_module_step_runs_and_grads_are_finite(dev):
@@ -249,8 +256,9 @@ def test_config4_weight_gradient_full_size(dev):
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     dw = torch.empty(4 * H, D, device=dev)
     db = torch.empty(4 * H, device=dev)
+    dx = torch.empty(T, B, D, device=dev)
     _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(xd), P(c0), P(gates), P(c_seq), P(w_ih), 1e-6,
-              None, P(dw), P(db), None, P(ws), nbytes, T, B, D, H, s)
+              P(dx), P(dw), P(db), None, P(ws), nbytes, T, B, D, H, s)
     torch.cuda.synchronize()
     rows = torch.arange(0, 4 * H, 29)
     dg = dgates.view(T * B, 4 * H)[:, rows.to(dev)].cpu()
@@ -263,3 +271,12 @@ def test_config4_weight_gradient_full_size(dev):
     assert_parity("dW_ih", got, cpu32, want, RTOL, ATOL)
     want_db = dg.double().sum(0)
     assert lim_ratio(db[rows.to(dev)].cpu().double(), want_db, RTOL, ATOL) <= 1.0
+    # dx = dgates W_ih (K = 4H) on 512 sampled (t, b) rows, all D columns
+    xr = torch.randperm(T * B, generator=g)[:512]
+    dgr = dgates.view(T * B, 4 * H)[xr.to(dev)].cpu()
+    wi = w_ih.cpu()
+    want_dx = dgr.double() @ wi.double()
+    got_dx = dx.view(T * B, D)[xr.to(dev)].cpu()
+    print(f"  dx rows {len(xr)}: gpu {lim_ratio(got_dx, want_dx, RTOL, ATOL):.3g}x of the tolerance vs fp64",
+          flush=True)
+    assert_parity("dx", got_dx, dgr @ wi, want_dx, RTOL, ATOL)

@@ -180,6 +180,12 @@ def test_config3_wide_forward(dev):
     assert prlstm_amd.last_recurrent_path() == 3
 
 
+def test_published_h1024_shape(dev):
+    """(T64, B32, D512, H1024): the reference's published shape between configs[2] and
+    configs[3] (README.md:78), on the path the library picks for it."""
+    check(64, 32, 512, 1024, dev, 0)
+
+
 @pytest.mark.parametrize("scope", [0, 1])
 def test_wide_forward_partial_batch_hx(dev, scope):
     """The wide forward with B < 32 (absent batch columns), h0/c0 given, a ~ U(0, 0.5), and
@@ -209,10 +215,17 @@ def test_sgd_training_step(dev):
         assert (p.detach().cpu() - q.detach()).abs().max() < 1e-5, n
 
 
-def test_long_sequence_persistent(dev):
-    """T=2048 on the persistent kernels: the fused weight gradients then keep 256 steps
-    (1024 products) per fp32 partial plane, the longest running sums the backward makes."""
-    check(2048, 4, 32, 512, dev, 2, a=[0.3, 0.2, 0.4, 0.1])
+@pytest.mark.parametrize("split", [True, False])
+def test_long_sequence_persistent(dev, split):
+    """T=2048 on the persistent kernels: the fused weight gradients keep at most 8 fp32
+    partial planes per batch group, so each plane then spans 256 steps: 32 windows of six
+    32-term bf16 piece products per running sum (split products on), or 1024 single fp32
+    products (split products off), the longest running sums the backward makes."""
+    prlstm_amd.set_split_products(split)
+    try:
+        check(2048, 4, 32, 512, dev, 2, a=[0.3, 0.2, 0.4, 0.1])
+    finally:
+        prlstm_amd.set_split_products(True)
 
 
 def test_repeated_calls_are_deterministic(dev):

@@ -67,6 +67,37 @@ def test_argument_errors_are_reported_without_a_gpu():
         _lib.call("hsl_rec_fwd", *([None] * 12), None, 0, 1, 1, 1, 1, None)
 
 
+@pytest.mark.parametrize("T,B,D,H,why", [
+    (1 << 16, 1 << 15, 8, 8, "T*B reaches 2^31 (GEMM rows, reduction length)"),
+    (4, 2, 8, 1 << 15, "4H*H reaches 2^31 (the W_hh elements)"),
+    (4, 2, 1 << 18, 2048, "4H*D reaches 2^31 (the W_ih elements)"),
+    (4, 1 << 13, 8, 1 << 14, "one time step of [B, 4H] gates reaches 2^31 bytes"),
+    (4, 1 << 12, 1 << 17, 8, "one time step of [B, D] inputs reaches 2^31 bytes"),
+    (1 << 30, 1, 8, 8, "T reaches 2^30"),
+])
+def test_shapes_beyond_32_bit_indexing_are_rejected(T, B, D, H, why):
+    """Every entry point that takes (T, B, D, H) refuses, before touching a pointer or the
+    GPU, any shape whose sizes the kernels' and GEMMs' 32-bit index math cannot hold."""
+    lib = _lib.load()
+    calls = {
+        "hsl_rec_fwd": lambda: lib.hsl_rec_fwd(*([None] * 12), None, 0, T, B, D, H, None),
+        "hsl_rec_fwd_noalloc": lambda: lib.hsl_rec_fwd_noalloc(*([None] * 12), T, B, D, H, None),
+        "hsl_rec_bwd": lambda: lib.hsl_rec_bwd(*([None] * 20), None, 0, T, B, D, H, None),
+        "hsl_par_fwd": lambda: lib.hsl_par_fwd(None, None, None, None, 1e-6, None, None, None, T, B, D, H, None),
+        "hsl_par_bwd": lambda: lib.hsl_par_bwd(*([None] * 8), 1e-6, None, None, None, None, None, 0,
+                                               T, B, D, H, None),
+    }
+    if D == 8:  # the scan entry points take no D
+        calls["hsl_scan_fwd"] = lambda: lib.hsl_scan_fwd(None, None, 1e-6, None, None, T, B, H, None)
+    for name, call in calls.items():
+        rc = call()
+        assert rc == 2, (name, why, rc, lib.hsl_last_error())  # HSL_ERR_UNSUPPORTED
+        assert b"32-bit index range" in lib.hsl_last_error(), (name, lib.hsl_last_error())
+    # the largest shapes of this build's configurations pass the check (they fail later,
+    # on the null pointers, with HSL_ERR_ARG)
+    assert lib.hsl_rec_fwd(*([None] * 12), None, 0, 64, 32, 1024, 2048, None) != 2
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libhsl.so")
     monkeypatch.setattr(_lib, "_lib", None)

@@ -1,28 +1,30 @@
-// Persistent recurrent forward for a large hidden size (H = 32 U with U = 64, i.e. H = 2048,
-// configs[3]), B <= 32.  Included by recurrent.hip: it shares that file's hand-off
-// helpers and its device error word.
+// Persistent recurrent kernels for a large hidden size, H = 32 U with U = 64 (H = 2048,
+// configs[3]) or U = 32 (H = 1024, the reference's published T64 B32 D512 H1024 shape),
+// B <= 32.  Included by recurrent.hip: they share that file's hand-off helpers and its
+// device error word.
 //
-// W_hh stays in registers for the whole launch: 64 MiB at H = 2048 is 256 KB per CU over
-// 256 workgroups, where the per-step path streams it from the Infinity Cache every step
-// (_torch.py:111-120 runs one h W_hh^T product per step).  Workgroup (x, r, kb),
-// blockIdx = x + 8 (8 r + kb), sits on XCD x:
+// W_hh stays in registers for the whole launch: 4H x H floats over 256 workgroups is
+// 256 KB per CU at H = 2048 and 64 KB at H = 1024, where the per-step path streams it
+// from the Infinity Cache every step (_torch.py:111-120 runs one h W_hh^T product per
+// step).  Workgroup (x, r, kb), blockIdx = x + 8 (8 r + kb), sits on XCD x:
 //   rows: the four gates of units [4U x + U r, +U) (4U gate rows, unit-interleaved); wave w
-//         takes units [U w / 4, +U/4) of them (two row tiles of 32);
+//         takes units [U w / 4, +U/4) of them (U/32 row tiles of 32);
 //   k:    units [4U kb, +4U), all of them for every wave (4U/2 k-steps).
-// Wave w holds its 64 x 256 block of W in the accumulator registers (256 per lane) and
+// Wave w holds its U x 4U block of W in the accumulator registers (4U per lane) and
 // multiplies it with h_{t-1}[32 batch][the workgroup's 4U k units] on
 // v_mfma_f32_32x32x2_f32 (M = gate rows, N = batch).  Per step:
 //   1. receive: wave w reads h block (kb, w) (the 32 x U values that row group (kb, w)
 //      publishes) -- from another XCD for 7 of 8 workgroups -- into LDS, where all four
 //      waves read the workgroup's four blocks as product operands;
 //   2. products; each wave's accumulators are the workgroup's partial (over k block kb) of
-//      its 16 units, two slices of 8 units, sent to the workgroups (x, r, j) of its row group
-//      that run those slices' cells (XCD-local);
+//      its U/4 units, two slices of U/8 units, sent to the workgroups (x, r, j) of its row
+//      group that run those slices' cells (XCD-local);
 //   3. lane (unit su of slice kb, batch b) sums the 8 partials of its slice in source
-//      order and runs the cell; the workgroup's 256 h values are one contiguous 1 KB group
-//      of h block (x, r), gathered in LDS and published by one wave in full cache lines
-//      (scattered 4-byte device-scope stores from 256 lanes took about 1 us longer to
-//      reach the readers on the other XCDs).
+//      order and runs the cell; the workgroup's 4U h values are one contiguous group of
+//      h block (x, r) (1 KB at U = 64; at U = 32 512 bytes, 8 per lane, interleaved with
+//      the neighbouring slice's), gathered in LDS and published by one wave in whole
+//      cache lines (scattered 4-byte device-scope stores from 256 lanes took about 1 us
+//      longer to reach the readers on the other XCDs).
 // Hand-off words are 4-byte values that start out kEmpty, as in the other persistent
 // kernels.  h blocks cross XCDs: device-scope stores and loads.  Partials stay on the XCD:
 // workgroup-scope stores (sc0) when every member of the row group runs on the group's XCD.
@@ -43,8 +45,11 @@ constexpr int kWideHSlots = 4, kWidePSlots = 3;
 
 template <int U>
 struct WideShape {
+  static_assert(U == 32 || U == 64, "H = 1024 or H = 2048");
+  static constexpr int RT = U / 32;         // row tiles of 32 per wave (forward), column tiles (backward)
   static constexpr int KS = 2 * U;          // k-steps of 2 per wave (4U k units)
   static constexpr int SU = U / 8;          // units per slice (8 slices per workgroup)
+  static constexpr int WPL = U / 16;        // h words per lane of a workgroup's published group
   static constexpr int CELLS = SU * 32;     // cell lanes (slice units x 32 batch)
   static constexpr int HW = 32 * U;         // words of an h block
   static constexpr int PW = SU * 32 * 4;    // words of one partial slice (one source)
@@ -76,8 +81,10 @@ struct WFwdArgs {
 
 // Layout of an h block (32 batch x U units of a row group): the operand of k-step i of the
 // products for lane l (batch l%32, unit 2 i + l/32 of the block) is word 256 (i/4) + 4 l +
-// i%4.  A reader lane loads its 16-byte groups j at 256 j + 4 l; group j (1 KB over the
-// 64 lanes) is exactly what row-group member kb = j publishes (units 8j .. 8j+7).
+// i%4.  A reader lane loads its 16-byte groups j at 256 j + 4 l (U/8 of them).  Row-group
+// member kb publishes units U kb / 8 .. +U/8, the k-steps kb WPL .. +WPL (WPL = U/16): the
+// words 256 (kb WPL / 4) + (kb WPL) % 4 + 4 l .. +WPL of every lane l -- the whole 1 KB
+// group kb at U = 64, half of every lane's 16 bytes of group kb/2 at U = 32.
 
 // Hand-off buffers addressed as raw buffers, so that a lane moves 16 bytes in one access
 // with the coherence bits of the relaxed atomics it replaces: loads sc1 (served by the
@@ -95,6 +102,11 @@ __device__ __forceinline__ u4v quad_load(__amdgpu_buffer_rsrc_t r, unsigned word
 template <bool FAST>
 __device__ __forceinline__ void quad_store(__amdgpu_buffer_rsrc_t r, unsigned word, u4v v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)(4u * word), 0, FAST ? kCpolSc0 : kCpolSc1);
+}
+typedef unsigned u2v __attribute__((ext_vector_type(2)));
+template <bool FAST>
+__device__ __forceinline__ void pair_store(__amdgpu_buffer_rsrc_t r, unsigned word, u2v v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)(4u * word), 0, FAST ? kCpolSc0 : kCpolSc1);
 }
 
 // Polls the lane's N 16-byte groups until no word is kEmpty (nothing is awaited when
@@ -150,6 +162,33 @@ __device__ __forceinline__ void wide_ksteps4(f16v (&acc)[4], const float (&w)[4]
         "a"(w[3][1]), "v"(h[0]), "v"(h[1]), "v"(h[2]), "v"(h[3]));
 }
 
+// The same for one row tile (U = 32): k-step e of the four goes to accumulator e, so a
+// product depends on the one four instructions back.
+__device__ __forceinline__ void wide_ksteps4(f16v (&acc)[4], const float (&w)[4][1], f4 h) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_mfma_f32_32x32x2_f32 %0, %4, %8, %0\n\t"
+      "v_mfma_f32_32x32x2_f32 %1, %5, %9, %1\n\t"
+      "v_mfma_f32_32x32x2_f32 %2, %6, %10, %2\n\t"
+      "v_mfma_f32_32x32x2_f32 %3, %7, %11, %3"
+      : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])
+      : "a"(w[0][0]), "a"(w[1][0]), "a"(w[2][0]), "a"(w[3][0]), "v"(h[0]), "v"(h[1]), "v"(h[2]), "v"(h[3]));
+}
+
+// The wave's partial of 4 consecutive gate rows (or columns) of row tile rt, register group
+// q, from the accumulators: two row tiles keep tile rt in acc[rt] (even k-steps) and
+// acc[rt + 2] (odd), one row tile keeps k-step e % 4 in acc[e % 4].
+template <int RT>
+__device__ __forceinline__ f4 wide_partial(const f16v (&acc)[4], int rt, int q) {
+  f4 v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int r = 4 * q + e;
+    v[e] = RT == 2 ? acc[rt][r] + acc[rt + 2][r] : (acc[0][r] + acc[1][r]) + (acc[2][r] + acc[3][r]);
+  }
+  return v;
+}
+
 // Wait states after the last products of a step, before any instruction reads their
 // accumulators (an XDL result read by VALU, LDS or memory instructions needs up to 18 on
 // the 16-pass 32x32x2; the compiler cannot see inside the asm above, so it adds none).
@@ -165,7 +204,7 @@ template <int U, bool FAST>
 __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int r, int kb, f4* hs,
                                                   int& abort_flag) {
   using S = WideShape<U>;
-  static_assert(U == 64, "the row tiles and slices below assume U = 64");
+  constexpr int RT = S::RT, WPL = S::WPL;
   const int T = p.T, B = p.B, H = p.H;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -177,11 +216,11 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
   // file); the gate's a scales the summed product in the cell.
   const int ubase = 4 * U * x + U * r;  // first unit of the workgroup's rows
   const int kbase = 4 * U * kb;         // first k (unit) of the workgroup's k block
-  float wreg[S::KS / 4][4][2];
+  float wreg[S::KS / 4][4][RT];
   {
-    const float* rows[2];
+    const float* rows[RT];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const int rho = 32 * rt + l32, g = rho & 3, u = ubase + U / 4 * w + (rho >> 2);
       rows[rt] = p.w_hh + ((size_t)g * H + u) * H + kbase + hb;
     }
@@ -194,14 +233,14 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
-          for (int rt = 0; rt < 2; ++rt)
+          for (int rt = 0; rt < RT; ++rt)
             wreg[i4][e][rt] = rows[rt][2 * (4 * i4 + e)];
 #pragma unroll
       for (int i4 = i8; i4 < i8 + 4; ++i4)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
-          for (int rt = 0; rt < 2; ++rt) asm volatile("" : "+a"(wreg[i4][e][rt]));  // held in the accumulator file
+          for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+a"(wreg[i4][e][rt]));  // held in the accumulator file
     }
   }
 
@@ -225,21 +264,21 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
   const size_t plane = (size_t)B * H, plane4 = 4 * plane;
   const int me = blockIdx.x;
   const size_t inbox_slot = (size_t)kWideWgs * S::IW;
-  // this workgroup's 1 KB group of h block (x, r) (16-byte group j = kb of every lane) and
-  // the block (kb, w) this wave reads
+  // this workgroup's group of h block (x, r) (WPL words of every lane l at 4 l) and the
+  // block (kb, w) this wave reads
   const size_t hblock = S::HW, hslot = (size_t)kWideXcds * kWideRowSubs * S::HW;
-  float* const hown = p.hbuf + (size_t)(x * kWideRowSubs + r) * hblock + 256u * kb;
+  float* const hown = p.hbuf + (size_t)(x * kWideRowSubs + r) * hblock + 256u * (kb * WPL / 4) + (kb * WPL) % 4;
   const float* const hsrc = p.hbuf + (size_t)(kb * kWideRowSubs + w) * hblock;
   const bool h_ok = l32 < B;  // batch column of this lane in the products
   constexpr int NQ = U / 8;   // 16-byte groups a lane reads from an h block
-  __shared__ float hst[256];  // this step's h values, in the order of the 1 KB group
+  __shared__ float hst[256];  // this step's h values, in the order of the published group
   if (tid < 256) hst[tid] = 0.f;  // absent batch columns stay 0
 
   float gin[4] = {0.f, 0.f, 0.f, 0.f};
   for (int t = 0; t < T; ++t) {
     f4* const hsb = hs + (size_t)(t & 1) * S::HS_F4;
     // ---- 1. h_{t-1} of block (kb, w) into LDS: group j of block w is
-    //         hs[t&1][(8 w + j) * 64 + lane], the operands of k-steps 4j .. 4j+3,
+    //         hs[t&1][(NQ w + j) * 64 + lane], the operands of k-steps 4j .. 4j+3,
     //         h[l%32][4U kb + U w + 2 (4j + e) + l/32] -----------------------------------
     if (t == 0) {
 #pragma unroll
@@ -296,7 +335,7 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
     if (abort_flag) return;
 
     // ---- 2. products over the workgroup's k block; the accumulators are the partial
-    //         of the wave's 16 units, sent to the two slices' cell workgroups -----------
+    //         of the wave's U/4 units, sent to the two slices' cell workgroups ------------
     f16v acc[4] = {f16v{}, f16v{}, f16v{}, f16v{}};
     {
       // the operands of group i4 + 1 are read from LDS while group i4 multiplies (volatile
@@ -314,18 +353,18 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
     wide_ksteps_drain(acc);
     {
       // D layout: lane l, register 4 q + g -> gate row 8 q + 4 (l/32) + g of tile rt, batch
-      // l%32; with unit-interleaved rows that is gate g of unit U w / 4 + 8 rt + 2 q + l/32,
-      // i.e. unit 2 q + l/32 of slice 2 w + rt
+      // l%32; with unit-interleaved rows that is gate g of unit U w / 4 + 8 rt + 2 q + l/32
+      // of the row group, i.e. unit su' = that % SU of slice that / SU
       float* const ib = p.inbox + (size_t)(t % kWidePSlots) * inbox_slot;
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        const int dst = x + kWideXcds * (r * kWideKBlocks + 2 * w + rt);
-        const __amdgpu_buffer_rsrc_t d = wide_rsrc(ib + (size_t)dst * S::IW + (size_t)kb * S::PW, S::PW);
+      for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const f4 v = f4{acc[rt][4 * q] + acc[rt + 2][4 * q], acc[rt][4 * q + 1] + acc[rt + 2][4 * q + 1],
-                          acc[rt][4 * q + 2] + acc[rt + 2][4 * q + 2], acc[rt][4 * q + 3] + acc[rt + 2][4 * q + 3]};
-          if (h_ok) quad_put<FAST>(d, 4u * ((2 * q + hb) * 32 + l32), v);
+          const int ur = U / 4 * w + 8 * rt + 2 * q + hb;  // unit of the row group
+          const int dst = x + kWideXcds * (r * kWideKBlocks + ur / S::SU);
+          const __amdgpu_buffer_rsrc_t d = wide_rsrc(ib + (size_t)dst * S::IW + (size_t)kb * S::PW, S::PW);
+          const f4 v = wide_partial<RT>(acc, rt, q);
+          if (h_ok) quad_put<FAST>(d, 4u * ((ur % S::SU) * 32 + l32), v);
         }
       }
     }
@@ -352,7 +391,7 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
         const float tc = tanh_f(c);
         const float h = act[3] * tc;
         c_reg = c;
-        hst[4 * (cb + 32 * (su & 1)) + (su >> 1)] = canon_nan(h);  // word 4 l + e of the group
+        hst[WPL * (cb + 32 * (su & 1)) + (su >> 1)] = canon_nan(h);  // word 4 l + su/2 of the group
         const size_t e = (size_t)cb * H + unit;
         __builtin_nontemporal_store(h, p.h_save + (size_t)(t + 1) * plane + e);
         __builtin_nontemporal_store(c, p.c_save + (size_t)(t + 1) * plane + e);
@@ -362,13 +401,19 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
       }
     }
     lds_barrier();  // the workgroup's h values are gathered
-    if (w == 0) {   // publish the 1 KB group, then clear it in the slot of two steps ago
-      const f4 hq = *reinterpret_cast<const f4*>(&hst[4 * lane]);
+    if (w == 0) {   // publish the group, then clear it in the slot of two steps ago
       const __amdgpu_buffer_rsrc_t hp = wide_rsrc(hown + (size_t)(t % kWideHSlots) * hslot, 256);
-      quad_store<false>(hp, 4u * lane, u4v{__float_as_uint(hq[0]), __float_as_uint(hq[1]), __float_as_uint(hq[2]),
-                                           __float_as_uint(hq[3])});
       const __amdgpu_buffer_rsrc_t hc = wide_rsrc(hown + (size_t)((t + 2) % kWideHSlots) * hslot, 256);
-      quad_store<false>(hc, 4u * lane, u4v{kEmpty, kEmpty, kEmpty, kEmpty});
+      if constexpr (WPL == 4) {
+        const f4 hq = *reinterpret_cast<const f4*>(&hst[4 * lane]);
+        quad_store<false>(hp, 4u * lane, u4v{__float_as_uint(hq[0]), __float_as_uint(hq[1]), __float_as_uint(hq[2]),
+                                             __float_as_uint(hq[3])});
+        quad_store<false>(hc, 4u * lane, u4v{kEmpty, kEmpty, kEmpty, kEmpty});
+      } else {
+        const float h0v = hst[2 * lane], h1v = hst[2 * lane + 1];
+        pair_store<false>(hp, 4u * lane, u2v{__float_as_uint(h0v), __float_as_uint(h1v)});
+        pair_store<false>(hc, 4u * lane, u2v{kEmpty, kEmpty});
+      }
     }
   }
 }
@@ -414,30 +459,41 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_wide(WFwdArgs p) {
 }
 
 // ---------------------------------------------------------------------------------
-// Persistent recurrent backward for H = 2048, B <= 32: the mirror of the wide
-// forward (_torch.py:133-150: dh_t = dout_t + dg_{t+1} W_s, then the cell backward).
-// Workgroup (x, c), blockIdx = x + 8 c, sits on XCD x and holds W_hh's 1024 gate rows of
-// units [256 x, +256) (unit-interleaved) for the output columns (units) [64 c, +64); wave w
-// takes rows [256 w, +256) (units [256 x + 64 w, +64)), 2 column tiles x 128 k-steps in the
-// accumulator registers.  The rows of XCD x are the gate rows of the units whose cells run
-// on XCD x, so the broadcast of a dg (4H values per batch row, four times h) stays inside
-// the XCD; the partial sums of dh (H per batch row) cross XCDs instead.  Per iteration:
-//   1. products: wave w reads a dg_{t+1} of its 256 rows from the XCD's broadcast buffer,
+// Persistent recurrent backward for H = 32 U (U = 64: H = 2048, configs[3]; U = 32:
+// H = 1024), B <= 32: the mirror of the wide forward (_torch.py:133-150: dh_t = dout_t +
+// dg_{t+1} W_s, then the cell backward).  Workgroup (x, c), blockIdx = x + 8 c, sits on XCD
+// x and holds W_hh's 16U gate rows of units [4U x, +4U) (unit-interleaved) for the output
+// columns (units) [U c, +U); wave w takes rows [4U w, +4U) (units [4U x + U w, +U)), U/32
+// column tiles x 2U k-steps in the accumulator registers.  The rows of XCD x are the gate
+// rows of the units whose cells run on XCD x, so the broadcast of a dg (4H values per batch
+// row, four times h) stays inside the XCD; the partial sums of dh (H per batch row) cross
+// XCDs instead.  Per iteration:
+//   1. products: wave w reads a dg_{t+1} of its 4U rows from the XCD's broadcast buffer,
 //      8 groups at a time (the next 8 are requested before the current ones multiply);
-//   2. the four waves' partials [64 columns x 32 batch] are summed in LDS and sent to the
-//      reducing workgroups of the columns' XCD (c / 4): slice sl of 8 units goes to
+//   2. the four waves' partials [U columns x 32 batch] are summed in LDS and sent to the
+//      reducing workgroups of the columns' XCD (c / 4): slice sl of U/8 units goes to
 //      workgroup (c / 4, 8 (c % 4) + sl), whose inbox holds the 8 row XCDs' partials;
 //   3. reducer lane (unit su of slice s, batch b) sums them in XCD order, adds dout_t (and
 //      dh_n at t = T-1), runs the cell backward with the dc carry in a register, stores
 //      dgates_t and publishes a_g dg_t (the a-scaling of W_s moved to the operand) to the
-//      XCD's broadcast buffer: its 8 units x 4 gates x 32 batch are one contiguous 4 KB
-//      group, gathered in LDS and written in full cache lines.
+//      XCD's broadcast buffer: its U/8 units x 4 gates x 32 batch are one contiguous group
+//      of 16U words, gathered in LDS and written in full cache lines.
 // One more product after t = 0 gives dh0.  Slots as in the forward: broadcast of iteration
 // k in slot k%4, its owner clears slot (k+2)%4 after publishing; partials of iteration k in
 // slot k%3, cleared by their one reader.
-constexpr int kWideBRows = 1024;             // gate rows held per XCD
-constexpr int kWideBInbox = 8 * 32 * 8;      // inbox words of a reducer per slot: [src x][batch][unit]
-constexpr int kWideBLdsBytes = 4 * 2048 * 4 + 1024 * 4;  // wave partials + the gathered dg group
+template <int U>
+struct WideBShape {
+  static constexpr int CT = U / 32;           // column tiles of 32 per wave
+  static constexpr int SU = U / 8;            // units per reducer slice
+  static constexpr int ROWS = 16 * U;         // gate rows held per XCD
+  static constexpr int WROWS = 4 * U;         // gate rows per wave
+  static constexpr int NQ = U / 2;            // 16-byte groups of a wave's dg operands (2U k-steps)
+  static constexpr int INBOX = 8 * 32 * SU;   // inbox words of a reducer per slot: [src x][batch][unit]
+  static constexpr int GROUP = 16 * U;        // words of a reducer's published dg group
+  static constexpr int RED = 32 * U;          // floats of one wave's partials [U columns][32 batch]
+  static constexpr int LDS_BYTES = 4 * (4 * RED + GROUP);  // wave partials + the gathered dg group
+  static constexpr int REDUCERS = 32 * SU;    // reducer lanes (unit, batch) of a workgroup
+};
 
 struct WBwdArgs {
   const float* dout;    // [T][B][H]
@@ -451,8 +507,8 @@ struct WBwdArgs {
   float* dgates;        // [T][B][4H]
   float* dh0;           // [B][H] or null
   float* dc0;           // [B][H] or null
-  float* dgbuf;         // [4 slots][8 XCDs][1024 rows x 32 batch]
-  float* inbox;         // [3 slots][256 workgroups][kWideBInbox]
+  float* dgbuf;         // [4 slots][8 XCDs][16U rows x 32 batch]
+  float* inbox;         // [3 slots][256 workgroups][INBOX]
   unsigned long long* hello;  // [8][32]
   int* err;
   int T, B, H;
@@ -460,50 +516,54 @@ struct WBwdArgs {
   long long spin;
 };
 
-// word of (local row rho, batch b) in an XCD's broadcast buffer: wave w = rho / 256 reads
-// group j (k-steps 4j .. 4j+3 of its rows) at 8192 w + 256 j + 4 l
+// word of (local row rho, batch b) in an XCD's broadcast buffer: wave w = rho / 4U reads
+// group j (k-steps 4j .. 4j+3 of its rows) at 128U w + 256 j + 4 l
+template <int U>
 __device__ __forceinline__ unsigned wideb_pos(int rho, int b) {
-  const int w = rho >> 8, rl = rho & 255, i = rl >> 1, l = b + 32 * (rl & 1);
-  return 8192u * w + 256u * (i >> 2) + 4u * l + (i & 3);
+  const int w = rho / (4 * U), rl = rho % (4 * U), i = rl >> 1, l = b + 32 * (rl & 1);
+  return 128u * U * w + 256u * (i >> 2) + 4u * l + (i & 3);
 }
 
-template <bool FAST>
+template <int U, bool FAST>
 __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int c, float* red, float* gst,
                                                   int& abort_flag) {
+  using S = WideBShape<U>;
+  constexpr int CT = S::CT, SU = S::SU;
   const int T = p.T, B = p.B, H = p.H;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hb = lane >> 5, l32 = lane & 31;
-  const int ubase = 256 * x;  // first unit of the XCD's rows
+  const int ubase = 4 * U * x;  // first unit of the XCD's rows
 
   // W_hh^T block of this wave: column tile ct, k-step 4 i4 + e -> column m = l%32 of the
-  // tile (unit 64 c + 32 ct + m), row rho = 256 w + 2 (4 i4 + e) + l/32 (unit ubase + rho/4,
+  // tile (unit U c + 32 ct + m), row rho = 4U w + 2 (4 i4 + e) + l/32 (unit ubase + rho/4,
   // gate rho % 4); unscaled, a multiplies the dg operand instead
-  float wreg[32][4][2];
+  float wreg[S::NQ][4][CT];
 #pragma unroll
-  for (int i8 = 0; i8 < 32; i8 += 4) {
+  for (int i8 = 0; i8 < S::NQ; i8 += 4) {
 #pragma unroll
     for (int i4 = i8; i4 < i8 + 4; ++i4)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int rho = 256 * w + 2 * (4 * i4 + e) + hb;
-        const float* row = p.w_hh + ((size_t)(rho & 3) * H + ubase + (rho >> 2)) * H + 64 * c + l32;
+        const int rho = S::WROWS * w + 2 * (4 * i4 + e) + hb;
+        const float* row = p.w_hh + ((size_t)(rho & 3) * H + ubase + (rho >> 2)) * H + U * c + l32;
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) wreg[i4][e][ct] = row[32 * ct];
+        for (int ct = 0; ct < CT; ++ct) wreg[i4][e][ct] = row[32 * ct];
       }
 #pragma unroll
     for (int i4 = i8; i4 < i8 + 4; ++i4)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) asm volatile("" : "+a"(wreg[i4][e][ct]));  // held in the accumulator file
+        for (int ct = 0; ct < CT; ++ct) asm volatile("" : "+a"(wreg[i4][e][ct]));  // held in the accumulator file
   }
 
-  // reducer lane: unit su of this workgroup's slice (slice s = c of XCD x: units ubase + 8 c
-  // + su), batch cb
+  // reducer lane (tid < REDUCERS): unit su of this workgroup's slice (slice c of XCD x:
+  // units ubase + SU c + su), batch cb
   const int su = tid >> 5, cb = tid & 31;
-  const bool c_ok = cb < B;
-  const int unit = ubase + 8 * c + su;
+  const bool reducer = tid < S::REDUCERS;
+  const bool c_ok = reducer && cb < B;
+  const int unit = ubase + SU * c + su;
   float ag[4];
 #pragma unroll
   for (int g = 0; g < 4; ++g) ag[g] = p.a[g];
@@ -511,21 +571,21 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
   if (c_ok && p.dc_n) dc = p.dc_n[(size_t)cb * H + unit];
   const size_t plane = (size_t)B * H, plane4 = 4 * plane;
   const bool h_ok = l32 < B;
-  // broadcast buffer of this XCD; this workgroup's 4 KB group in it
-  const size_t bslot = (size_t)kWideXcds * kWideBRows * 32;
-  float* const bx = p.dgbuf + (size_t)x * kWideBRows * 32;
-  // send: lane (c4 = tid / 32, batch sb = tid % 32) sends columns 8 c4 .. 8 c4 + 7 (slice c4)
-  // to reducer (c / 4, 8 (c % 4) + c4), inbox [src x][sb][8 units]
+  // broadcast buffer of this XCD; this workgroup's group in it
+  const size_t bslot = (size_t)kWideXcds * S::ROWS * 32;
+  float* const bx = p.dgbuf + (size_t)x * S::ROWS * 32;
+  // send: lane (c4 = tid / 32, batch sb = tid % 32) sends columns SU c4 .. +SU (slice c4)
+  // to reducer (c / 4, 8 (c % 4) + c4), inbox [src x][sb][SU units]
   const int c4 = tid >> 5, sb = tid & 31;
   const int dst = (c >> 2) + kWideXcds * (8 * (c & 3) + c4);
-  const size_t islot = (size_t)kWideWgs * kWideBInbox;
+  const size_t islot = (size_t)kWideWgs * S::INBOX;
   for (int k = 0; k <= T; ++k) {
     const int t = T - 1 - k;  // the cell's step (-1 after the last product: dh0)
     float dsum = 0.f;
     if (k > 0) {
       // ---- 1. products with a_g dg_{t+1} of the wave's rows ---------------------------
       const __amdgpu_buffer_rsrc_t src =
-          wide_rsrc(bx + (size_t)((k - 1) % kWideHSlots) * bslot + 8192u * w, 8192);
+          wide_rsrc(bx + (size_t)((k - 1) % kWideHSlots) * bslot + 128u * U * w, 128 * U);
       f16v acc[4] = {f16v{}, f16v{}, f16v{}, f16v{}};
       u4v qa[8], qb[8];
       auto issue = [&](u4v (&q)[8], int jb) {
@@ -555,54 +615,58 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
                        f4{__uint_as_float(q[j][0]), __uint_as_float(q[j][1]), __uint_as_float(q[j][2]),
                           __uint_as_float(q[j][3])});
       };
+      static_assert(S::NQ == 16 || S::NQ == 32, "two or four batches of eight groups");
       issue(qa, 0);
       if (!settle(qa, 0)) return;
       issue(qb, 8);
       mult(qa, 0);
       if (!settle(qb, 8)) return;
-      issue(qa, 16);
-      mult(qb, 8);
-      if (!settle(qa, 16)) return;
-      issue(qb, 24);
-      mult(qa, 16);
-      if (!settle(qb, 24)) return;
-      mult(qb, 24);
+      if constexpr (S::NQ == 32) {
+        issue(qa, 16);
+        mult(qb, 8);
+        if (!settle(qa, 16)) return;
+        issue(qb, 24);
+        mult(qa, 16);
+        if (!settle(qb, 24)) return;
+        mult(qb, 24);
+      } else {
+        mult(qb, 8);
+      }
       wide_ksteps_drain(acc);
       // ---- 2. the four waves' partials summed in LDS, sent to the reducers ------------
-      // D layout: lane l, register 4 q + e -> column 8 q + 4 (l/32) + e of tile ct, batch l%32
+      // D layout: lane l, register 4 q + e -> column 8 q + 4 (l/32) + e of tile ct, batch
+      // l%32; red[w][column quad][batch] holds 4 columns
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
+      for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          *reinterpret_cast<f4*>(&red[((w * 16 + 8 * ct + 2 * q + hb) * 32 + l32) * 4]) =
-              f4{acc[ct][4 * q] + acc[ct + 2][4 * q], acc[ct][4 * q + 1] + acc[ct + 2][4 * q + 1],
-                 acc[ct][4 * q + 2] + acc[ct + 2][4 * q + 2], acc[ct][4 * q + 3] + acc[ct + 2][4 * q + 3]};
+          *reinterpret_cast<f4*>(&red[((w * (U / 4) + 8 * ct + 2 * q + hb) * 32 + l32) * 4]) =
+              wide_partial<CT>(acc, ct, q);
       lds_barrier();
       if (abort_flag) return;
       if (sb < B) {
-        f4 s0 = f4{0.f, 0.f, 0.f, 0.f}, s1 = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ww = 0; ww < 4; ++ww) {
-          s0 = s0 + *reinterpret_cast<const f4*>(&red[((ww * 16 + 2 * c4) * 32 + sb) * 4]);
-          s1 = s1 + *reinterpret_cast<const f4*>(&red[((ww * 16 + 2 * c4 + 1) * 32 + sb) * 4]);
-        }
         const __amdgpu_buffer_rsrc_t d =
-            wide_rsrc(p.inbox + (size_t)((k - 1) % kWidePSlots) * islot + (size_t)dst * kWideBInbox, kWideBInbox);
-        quad_put<false>(d, (unsigned)(x * 256 + sb * 8), s0);
-        quad_put<false>(d, (unsigned)(x * 256 + sb * 8 + 4), s1);
+            wide_rsrc(p.inbox + (size_t)((k - 1) % kWidePSlots) * islot + (size_t)dst * S::INBOX, S::INBOX);
+#pragma unroll
+        for (int qq = 0; qq < SU / 4; ++qq) {
+          f4 sum = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ww = 0; ww < 4; ++ww)
+            sum = sum + *reinterpret_cast<const f4*>(&red[((ww * (U / 4) + (SU / 4) * c4 + qq) * 32 + sb) * 4]);
+          quad_put<false>(d, (unsigned)(x * 32 * SU + sb * SU + 4 * qq), sum);
+        }
       }
       // ---- 3a. the reducer's sum of the 8 row XCDs' partials --------------------------
       if (c_ok) {
         const __amdgpu_buffer_rsrc_t ib =
-            wide_rsrc(p.inbox + (size_t)((k - 1) % kWidePSlots) * islot + (size_t)blockIdx.x * kWideBInbox,
-                      kWideBInbox);
+            wide_rsrc(p.inbox + (size_t)((k - 1) % kWidePSlots) * islot + (size_t)blockIdx.x * S::INBOX, S::INBOX);
         unsigned v[8];
         const long long t0 = wall_clock64();
         while (true) {
           unsigned m = 0u;
 #pragma unroll
           for (int sx = 0; sx < 8; ++sx) {
-            v[sx] = __builtin_amdgcn_raw_buffer_load_b32(ib, (int)(4u * (sx * 256 + cb * 8 + su)), 0, kCpolSc1);
+            v[sx] = __builtin_amdgcn_raw_buffer_load_b32(ib, (int)(4u * (sx * 32 * SU + cb * SU + su)), 0, kCpolSc1);
             m = max(m, v[sx]);
           }
           if (__all(m != kEmpty)) break;
@@ -613,7 +677,7 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
         }
 #pragma unroll
         for (int sx = 0; sx < 8; ++sx)
-          __builtin_amdgcn_raw_buffer_store_b32(kEmpty, ib, (int)(4u * (sx * 256 + cb * 8 + su)), 0, kCpolSc1);
+          __builtin_amdgcn_raw_buffer_store_b32(kEmpty, ib, (int)(4u * (sx * 32 * SU + cb * SU + su)), 0, kCpolSc1);
         dsum = __uint_as_float(v[0]);
 #pragma unroll
         for (int sx = 1; sx < 8; ++sx) dsum += __uint_as_float(v[sx]);
@@ -637,19 +701,23 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
 #pragma unroll
       for (int g = 0; g < 4; ++g) __builtin_nontemporal_store(d[g], dg + (size_t)g * H);
     }
-    // gather: rows 4 (8 c + su) + g of this XCD are word 1024 c + (wideb_pos - 1024 c) of the
-    // buffer; absent batch rows publish 0
+    // gather: rows 4 (SU c + su) + g of this XCD are word GROUP c + (wideb_pos - GROUP c) of
+    // the buffer; absent batch rows publish 0
+    if (reducer) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      gst[wideb_pos(4 * (8 * c + su) + g, cb) - 1024u * c] = c_ok ? canon_nan(ag[g] * d[g]) : 0.f;
+      for (int g = 0; g < 4; ++g)
+        gst[wideb_pos<U>(4 * (SU * c + su) + g, cb) - (unsigned)S::GROUP * c] = c_ok ? canon_nan(ag[g] * d[g]) : 0.f;
+    }
     lds_barrier();
     if (abort_flag) return;
-    {
+    if (tid < S::GROUP / 4) {
       const f4 qv = *reinterpret_cast<const f4*>(&gst[4 * tid]);
-      const __amdgpu_buffer_rsrc_t bp = wide_rsrc(bx + (size_t)(k % kWideHSlots) * bslot + 1024u * c, 1024);
+      const __amdgpu_buffer_rsrc_t bp =
+          wide_rsrc(bx + (size_t)(k % kWideHSlots) * bslot + (size_t)S::GROUP * c, S::GROUP);
       quad_store<FAST>(bp, 4u * tid, u4v{__float_as_uint(qv[0]), __float_as_uint(qv[1]), __float_as_uint(qv[2]),
                                          __float_as_uint(qv[3])});
-      const __amdgpu_buffer_rsrc_t bc = wide_rsrc(bx + (size_t)((k + 2) % kWideHSlots) * bslot + 1024u * c, 1024);
+      const __amdgpu_buffer_rsrc_t bc =
+          wide_rsrc(bx + (size_t)((k + 2) % kWideHSlots) * bslot + (size_t)S::GROUP * c, S::GROUP);
       quad_store<FAST>(bc, 4u * tid, u4v{kEmpty, kEmpty, kEmpty, kEmpty});
     }
   }
@@ -657,10 +725,12 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
 
 // After an abort the reducer lanes set what they own to NaN: dgates of their unit and batch
 // row at every step, and dh0 / dc0.
+template <int U>
 __device__ void poison_wide_bwd(const WBwdArgs& p, int x, int c) {
+  using S = WideBShape<U>;
   const int tid = threadIdx.x, su = tid >> 5, cb = tid & 31;
-  if (cb >= p.B) return;
-  const int unit = 256 * x + 8 * c + su, H = p.H;
+  if (tid >= S::REDUCERS || cb >= p.B) return;
+  const int unit = 4 * U * x + S::SU * c + su, H = p.H;
   const float nan = __uint_as_float(0x7FC00000u);
   const size_t e = (size_t)cb * H + unit;
   if (p.dh0) p.dh0[e] = nan;
@@ -669,7 +739,9 @@ __device__ void poison_wide_bwd(const WBwdArgs& p, int x, int c) {
     for (int g = 0; g < 4; ++g) p.dgates[((size_t)t * p.B + cb) * 4 * H + g * H + unit] = nan;
 }
 
+template <int U>
 __global__ __launch_bounds__(256, 1) void rec_bwd_wide(WBwdArgs p) {
+  using S = WideBShape<U>;
   extern __shared__ float wide_lds[];  // wave partials, then the gathered dg group (padded: one workgroup per CU)
   __shared__ int abort_flag;
   const int x = blockIdx.x % kWideXcds, c = blockIdx.x / kWideXcds;
@@ -679,10 +751,10 @@ __global__ __launch_bounds__(256, 1) void rec_bwd_wide(WBwdArgs p) {
                     !p.device_scope;
   if (!abort_flag) {
     if (fast)
-      rec_bwd_wide_body<true>(p, x, c, wide_lds, wide_lds + 4 * 2048, abort_flag);
+      rec_bwd_wide_body<U, true>(p, x, c, wide_lds, wide_lds + 4 * S::RED, abort_flag);
     else
-      rec_bwd_wide_body<false>(p, x, c, wide_lds, wide_lds + 4 * 2048, abort_flag);
+      rec_bwd_wide_body<U, false>(p, x, c, wide_lds, wide_lds + 4 * S::RED, abort_flag);
   }
   lds_barrier();
-  if (abort_flag) poison_wide_bwd(p, x, c);
+  if (abort_flag) poison_wide_bwd<U>(p, x, c);
 }

@@ -2126,31 +2126,57 @@ int plan_persistent(int B, int H, int D, bool bwd, PersistentPlan* pl) {
   return HSL_OK;
 }
 
-// The W_hh-resident forward for large H (rec_wide.h): H = 2048, B <= 32, eight XCDs and all
-// 256 workgroups resident at once (one per CU).
+// The W_hh-resident kernels for large H (rec_wide.h): H = 32 U with U = 64 (2048) or 32
+// (1024), B <= 32, eight XCDs and all 256 workgroups resident at once (one per CU).
 struct WidePlan {
   bool ok = false;
+  int U = 0;
 };
 
-// the double-buffered h blocks (64 KB), padded so that one workgroup fits per CU
-constexpr size_t kWideLdsBytes =
-    WideShape<64>::LDS_BYTES > (size_t)kPadLdsBytes ? WideShape<64>::LDS_BYTES : (size_t)kPadLdsBytes;
+// dynamic LDS of the wide kernels, padded so that one workgroup fits per CU: the forward's
+// double-buffered h blocks, the backward's wave partials and gathered dg group
+template <int U>
+constexpr size_t wide_fwd_lds() {
+  return WideShape<U>::LDS_BYTES > (size_t)kPadLdsBytes ? WideShape<U>::LDS_BYTES : (size_t)kPadLdsBytes;
+}
+template <int U>
+constexpr size_t wide_bwd_lds() {
+  return (size_t)WideBShape<U>::LDS_BYTES > (size_t)kPadLdsBytes ? (size_t)WideBShape<U>::LDS_BYTES
+                                                                  : (size_t)kPadLdsBytes;
+}
 
-constexpr size_t kWideBwdLdsBytes =
-    (size_t)kWideBLdsBytes > (size_t)kPadLdsBytes ? (size_t)kWideBLdsBytes : (size_t)kPadLdsBytes;
+// exchange words of the wide kernels: forward h blocks then partial inboxes; backward dg
+// broadcasts then partial inboxes (floats)
+size_t wide_fwd_hfloats(int U) { return (size_t)kWideHSlots * kWideXcds * kWideRowSubs * 32 * U; }
+size_t wide_fwd_floats(int U) {
+  return wide_fwd_hfloats(U) + (size_t)kWidePSlots * kWideWgs * kWideKBlocks * (U / 8) * 32 * 4;
+}
+size_t wide_bwd_bfloats(int U) { return (size_t)kWideHSlots * kWideXcds * (16 * U) * 32; }
+size_t wide_bwd_floats(int U) { return wide_bwd_bfloats(U) + (size_t)kWidePSlots * kWideWgs * (8 * 32 * (U / 8)); }
+
+template <int U>
+int wide_occupancy(bool bwd, int* occ) {
+  if (bwd)
+    HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(occ, rec_bwd_wide<U>, 256, wide_bwd_lds<U>()));
+  else
+    HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(occ, rec_fwd_wide<U>, 256, wide_fwd_lds<U>()));
+  return HSL_OK;
+}
 
 int plan_wide(int B, int H, bool bwd, WidePlan* pl) {
   *pl = WidePlan{};
-  if (recurrent_path_mode() == 1 || B < 1 || B > 32 || H != 2048) return HSL_OK;
+  if (recurrent_path_mode() == 1 || B < 1 || B > 32 || (H != 2048 && H != 1024)) return HSL_OK;
   DeviceInfo di;
   HSL_CHECK(device_info(&di));
   if (di.num_xcds != kWideXcds || di.num_cus < kWideWgs) return HSL_OK;
+  const int U = H / 32;
   int occ = 0;
-  if (bwd)
-    HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, rec_bwd_wide, 256, kWideBwdLdsBytes));
+  if (U == 64)
+    HSL_CHECK(wide_occupancy<64>(bwd, &occ));
   else
-    HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, rec_fwd_wide<64>, 256, kWideLdsBytes));
+    HSL_CHECK(wide_occupancy<32>(bwd, &occ));
   pl->ok = occ >= 1 && (long)occ * di.num_cus >= kWideWgs;
+  pl->U = U;
   return HSL_OK;
 }
 
@@ -2251,10 +2277,9 @@ size_t carve_fwd(void* ws, size_t cap, int T, int B, int H, FwdNeeds nd, FwdWs* 
     o->hello = c.take<unsigned long long>(o->hwords);
   }
   if (nd.gih) o->gih = c.take<float>((size_t)T * B * 4 * H);
-  if (nd.wide && H == 2048) {
-    const size_t U = 64;
-    o->whfloats = (size_t)kWideHSlots * kWideXcds * kWideRowSubs * 32 * U;
-    o->wfloats = o->whfloats + (size_t)kWidePSlots * kWideWgs * kWideKBlocks * (U / 8) * 32 * 4;
+  if (nd.wide && (H == 2048 || H == 1024)) {
+    o->whfloats = wide_fwd_hfloats(H / 32);
+    o->wfloats = wide_fwd_floats(H / 32);
     o->wbuf = c.take<float>(o->wfloats);
     o->whello = c.take<unsigned long long>(kWideWgs);
   }
@@ -2358,8 +2383,8 @@ size_t carve_bwd(void* ws, size_t cap, int T, int B, int D, int H, BwdNeeds nd, 
     o->pbuf = c.take<float>(o->pfloats);
     o->hello = c.take<unsigned long long>(o->hwords);
   }
-  if (nd.wide && H == 2048) {
-    o->wfloats = (size_t)kWideHSlots * kWideXcds * kWideBRows * 32 + (size_t)kWidePSlots * kWideWgs * kWideBInbox;
+  if (nd.wide && (H == 2048 || H == 1024)) {
+    o->wfloats = wide_bwd_floats(H / 32);
     o->wbuf = c.take<float>(o->wfloats);
     o->whello = c.take<unsigned long long>(kWideWgs);
   }
@@ -2542,7 +2567,10 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
     WFwdArgs wa{w.gih, w_hh, b_hh, a, h0, c0, h_save, c_save, gact, tanh_c, w.wbuf, w.wbuf + w.whfloats, w.whello,
                 w.err, T, B, H, exchange_scope_mode(), spin_timeout_ticks()};
     const int slot = timing_begin(kTimeRecFwd, s);
-    hipLaunchKernelGGL(rec_fwd_wide<64>, dim3(kWideWgs), dim3(256), kWideLdsBytes, s, wa);
+    if (wp.U == 64)
+      hipLaunchKernelGGL(rec_fwd_wide<64>, dim3(kWideWgs), dim3(256), wide_fwd_lds<64>(), s, wa);
+    else
+      hipLaunchKernelGGL(rec_fwd_wide<32>, dim3(kWideWgs), dim3(256), wide_fwd_lds<32>(), s, wa);
     HSL_HIP(hipGetLastError());
     timing_end(slot, s);
     note_recurrent_path(3);
@@ -2701,10 +2729,13 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
   } else if (wp.ok) {
     note_backward_fused(0);
     WBwdArgs wa{dout, dh_n, dc_n, c_save, gact, tanh_c, w_hh, a, w.dgates, dh0, dc0, w.wbuf,
-                w.wbuf + (size_t)kWideHSlots * kWideXcds * kWideBRows * 32, w.whello, w.err, T, B, H,
+                w.wbuf + wide_bwd_bfloats(wp.U), w.whello, w.err, T, B, H,
                 exchange_scope_mode(), spin_timeout_ticks()};
     const int slot = timing_begin(kTimeRecBwd, s);
-    hipLaunchKernelGGL(rec_bwd_wide, dim3(kWideWgs), dim3(256), kWideBwdLdsBytes, s, wa);
+    if (wp.U == 64)
+      hipLaunchKernelGGL(rec_bwd_wide<64>, dim3(kWideWgs), dim3(256), wide_bwd_lds<64>(), s, wa);
+    else
+      hipLaunchKernelGGL(rec_bwd_wide<32>, dim3(kWideWgs), dim3(256), wide_bwd_lds<32>(), s, wa);
     HSL_HIP(hipGetLastError());
     timing_end(slot, s);
     hipLaunchKernelGGL(colsum_time_kernel, dim3(grid_for(plane4)), dim3(256), 0, s, w.dgates, w.db_part, T,

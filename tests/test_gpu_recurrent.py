@@ -182,16 +182,23 @@ def test_config3_wide_forward(dev):
 
 def test_published_h1024_shape(dev):
     """(T64, B32, D512, H1024): the reference's published shape between configs[2] and
-    configs[3] (README.md:78), on the path the library picks for it."""
-    check(64, 32, 512, 1024, dev, 0)
+    configs[3] (README.md:78), on the W_hh-resident kernels for H = 1024 (path 3)."""
+    check(64, 32, 512, 1024, dev, 0, fwd_path=3)
+    assert prlstm_amd.last_recurrent_path() == 3
 
 
+def test_h1024_on_the_per_step_path(dev):
+    """The same shape on the one-launch-per-step path, which the wide kernels replace."""
+    check(64, 32, 512, 1024, dev, 1)
+
+
+@pytest.mark.parametrize("H", [1024, 2048])
 @pytest.mark.parametrize("scope", [0, 1])
-def test_wide_forward_partial_batch_hx(dev, scope):
-    """The wide forward with B < 32 (absent batch columns), h0/c0 given, a ~ U(0, 0.5), and
-    with device-scope stores for the partial exchange (scope 1)."""
+def test_wide_forward_partial_batch_hx(dev, scope, H):
+    """The wide kernels (both widths) with B < 32 (absent batch columns), h0/c0 given,
+    a ~ U(0, 0.5), and with device-scope stores for the partial exchange (scope 1)."""
     prlstm_amd.set_exchange_scope(scope)
-    check(6, 20, 64, 2048, dev, 0, a=[0.3, 0.5, 0.1, 0.2], with_hx=True, fwd_path=3)
+    check(6, 20, 64, H, dev, 0, a=[0.3, 0.5, 0.1, 0.2], with_hx=True, fwd_path=3)
     assert prlstm_amd.last_recurrent_path() == 3
 
 

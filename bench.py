@@ -238,6 +238,8 @@ def bench_modes(args):
     dev = torch.device("cuda", 0)
     res = []
     for name, t, b, d, h, par, a, dt in MODE_CONFIGS:
+        if args.mode_filter and not any(f in name for f in args.mode_filter.split(",")):
+            continue
         torch.manual_seed(0)
         m = HeadStartLSTM(d, h, a_init=0.0 if a is None else a, parallel=par)
         if a is None:  # the configs[2] variant: a drawn right after init
@@ -359,6 +361,9 @@ def main():
     ap.add_argument("--no-cpu-parallel", action="store_true", help="skip the parallel-mode CPU baseline")
     ap.add_argument("--no-scan", action="store_true")
     ap.add_argument("--no-modes", action="store_true", help="skip the per-config table of both modes")
+    ap.add_argument("--mode-filter", default="",
+                    help="run only the modes rows whose name contains one of these comma-separated "
+                         "strings (e.g. 'configs[3],README.md:78' for a kernel trace of those steps)")
     ap.add_argument("--no-split-off", action="store_true",
                     help="skip the headline step with the split products switched off")
     args = ap.parse_args()

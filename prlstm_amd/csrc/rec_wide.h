@@ -475,7 +475,9 @@ __global__ __launch_bounds__(256, 1) void rec_fwd_wide(WFwdArgs p) {
 //      workgroup (c / 4, 8 (c % 4) + sl), whose inbox holds the 8 row XCDs' partials;
 //   3. reducer lane (unit su of slice s, batch b) sums them in XCD order, adds dout_t (and
 //      dh_n at t = T-1), runs the cell backward with the dc carry in a register, stores
-//      dgates_t and publishes a_g dg_t (the a-scaling of W_s moved to the operand) to the
+//      dgates_t, adds it to the lane's fp64 sums over t (the bias gradients' partials,
+//      _torch.py:163, written at the end) and publishes a_g dg_t (the a-scaling of W_s
+//      moved to the operand) to the
 //      XCD's broadcast buffer: its U/8 units x 4 gates x 32 batch are one contiguous group
 //      of 16U words, gathered in LDS and written in full cache lines.
 // One more product after t = 0 gives dh0.  Slots as in the forward: broadcast of iteration
@@ -505,6 +507,7 @@ struct WBwdArgs {
   const float* w_hh;
   const float* a;
   float* dgates;        // [T][B][4H]
+  double* db_part;      // [B][4H]: sum over t of dgates, in fp64
   float* dh0;           // [B][H] or null
   float* dc0;           // [B][H] or null
   float* dgbuf;         // [4 slots][8 XCDs][16U rows x 32 batch]
@@ -568,6 +571,7 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
 #pragma unroll
   for (int g = 0; g < 4; ++g) ag[g] = p.a[g];
   float dc = 0.f;
+  double dbacc[4] = {0.0, 0.0, 0.0, 0.0};
   if (c_ok && p.dc_n) dc = p.dc_n[(size_t)cb * H + unit];
   const size_t plane = (size_t)B * H, plane4 = 4 * plane;
   const bool h_ok = l32 < B;
@@ -683,10 +687,12 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
         for (int sx = 1; sx < 8; ++sx) dsum += __uint_as_float(v[sx]);
       }
     }
-    if (k == T) {  // dh of h0, and the carry into c0
+    if (k == T) {  // dh of h0, the carry into c0, the bias partials
       if (c_ok) {
         if (p.dh0) p.dh0[(size_t)cb * H + unit] = dsum;
         if (p.dc0) p.dc0[(size_t)cb * H + unit] = dc;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) p.db_part[(size_t)cb * 4 * H + g * H + unit] = dbacc[g];
       }
       break;
     }
@@ -699,7 +705,10 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
       cell_bwd(dh, dc, p.c_save[(size_t)t * plane + e], ga[0], ga[1], ga[2], ga[3], p.tanh_c[(size_t)t * plane + e], d);
       float* const dg = p.dgates + (size_t)t * plane4 + (size_t)cb * 4 * H + unit;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) __builtin_nontemporal_store(d[g], dg + (size_t)g * H);
+      for (int g = 0; g < 4; ++g) {
+        __builtin_nontemporal_store(d[g], dg + (size_t)g * H);
+        dbacc[g] += (double)d[g];
+      }
     }
     // gather: rows 4 (SU c + su) + g of this XCD are word GROUP c + (wideb_pos - GROUP c) of
     // the buffer; absent batch rows publish 0
@@ -724,7 +733,7 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
 }
 
 // After an abort the reducer lanes set what they own to NaN: dgates of their unit and batch
-// row at every step, and dh0 / dc0.
+// row at every step, the bias partials, and dh0 / dc0.
 template <int U>
 __device__ void poison_wide_bwd(const WBwdArgs& p, int x, int c) {
   using S = WideBShape<U>;
@@ -735,6 +744,7 @@ __device__ void poison_wide_bwd(const WBwdArgs& p, int x, int c) {
   const size_t e = (size_t)cb * H + unit;
   if (p.dh0) p.dh0[e] = nan;
   if (p.dc0) p.dc0[e] = nan;
+  for (int g = 0; g < 4; ++g) p.db_part[(size_t)cb * 4 * H + g * H + unit] = (double)nan;
   for (int t = 0; t < p.T; ++t)
     for (int g = 0; g < 4; ++g) p.dgates[((size_t)t * p.B + cb) * 4 * H + g * H + unit] = nan;
 }

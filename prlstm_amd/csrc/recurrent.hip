@@ -2728,7 +2728,7 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     note_backward_fused(fused_ih ? 2 : fused ? 1 : 0);
   } else if (wp.ok) {
     note_backward_fused(0);
-    WBwdArgs wa{dout, dh_n, dc_n, c_save, gact, tanh_c, w_hh, a, w.dgates, dh0, dc0, w.wbuf,
+    WBwdArgs wa{dout, dh_n, dc_n, c_save, gact, tanh_c, w_hh, a, w.dgates, w.db_part, dh0, dc0, w.wbuf,
                 w.wbuf + wide_bwd_bfloats(wp.U), w.whello, w.err, T, B, H,
                 exchange_scope_mode(), spin_timeout_ticks()};
     const int slot = timing_begin(kTimeRecBwd, s);
@@ -2738,9 +2738,6 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
       hipLaunchKernelGGL(rec_bwd_wide<32>, dim3(kWideWgs), dim3(256), wide_bwd_lds<32>(), s, wa);
     HSL_HIP(hipGetLastError());
     timing_end(slot, s);
-    hipLaunchKernelGGL(colsum_time_kernel, dim3(grid_for(plane4)), dim3(256), 0, s, w.dgates, w.db_part, T,
-                       (int)plane4);
-    HSL_HIP(hipGetLastError());
     note_recurrent_path(3);
   } else {
     note_backward_fused(0);

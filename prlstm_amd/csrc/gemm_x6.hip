@@ -98,8 +98,9 @@ __device__ __forceinline__ float swap_pair_lane(float v) {
 //      swap half their values, so the even lane writes rows 0-1 and the odd lane rows 2-3,
 //      each as (k even, k odd) pairs.
 // `kend` bounds k (the end of this workgroup's split): masked loads zero k >= kend and
-// rows >= rows, reading clamped addresses.
-template <bool FULL, bool KC, int ROWS>
+// rows >= rows, reading clamped addresses.  NSET register sets hold loaded slices (two
+// let a slice be requested two iterations before it is stored).
+template <bool FULL, bool KC, int ROWS, int NSET = 1>
 struct X6Operand {
   static constexpr int L = ROWS * kBK / 4 / kThreads;
   static_assert(L == 1 || L == 2, "128 or 256 rows");
@@ -109,7 +110,7 @@ struct X6Operand {
   int ld, rows, kend;
   int r[L], k[L];  // KC: row and k of load j; !KC: r[0] = first row, k[0] = first k
   int so[L];       // LDS element offsets within one piece
-  f4 v[2];
+  f4 vv[NSET][2];
   __device__ __forceinline__ void init(const float* b, int ld_, int r0, int rows_, int kbeg, int kend_) {
     base = b;
     ld = ld_;
@@ -151,7 +152,9 @@ struct X6Operand {
       return x;
     }
   }
+  template <int SET>
   __device__ __forceinline__ void load(int slice) {
+    f4 (&v)[2] = vv[SET];
     const int ks = slice * kBK;
     if constexpr (KC) {
 #pragma unroll
@@ -176,7 +179,9 @@ struct X6Operand {
     }
   }
   // the three pieces into LDS: piece q of this operand starts at p0 + q * ROWS * kLDK
+  template <int SET>
   __device__ __forceinline__ void store(unsigned short* p0) const {
+    const f4 (&v)[2] = vv[SET];
     constexpr int P = ROWS * kLDK;
     if constexpr (KC) {
 #pragma unroll
@@ -220,14 +225,14 @@ struct X6Operand {
 // pieces 1 and 2 (zero for such values) are not issued.  Thread t loads rows
 // 4 (t / 16) .. +3 at k-row t % 16 (8 bytes); lanes t and t^1 swap two of those rows, so
 // the even lane writes rows 0-1 and the odd lane rows 2-3, each as a (k even, k odd) pair.
-template <bool FULL>
+template <bool FULL, int NSET = 1>
 struct X6OperandB16 {
   static constexpr int kWrites = 2, kLoads = 1;
   const unsigned short* base;
   int ld, rows, kend;
   int r0q, k0;  // first row of the thread's quad, its k-row offset
   int so;
-  u32x2 v;      // rows 0-1 and rows 2-3 of the quad, two bf16 each
+  u32x2 vv[NSET];  // rows 0-1 and rows 2-3 of the quad, two bf16 each
   __device__ __forceinline__ void init(const float* b, int ld_, int r0, int rows_, int kbeg, int kend_) {
     base = reinterpret_cast<const unsigned short*>(b);
     ld = ld_;
@@ -238,7 +243,9 @@ struct X6OperandB16 {
     k0 = kbeg + t % 16;
     so = (4 * (t / 16) + 2 * odd) * kLDK + (t % 16) - odd;
   }
+  template <int SET>
   __device__ __forceinline__ void load(int slice) {
+    u32x2& v = vv[SET];
     const int kk = k0 + slice * kBK;
     if constexpr (FULL) {
       v = *reinterpret_cast<const u32x2*>(base + (size_t)kk * ld + r0q);
@@ -255,7 +262,9 @@ struct X6OperandB16 {
       v = u32x2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
     }
   }
+  template <int SET>
   __device__ __forceinline__ void store(unsigned short* p0) const {  // piece 0 only
+    const u32x2& v = vv[SET];
     const bool odd = threadIdx.x & 1;
     const unsigned recv =
         static_cast<unsigned>(__builtin_amdgcn_mov_dpp(static_cast<int>(odd ? v[0] : v[1]), 0xB1, 0xF, 0xF, false));
@@ -269,21 +278,22 @@ struct X6OperandB16 {
 template <class S, bool FULL, bool AKC, bool BKC, int BP>
 __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigned short* sm) {
   static_assert(BP == 3 || (BP == 1 && !BKC && S::BN == 128), "bf16 B: row-contiguous, 128 rows");
-  using OpB = std::conditional_t<BP == 1, X6OperandB16<FULL>, X6Operand<FULL, BKC, S::BN>>;
+  // The long-K shape (FOLD) keeps two slices in registers: a slice is requested two
+  // iterations before it is stored, whose products alone (24 per wave) are shorter than a
+  // load's latency under load.  The projection shape has no registers to spare.
+  constexpr int NSET = S::FOLD ? 2 : 1;
+  using OpA = X6Operand<FULL, AKC, S::BM, NSET>;
+  using OpB = std::conditional_t<BP == 1, X6OperandB16<FULL, NSET>, X6Operand<FULL, BKC, S::BN, NSET>>;
   constexpr int NPP = BP == 1 ? 3 : 6;  // piece products per k-step
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / S::WN, wn = wave % S::WN;
   const int half = lane >> 5, r32 = lane & 31;
   const int kbeg = blockIdx.z * g.kps;
   const int kend = min(g.K, kbeg + g.kps);
-  X6Operand<FULL, AKC, S::BM> oa;
+  OpA oa;
   OpB ob;
   oa.init(g.A, g.lda, m0, g.M, kbeg, kend);
   ob.init(g.B, g.ldb, n0, g.N, kbeg, kend);
-  auto store = [&](int buf) __attribute__((always_inline)) {
-    oa.store(sm + buf * S::BUF);
-    ob.store(sm + buf * S::BUF + 3 * S::PA);
-  };
   f16v acc[S::FM][S::FN];
   f16v tot[S::FOLD ? S::FM : 1][S::FOLD ? S::FN : 1];
 #pragma unroll
@@ -295,14 +305,23 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
     }
 
   const int nk = (kend - kbeg + kBK - 1) / kBK;
-  oa.load(0);
-  ob.load(0);
-  store(0);
-  oa.load(min(1, nk - 1));
-  ob.load(min(1, nk - 1));
+  // slice s lives in register set s % NSET from its load to its store
+  oa.template load<0>(0);
+  ob.template load<0>(0);
+  oa.template store<0>(sm);
+  ob.template store<0>(sm + 3 * S::PA);
+  oa.template load<NSET - 1>(min(1, nk - 1));
+  ob.template load<NSET - 1>(min(1, nk - 1));
+  if constexpr (NSET == 2) {
+    oa.template load<0>(min(2, nk - 1));
+    ob.template load<0>(min(2, nk - 1));
+  }
   __syncthreads();
   const int arow = (wm * S::TM + r32) * kLDK + 8 * half, brow = (wn * S::TN + r32) * kLDK + 8 * half;
-  for (int it = 0; it < nk; ++it) {
+  // iteration it: products of slice it (LDS buffer it&1), slice it+1 from register set SET
+  // into the other buffer, slice it+NSET+1 requested into SET
+  auto iteration = [&](int it, auto setc) __attribute__((always_inline)) {
+    constexpr int SET = decltype(setc)::value;
     const unsigned short* base = sm + (it & 1) * S::BUF;
     u32x4 fa[3][S::FM], fb[3][S::FN];
 #pragma unroll
@@ -317,10 +336,14 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
       }
     }
     // slice it+1 into the other buffer (its last reads were before the previous barrier)
-    store((it & 1) ^ 1);
-    const int nxt = min(it + 2, nk - 1);
-    oa.load(nxt);
-    ob.load(nxt);
+    {
+      unsigned short* const dstb = sm + ((it & 1) ^ 1) * S::BUF;
+      oa.template store<SET>(dstb);
+      ob.template store<SET>(dstb + 3 * S::PA);
+    }
+    const int nxt = min(it + NSET + 1, nk - 1);
+    oa.template load<SET>(nxt);
+    ob.template load<SET>(nxt);
 #pragma unroll
     for (int pp = 0; pp < NPP; ++pp) {
       // one-piece B: (a0, b), (a1, b), (a2, b) -- the non-zero terms of the six-product
@@ -335,8 +358,8 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
       // fragment reads first, then the products with the split and the LDS writes spread
       // between them, then the next slice's loads
       constexpr int kMfma = NPP * S::FM * S::FN;
-      constexpr int kWrites = X6Operand<FULL, AKC, S::BM>::kWrites + OpB::kWrites;
-      constexpr int kLoads = X6Operand<FULL, AKC, S::BM>::kLoads + OpB::kLoads;
+      constexpr int kWrites = OpA::kWrites + OpB::kWrites;
+      constexpr int kLoads = OpA::kLoads + OpB::kLoads;
       constexpr int kValu = 28 * kLoads;
       __builtin_amdgcn_sched_group_barrier(0x100, 3 * (S::FM + S::FN), 0);
 #pragma unroll
@@ -359,6 +382,14 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
             acc[i][j] = f16v{};
           }
       }
+    }
+  };
+  if constexpr (NSET == 1) {
+    for (int it = 0; it < nk; ++it) iteration(it, std::integral_constant<int, 0>{});
+  } else {
+    for (int it = 0; it < nk; it += 2) {
+      iteration(it, std::integral_constant<int, 1>{});
+      if (it + 1 < nk) iteration(it + 1, std::integral_constant<int, 0>{});
     }
   }
 

@@ -98,8 +98,8 @@ __device__ __forceinline__ float swap_pair_lane(float v) {
 //      swap half their values, so the even lane writes rows 0-1 and the odd lane rows 2-3,
 //      each as (k even, k odd) pairs.
 // `kend` bounds k (the end of this workgroup's split): masked loads zero k >= kend and
-// rows >= rows, reading clamped addresses.  NSET register sets hold loaded slices (two
-// let a slice be requested two iterations before it is stored).
+// rows >= rows, reading clamped addresses.  NSET register sets hold loaded slices (N sets
+// let a slice be requested N iterations before it is stored).
 template <bool FULL, bool KC, int ROWS, int NSET = 1>
 struct X6Operand {
   static constexpr int L = ROWS * kBK / 4 / kThreads;
@@ -278,10 +278,12 @@ struct X6OperandB16 {
 template <class S, bool FULL, bool AKC, bool BKC, int BP>
 __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigned short* sm) {
   static_assert(BP == 3 || (BP == 1 && !BKC && S::BN == 128), "bf16 B: row-contiguous, 128 rows");
-  // The long-K shape (FOLD) keeps two slices in registers: a slice is requested two
-  // iterations before it is stored, whose products alone (24 per wave) are shorter than a
-  // load's latency under load.  The projection shape has no registers to spare.
-  constexpr int NSET = S::FOLD ? 2 : 1;
+  // The long-K shape (FOLD) keeps three slices in registers: a slice is requested three
+  // iterations before it is stored, since one iteration's products (24 per wave) are much
+  // shorter than a load's latency under load (one set: configs[4] dW_ih at 38% MFMA busy,
+  // waves waiting 54% of their cycles; two sets took configs[4] from 2.54 to 2.42 ms per
+  // step, three to 2.42-2.43).  The projection shape has no registers to spare.
+  constexpr int NSET = S::FOLD ? 3 : 1;
   using OpA = X6Operand<FULL, AKC, S::BM, NSET>;
   using OpB = std::conditional_t<BP == 1, X6OperandB16<FULL, NSET>, X6Operand<FULL, BKC, S::BN, NSET>>;
   constexpr int NPP = BP == 1 ? 3 : 6;  // piece products per k-step
@@ -310,11 +312,15 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
   ob.template load<0>(0);
   oa.template store<0>(sm);
   ob.template store<0>(sm + 3 * S::PA);
-  oa.template load<NSET - 1>(min(1, nk - 1));
-  ob.template load<NSET - 1>(min(1, nk - 1));
-  if constexpr (NSET == 2) {
-    oa.template load<0>(min(2, nk - 1));
-    ob.template load<0>(min(2, nk - 1));
+  oa.template load<1 % NSET>(min(1, nk - 1));
+  ob.template load<1 % NSET>(min(1, nk - 1));
+  if constexpr (NSET >= 2) {
+    oa.template load<2 % NSET>(min(2, nk - 1));
+    ob.template load<2 % NSET>(min(2, nk - 1));
+  }
+  if constexpr (NSET >= 3) {
+    oa.template load<0>(min(3, nk - 1));
+    ob.template load<0>(min(3, nk - 1));
   }
   __syncthreads();
   const int arow = (wm * S::TM + r32) * kLDK + 8 * half, brow = (wn * S::TN + r32) * kLDK + 8 * half;
@@ -386,10 +392,16 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
   };
   if constexpr (NSET == 1) {
     for (int it = 0; it < nk; ++it) iteration(it, std::integral_constant<int, 0>{});
-  } else {
+  } else if constexpr (NSET == 2) {
     for (int it = 0; it < nk; it += 2) {
       iteration(it, std::integral_constant<int, 1>{});
       if (it + 1 < nk) iteration(it + 1, std::integral_constant<int, 0>{});
+    }
+  } else {
+    for (int it = 0; it < nk; it += 3) {
+      iteration(it, std::integral_constant<int, 1>{});
+      if (it + 1 < nk) iteration(it + 1, std::integral_constant<int, 2>{});
+      if (it + 2 < nk) iteration(it + 2, std::integral_constant<int, 0>{});
     }
   }
 

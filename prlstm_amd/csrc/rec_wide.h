@@ -1,40 +1,28 @@
 // Persistent recurrent kernels for a large hidden size, H = 32 U with U = 64 (H = 2048,
 // configs[3]) or U = 32 (H = 1024, the reference's published T64 B32 D512 H1024 shape),
 // B <= 32.  Included by recurrent.hip: they share that file's hand-off helpers and its
-// device error word.
+// device error word.  This file holds what the wide forward (rec_wide_fwd.h) and backward
+// share -- the grid, the hand-off buffers and their access helpers, the slot rotation --
+// and the backward.
 //
 // W_hh stays in registers for the whole launch: 4H x H floats over 256 workgroups is
 // 256 KB per CU at H = 2048 and 64 KB at H = 1024, where the per-step path streams it
 // from the Infinity Cache every step (_torch.py:111-120 runs one h W_hh^T product per
-// step).  Workgroup (x, r, kb), blockIdx = x + 8 (8 r + kb), sits on XCD x:
-//   rows: the four gates of units [4U x + U r, +U) (4U gate rows, unit-interleaved); wave w
-//         takes units [U w / 4, +U/4) of them (U/32 row tiles of 32);
-//   k:    units [4U kb, +4U), all of them for every wave (4U/2 k-steps).
-// Wave w holds its U x 4U block of W in the accumulator registers (4U per lane) and
-// multiplies it with h_{t-1}[32 batch][the workgroup's 4U k units] on
-// v_mfma_f32_32x32x2_f32 (M = gate rows, N = batch).  Per step:
-//   1. receive: wave w reads h block (kb, w) (the 32 x U values that row group (kb, w)
-//      publishes) -- from another XCD for 7 of 8 workgroups -- into LDS, where all four
-//      waves read the workgroup's four blocks as product operands;
-//   2. products; each wave's accumulators are the workgroup's partial (over k block kb) of
-//      its U/4 units, two slices of U/8 units, sent to the workgroups (x, r, j) of its row
-//      group that run those slices' cells (XCD-local);
-//   3. lane (unit su of slice kb, batch b) sums the 8 partials of its slice in source
-//      order and runs the cell; the workgroup's 4U h values are one contiguous group of
-//      h block (x, r) (1 KB at U = 64; at U = 32 512 bytes, 8 per lane, interleaved with
-//      the neighbouring slice's), gathered in LDS and published by one wave in whole
-//      cache lines (scattered 4-byte device-scope stores from 256 lanes took about 1 us
-//      longer to reach the readers on the other XCDs).
-// Hand-off words are 4-byte values that start out kEmpty, as in the other persistent
-// kernels.  h blocks cross XCDs: device-scope stores and loads.  Partials stay on the XCD:
-// workgroup-scope stores (sc0) when every member of the row group runs on the group's XCD.
+// step).  All 256 workgroups are resident at once, one per CU, 32 on each of the 8 XCDs
+// (blockIdx % 8 = XCD); each step's values cross the XCDs once.
 //
-// Slots.  h_t goes to slot t%4 of its block; after publishing h_t the owner clears its word
-// in slot (t+2)%4.  Every workgroup's step-t products need h_{t-1} of all H units (the 8
-// workgroups of a row group cover all k), and every unit's h_{t-1} needed the partials of
-// its row group at t-1, which read h_{t-2} of all units: so when the owner publishes h_t,
-// every reader has read h_{t-2}.  A reader of h_{t+2} read the owner's h_{t+1} first, which
-// the owner published after its clear completed (its next receive waits for it), so it sees
+// Hand-off words are 4-byte values that start out kEmpty, as in the other persistent
+// kernels.  Values that cross XCDs use device-scope stores and loads; values that stay on
+// an XCD use workgroup-scope stores (sc0) when every member of the group runs on the
+// group's XCD.
+//
+// Slots (forward; the backward uses the same rotation for its dg broadcasts and partials).
+// h_t goes to slot t%4 of its block; after publishing h_t the owner clears its word in slot
+// (t+2)%4.  Every workgroup's step-t products need h_{t-1} of all H units (the 8 workgroups
+// of a row group cover all k), and every unit's h_{t-1} needed the partials of its row
+// group at t-1, which read h_{t-2} of all units: so when the owner publishes h_t, every
+// reader has read h_{t-2}.  A reader of h_{t+2} read the owner's h_{t+1} first, which the
+// owner published after its clear completed (its next receive waits for it), so it sees
 // the clear or h_{t+2}.  Partials of step t go to slot t%3 and have one reader, which clears
 // them after reading; the writer uses that slot again at step t+3, after receiving h_{t+2},
 // which needed the reader's h_{t+1}, published after the clear completed.
@@ -42,49 +30,6 @@
 constexpr int kWideXcds = 8, kWideRowSubs = 4, kWideKBlocks = 8;
 constexpr int kWideWgs = kWideXcds * kWideRowSubs * kWideKBlocks;  // 256
 constexpr int kWideHSlots = 4, kWidePSlots = 3;
-
-template <int U>
-struct WideShape {
-  static_assert(U == 32 || U == 64, "H = 1024 or H = 2048");
-  static constexpr int RT = U / 32;         // row tiles of 32 per wave (forward), column tiles (backward)
-  static constexpr int KS = 2 * U;          // k-steps of 2 per wave (4U k units)
-  static constexpr int SU = U / 8;          // units per slice (8 slices per workgroup)
-  static constexpr int WPL = U / 16;        // h words per lane of a workgroup's published group
-  static constexpr int CELLS = SU * 32;     // cell lanes (slice units x 32 batch)
-  static constexpr int HW = 32 * U;         // words of an h block
-  static constexpr int PW = SU * 32 * 4;    // words of one partial slice (one source)
-  static constexpr int IW = kWideKBlocks * PW;  // inbox words of a workgroup (8 sources)
-  // LDS: the workgroup's four h blocks, double-buffered: [step parity][block][k-step/4][lane] f4
-  static constexpr int HS_F4 = 4 * (U / 2 / 4) * 64;  // f4 per buffer
-  static constexpr int LDS_BYTES = 2 * HS_F4 * 16;
-};
-
-struct WFwdArgs {
-  const float* gih;   // [T][B][4H]: x W_ih^T + b_ih
-  const float* w_hh;  // [4H][H]
-  const float* b_hh;
-  const float* a;
-  const float* h0;
-  const float* c0;
-  float* h_save;
-  float* c_save;
-  float* gact;
-  float* tanh_c;
-  float* hbuf;    // [4 slots][8 x][4 r][HW] h blocks
-  float* inbox;   // [3 slots][256 workgroups][8 sources][PW] partial slices
-  unsigned long long* hello;  // [8][32] placement words
-  int* err;
-  int T, B, H;
-  int device_scope;  // 1: partials with device-scope stores too
-  long long spin;
-};
-
-// Layout of an h block (32 batch x U units of a row group): the operand of k-step i of the
-// products for lane l (batch l%32, unit 2 i + l/32 of the block) is word 256 (i/4) + 4 l +
-// i%4.  A reader lane loads its 16-byte groups j at 256 j + 4 l (U/8 of them).  Row-group
-// member kb publishes units U kb / 8 .. +U/8, the k-steps kb WPL .. +WPL (WPL = U/16): the
-// words 256 (kb WPL / 4) + (kb WPL) % 4 + 4 l .. +WPL of every lane l -- the whole 1 KB
-// group kb at U = 64, half of every lane's 16 bytes of group kb/2 at U = 32.
 
 // Hand-off buffers addressed as raw buffers, so that a lane moves 16 bytes in one access
 // with the coherence bits of the relaxed atomics it replaces: loads sc1 (served by the
@@ -109,40 +54,16 @@ __device__ __forceinline__ void pair_store(__amdgpu_buffer_rsrc_t r, unsigned wo
   __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)(4u * word), 0, FAST ? kCpolSc0 : kCpolSc1);
 }
 
-// Polls the lane's N 16-byte groups until no word is kEmpty (nothing is awaited when
-// expect is false).  Every poll reloads all N groups: that keeps the loop's live state to
-// the values themselves.  kEmpty is the largest 32-bit pattern, so the groups are complete
-// when the maximum of their words differs from it.  Returns false after raising the error
-// flags when the spin limit runs out.
-template <int N>
-__device__ __forceinline__ bool quads_wait(__amdgpu_buffer_rsrc_t r, const unsigned (&off)[N], bool expect,
-                                           f4 (&v)[N], long long spin, int* abort_flag, int* err) {
-  const long long t0 = wall_clock64();
-  while (true) {
-    unsigned m = 0u;
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const u4v q = expect ? quad_load(r, off[i]) : u4v{0u, 0u, 0u, 0u};
-      m = max(m, max(max(q[0], q[1]), max(q[2], q[3])));
-      v[i] = f4{__uint_as_float(q[0]), __uint_as_float(q[1]), __uint_as_float(q[2]), __uint_as_float(q[3])};
-    }
-    if (__all(m != kEmpty)) return true;
-    if (wall_clock64() - t0 > spin) {
-      raise_abort(abort_flag, err);
-      return false;
-    }
-  }
-}
-
 template <bool FAST>
 __device__ __forceinline__ void quad_put(__amdgpu_buffer_rsrc_t r, unsigned word, f4 v) {
   quad_store<FAST>(r, word, u4v{__float_as_uint(canon_nan(v[0])), __float_as_uint(canon_nan(v[1])),
                                 __float_as_uint(canon_nan(v[2])), __float_as_uint(canon_nan(v[3]))});
 }
 
-// Four k-steps of the wide products for the wave's two row tiles: acc[rt + 2 (k % 2)] +=
-// W[k][rt] h[k], on v_mfma_f32_32x32x2_f32 with the W operand read from the accumulator
-// register file (the compiler does not keep a 256-register operand block there by itself).
+// Four k-steps of the wide backward's products for the wave's two column tiles:
+// acc[rt + 2 (k % 2)] += W[k][rt] dg[k], on v_mfma_f32_32x32x2_f32 with the W operand read
+// from the accumulator register file (the compiler does not keep a 256-register operand
+// block there by itself).
 // Even and odd k-steps go to separate accumulators, so a product depends on the one two
 // instructions back.  The leading nops separate VALU writes of the operands from the
 // products' reads.
@@ -162,7 +83,7 @@ __device__ __forceinline__ void wide_ksteps4(f16v (&acc)[4], const float (&w)[4]
         "a"(w[3][1]), "v"(h[0]), "v"(h[1]), "v"(h[2]), "v"(h[3]));
 }
 
-// The same for one row tile (U = 32): k-step e of the four goes to accumulator e, so a
+// The same for one column tile (U = 32): k-step e of the four goes to accumulator e, so a
 // product depends on the one four instructions back.
 __device__ __forceinline__ void wide_ksteps4(f16v (&acc)[4], const float (&w)[4][1], f4 h) {
   asm volatile(
@@ -175,9 +96,9 @@ __device__ __forceinline__ void wide_ksteps4(f16v (&acc)[4], const float (&w)[4]
       : "a"(w[0][0]), "a"(w[1][0]), "a"(w[2][0]), "a"(w[3][0]), "v"(h[0]), "v"(h[1]), "v"(h[2]), "v"(h[3]));
 }
 
-// The wave's partial of 4 consecutive gate rows (or columns) of row tile rt, register group
-// q, from the accumulators: two row tiles keep tile rt in acc[rt] (even k-steps) and
-// acc[rt + 2] (odd), one row tile keeps k-step e % 4 in acc[e % 4].
+// The wave's partial of 4 consecutive columns of column tile rt, register group q, from the
+// accumulators: two tiles keep tile rt in acc[rt] (even k-steps) and acc[rt + 2] (odd), one
+// tile keeps k-step e % 4 in acc[e % 4].
 template <int RT>
 __device__ __forceinline__ f4 wide_partial(const f16v (&acc)[4], int rt, int q) {
   f4 v;
@@ -200,267 +121,9 @@ __device__ __forceinline__ void wide_ksteps_drain(f16v (&acc)[4]) {
   for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i]));
 }
 
-template <int U, bool FAST>
-__device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int r, int kb, f4* hs,
-                                                  int& abort_flag) {
-  using S = WideShape<U>;
-  constexpr int RT = S::RT, WPL = S::WPL;
-  const int T = p.T, B = p.B, H = p.H;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hb = lane >> 5, l32 = lane & 31;
-
-  // W_hh block of this wave: row tile rt, k-step 4 i4 + e -> row m = l%32 of the tile (unit
-  // offset U w / 4 + (32 rt + m) / 4, gate m % 4), k = 4U kb + 2 (4 i4 + e) + l/32.  It is
-  // held unscaled (a register that only feeds the products can live in the accumulator
-  // file); the gate's a scales the summed product in the cell.
-  const int ubase = 4 * U * x + U * r;  // first unit of the workgroup's rows
-  const int kbase = 4 * U * kb;         // first k (unit) of the workgroup's k block
-  float wreg[S::KS / 4][4][RT];
-  {
-    const float* rows[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const int rho = 32 * rt + l32, g = rho & 3, u = ubase + U / 4 * w + (rho >> 2);
-      rows[rt] = p.w_hh + ((size_t)g * H + u) * H + kbase + hb;
-    }
-    // loaded 32 at a time and moved to the accumulator file group by group, so that the
-    // loads in flight never hold more than a few dozen VGPRs
-#pragma unroll
-    for (int i8 = 0; i8 < S::KS / 4; i8 += 4) {
-#pragma unroll
-      for (int i4 = i8; i4 < i8 + 4; ++i4)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt)
-            wreg[i4][e][rt] = rows[rt][2 * (4 * i4 + e)];
-#pragma unroll
-      for (int i4 = i8; i4 < i8 + 4; ++i4)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+a"(wreg[i4][e][rt]));  // held in the accumulator file
-    }
-  }
-
-  // cell lane: tid < CELLS -> unit su of this workgroup's slice kb, batch cb
-  const int su = tid >> 5, cb = tid & 31;
-  const bool cell = tid < S::CELLS;
-  const bool c_ok = cell && cb < B;
-  const int unit = ubase + S::SU * kb + su;  // < H
-  float c_reg = 0.f, bs[4] = {0.f, 0.f, 0.f, 0.f}, ag[4] = {0.f, 0.f, 0.f, 0.f};
-  if (c_ok) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      ag[g] = p.a[g];
-      bs[g] = ag[g] * p.b_hh[g * H + unit];
-    }
-    const size_t e = (size_t)cb * H + unit;
-    c_reg = p.c0 ? p.c0[e] : 0.f;
-    p.h_save[e] = p.h0 ? p.h0[e] : 0.f;
-    p.c_save[e] = c_reg;
-  }
-  const size_t plane = (size_t)B * H, plane4 = 4 * plane;
-  const int me = blockIdx.x;
-  const size_t inbox_slot = (size_t)kWideWgs * S::IW;
-  // this workgroup's group of h block (x, r) (WPL words of every lane l at 4 l) and the
-  // block (kb, w) this wave reads
-  const size_t hblock = S::HW, hslot = (size_t)kWideXcds * kWideRowSubs * S::HW;
-  float* const hown = p.hbuf + (size_t)(x * kWideRowSubs + r) * hblock + 256u * (kb * WPL / 4) + (kb * WPL) % 4;
-  const float* const hsrc = p.hbuf + (size_t)(kb * kWideRowSubs + w) * hblock;
-  const bool h_ok = l32 < B;  // batch column of this lane in the products
-  constexpr int NQ = U / 8;   // 16-byte groups a lane reads from an h block
-  __shared__ float hst[256];  // this step's h values, in the order of the published group
-  if (tid < 256) hst[tid] = 0.f;  // absent batch columns stay 0
-
-  float gin[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int t = 0; t < T; ++t) {
-    f4* const hsb = hs + (size_t)(t & 1) * S::HS_F4;
-    // ---- 1. h_{t-1} of block (kb, w) into LDS: group j of block w is
-    //         hs[t&1][(NQ w + j) * 64 + lane], the operands of k-steps 4j .. 4j+3,
-    //         h[l%32][4U kb + U w + 2 (4j + e) + l/32] -----------------------------------
-    if (t == 0) {
-#pragma unroll
-      for (int j = 0; j < NQ; ++j) {
-        f4 v = f4{0.f, 0.f, 0.f, 0.f};
-        if (h_ok && p.h0) {
-          const float* row = p.h0 + (size_t)l32 * H + kbase + U * w + hb;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = row[2 * (4 * j + e)];
-        }
-        hsb[(NQ * w + j) * 64 + lane] = v;
-      }
-    } else {
-      // groups j at 256 j + 4 lane; groups still holding a kEmpty word are loaded again
-      const __amdgpu_buffer_rsrc_t src = wide_rsrc(hsrc + (size_t)((t - 1) % kWideHSlots) * hslot, S::HW);
-      bool need[NQ];
-      u4v q4[NQ];
-#pragma unroll
-      for (int j = 0; j < NQ; ++j) {
-        need[j] = h_ok;
-        q4[j] = need[j] ? quad_load(src, 256u * j + 4u * lane) : u4v{0u, 0u, 0u, 0u};
-      }
-      const long long t0 = wall_clock64();
-      while (true) {
-        bool ok = true;
-#pragma unroll
-        for (int j = 0; j < NQ; ++j) {
-          need[j] = need[j] && max(max(q4[j][0], q4[j][1]), max(q4[j][2], q4[j][3])) == kEmpty;
-          ok = ok && !need[j];
-        }
-        if (__all(ok)) break;
-        if (wall_clock64() - t0 > p.spin) {
-          raise_abort(&abort_flag, p.err);
-          return;
-        }
-#pragma unroll
-        for (int j = 0; j < NQ; ++j)
-          if (need[j]) q4[j] = quad_load(src, 256u * j + 4u * lane);
-      }
-#pragma unroll
-      for (int j = 0; j < NQ; ++j)
-        hsb[(NQ * w + j) * 64 + lane] =
-            h_ok ? f4{__uint_as_float(q4[j][0]), __uint_as_float(q4[j][1]), __uint_as_float(q4[j][2]),
-                      __uint_as_float(q4[j][3])}
-                 : f4{0.f, 0.f, 0.f, 0.f};
-    }
-    // this step's input projection for the cell lanes (used after the products)
-    if (c_ok) {
-      const float* g = p.gih + (size_t)t * plane4 + (size_t)cb * 4 * H + unit;
-#pragma unroll
-      for (int gt = 0; gt < 4; ++gt) gin[gt] = __builtin_nontemporal_load(g + (size_t)gt * H);
-    }
-    lds_barrier();  // the four blocks are in LDS; the other buffer is free (step t-1's products are done)
-    if (abort_flag) return;
-
-    // ---- 2. products over the workgroup's k block; the accumulators are the partial
-    //         of the wave's U/4 units, sent to the two slices' cell workgroups ------------
-    f16v acc[4] = {f16v{}, f16v{}, f16v{}, f16v{}};
-    {
-      // the operands of group i4 + 1 are read from LDS while group i4 multiplies (volatile
-      // reads stay in program order with the asm, so only two groups' operands are live)
-      typedef __attribute__((address_space(3))) const volatile f4 lds_vf4;
-      lds_vf4* const hv = (lds_vf4*)(hsb);
-      f4 hcur = hv[lane];
-#pragma unroll
-      for (int i4 = 0; i4 < S::KS / 4; ++i4) {
-        const f4 hnext = i4 + 1 < S::KS / 4 ? hv[(i4 + 1) * 64 + lane] : hcur;
-        wide_ksteps4(acc, wreg[i4], hcur);
-        hcur = hnext;
-      }
-    }
-    wide_ksteps_drain(acc);
-    {
-      // D layout: lane l, register 4 q + g -> gate row 8 q + 4 (l/32) + g of tile rt, batch
-      // l%32; with unit-interleaved rows that is gate g of unit U w / 4 + 8 rt + 2 q + l/32
-      // of the row group, i.e. unit su' = that % SU of slice that / SU
-      float* const ib = p.inbox + (size_t)(t % kWidePSlots) * inbox_slot;
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int ur = U / 4 * w + 8 * rt + 2 * q + hb;  // unit of the row group
-          const int dst = x + kWideXcds * (r * kWideKBlocks + ur / S::SU);
-          const __amdgpu_buffer_rsrc_t d = wide_rsrc(ib + (size_t)dst * S::IW + (size_t)kb * S::PW, S::PW);
-          const f4 v = wide_partial<RT>(acc, rt, q);
-          if (h_ok) quad_put<FAST>(d, 4u * ((ur % S::SU) * 32 + l32), v);
-        }
-      }
-    }
-
-    // ---- 3. the cell of slice kb: sum the 8 sources, activate, publish h_t ---------
-    if (cell) {
-      const __amdgpu_buffer_rsrc_t ib =
-          wide_rsrc(p.inbox + (size_t)(t % kWidePSlots) * inbox_slot + (size_t)me * S::IW, S::IW);
-      unsigned offs[kWideKBlocks];
-#pragma unroll
-      for (int sidx = 0; sidx < kWideKBlocks; ++sidx) offs[sidx] = (unsigned)sidx * S::PW + 4u * (su * 32 + cb);
-      f4 v[kWideKBlocks];
-      if (!quads_wait<kWideKBlocks>(ib, offs, c_ok, v, p.spin, &abort_flag, p.err)) return;
-      if (c_ok) {
-#pragma unroll
-        for (int sidx = 0; sidx < kWideKBlocks; ++sidx) quad_store<FAST>(ib, offs[sidx], u4v{kEmpty, kEmpty, kEmpty, kEmpty});
-        f4 z = v[0];
-#pragma unroll
-        for (int sidx = 1; sidx < kWideKBlocks; ++sidx) z = z + v[sidx];
-        float act[4];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) act[g] = sigmoid_f((gin[g] + ag[g] * z[g]) + bs[g]);
-        const float c = act[1] * c_reg + act[0] * act[2];
-        const float tc = tanh_f(c);
-        const float h = act[3] * tc;
-        c_reg = c;
-        hst[WPL * (cb + 32 * (su & 1)) + (su >> 1)] = canon_nan(h);  // word 4 l + su/2 of the group
-        const size_t e = (size_t)cb * H + unit;
-        __builtin_nontemporal_store(h, p.h_save + (size_t)(t + 1) * plane + e);
-        __builtin_nontemporal_store(c, p.c_save + (size_t)(t + 1) * plane + e);
-        __builtin_nontemporal_store(tc, p.tanh_c + (size_t)t * plane + e);
-        __builtin_nontemporal_store(f4{act[0], act[1], act[2], act[3]},
-                                    reinterpret_cast<f4*>(p.gact + ((size_t)t * plane + e) * 4));
-      }
-    }
-    lds_barrier();  // the workgroup's h values are gathered
-    if (w == 0) {   // publish the group, then clear it in the slot of two steps ago
-      const __amdgpu_buffer_rsrc_t hp = wide_rsrc(hown + (size_t)(t % kWideHSlots) * hslot, 256);
-      const __amdgpu_buffer_rsrc_t hc = wide_rsrc(hown + (size_t)((t + 2) % kWideHSlots) * hslot, 256);
-      if constexpr (WPL == 4) {
-        const f4 hq = *reinterpret_cast<const f4*>(&hst[4 * lane]);
-        quad_store<false>(hp, 4u * lane, u4v{__float_as_uint(hq[0]), __float_as_uint(hq[1]), __float_as_uint(hq[2]),
-                                             __float_as_uint(hq[3])});
-        quad_store<false>(hc, 4u * lane, u4v{kEmpty, kEmpty, kEmpty, kEmpty});
-      } else {
-        const float h0v = hst[2 * lane], h1v = hst[2 * lane + 1];
-        pair_store<false>(hp, 4u * lane, u2v{__float_as_uint(h0v), __float_as_uint(h1v)});
-        pair_store<false>(hc, 4u * lane, u2v{kEmpty, kEmpty});
-      }
-    }
-  }
-}
-
-// After an abort the cell lanes set their outputs (rows 0..T of h_save / c_save, the
-// activations of every step) to NaN.
-template <int U>
-__device__ void poison_wide_fwd(const WFwdArgs& p, int x, int r, int kb) {
-  using S = WideShape<U>;
-  const int tid = threadIdx.x, su = tid >> 5, cb = tid & 31;
-  if (tid >= S::CELLS || cb >= p.B) return;
-  const int unit = 4 * U * x + U * r + S::SU * kb + su;
-  const float nan = __uint_as_float(0x7FC00000u);
-  const size_t plane = (size_t)p.B * p.H, e = (size_t)cb * p.H + unit;
-  for (int t = 0; t <= p.T; ++t) {
-    p.h_save[t * plane + e] = nan;
-    p.c_save[t * plane + e] = nan;
-    if (t < p.T) {
-      p.tanh_c[t * plane + e] = nan;
-      *reinterpret_cast<f4*>(p.gact + (t * plane + e) * 4) = f4{nan, nan, nan, nan};
-    }
-  }
-}
-
-template <int U>
-__global__ __launch_bounds__(256, 1) void rec_fwd_wide(WFwdArgs p) {
-  extern __shared__ f4 wide_hs[];  // the h blocks of two steps (sized to keep one workgroup per CU)
-  __shared__ int abort_flag;
-  const int x = blockIdx.x % kWideXcds, loc = blockIdx.x / kWideXcds;
-  const int r = loc / kWideKBlocks, kb = loc % kWideKBlocks;
-  if (threadIdx.x == 0) abort_flag = 0;
-  const bool fast = agree_placement(p.hello + (size_t)x * (kWideRowSubs * kWideKBlocks), loc,
-                                    kWideRowSubs * kWideKBlocks, p.spin, &abort_flag, p.err) &&
-                    !p.device_scope;
-  if (!abort_flag) {
-    if (fast)
-      rec_fwd_wide_body<U, true>(p, x, r, kb, wide_hs, abort_flag);
-    else
-      rec_fwd_wide_body<U, false>(p, x, r, kb, wide_hs, abort_flag);
-  }
-  lds_barrier();
-  if (abort_flag) poison_wide_fwd<U>(p, x, r, kb);
-}
-
 // ---------------------------------------------------------------------------------
 // Persistent recurrent backward for H = 32 U (U = 64: H = 2048, configs[3]; U = 32:
-// H = 1024), B <= 32: the mirror of the wide forward (_torch.py:133-150: dh_t = dout_t +
+// H = 1024), B <= 32: the mirror of the wide forward in rec_wide_fwd.h (_torch.py:133-150: dh_t = dout_t +
 // dg_{t+1} W_s, then the cell backward).  Workgroup (x, c), blockIdx = x + 8 c, sits on XCD
 // x and holds W_hh's 16U gate rows of units [4U x, +4U) (unit-interleaved) for the output
 // columns (units) [U c, +U); wave w takes rows [4U w, +4U) (units [4U x + U w, +U)), U/32

@@ -1992,6 +1992,7 @@ __global__ __launch_bounds__(XT >= 0 ? 512 : 256, 1) void rec_bwd_persistent(PBw
 }
 
 #include "rec_wide.h"
+#include "rec_wide_fwd.h"
 
 // ---------------------------------------------------------------------------------
 // host side
@@ -2126,7 +2127,7 @@ int plan_persistent(int B, int H, int D, bool bwd, PersistentPlan* pl) {
   return HSL_OK;
 }
 
-// The W_hh-resident kernels for large H (rec_wide.h): H = 32 U with U = 64 (2048) or 32
+// The W_hh-resident kernels for large H (rec_wide.h, rec_wide_fwd.h): H = 32 U with U = 64 (2048) or 32
 // (1024), B <= 32, eight XCDs and all 256 workgroups resident at once (one per CU).
 struct WidePlan {
   bool ok = false;
@@ -2134,10 +2135,10 @@ struct WidePlan {
 };
 
 // dynamic LDS of the wide kernels, padded so that one workgroup fits per CU: the forward's
-// double-buffered h blocks, the backward's wave partials and gathered dg group
+// h buffer of each chain, the backward's wave partials and gathered dg group
 template <int U>
 constexpr size_t wide_fwd_lds() {
-  return WideShape<U>::LDS_BYTES > (size_t)kPadLdsBytes ? WideShape<U>::LDS_BYTES : (size_t)kPadLdsBytes;
+  return WideFShape<U>::LDS_BYTES > (size_t)kPadLdsBytes ? WideFShape<U>::LDS_BYTES : (size_t)kPadLdsBytes;
 }
 template <int U>
 constexpr size_t wide_bwd_lds() {
@@ -2147,9 +2148,9 @@ constexpr size_t wide_bwd_lds() {
 
 // exchange words of the wide kernels: forward h blocks then partial inboxes; backward dg
 // broadcasts then partial inboxes (floats)
-size_t wide_fwd_hfloats(int U) { return (size_t)kWideHSlots * kWideXcds * kWideRowSubs * 32 * U; }
+size_t wide_fwd_hfloats(int U) { return (size_t)kWideHSlots * 2 * (kWideXcds * kWideRowSubs) * 16 * U; }
 size_t wide_fwd_floats(int U) {
-  return wide_fwd_hfloats(U) + (size_t)kWidePSlots * kWideWgs * kWideKBlocks * (U / 8) * 32 * 4;
+  return wide_fwd_hfloats(U) + (size_t)kWidePSlots * 2 * kWideWgs * kWideKBlocks * (U / 8) * 16 * 4;
 }
 size_t wide_bwd_bfloats(int U) { return (size_t)kWideHSlots * kWideXcds * (16 * U) * 32; }
 size_t wide_bwd_floats(int U) { return wide_bwd_bfloats(U) + (size_t)kWidePSlots * kWideWgs * (8 * 32 * (U / 8)); }

@@ -398,11 +398,18 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
       if (it + 1 < nk) iteration(it + 1, std::integral_constant<int, 0>{});
     }
   } else {
-    for (int it = 0; it < nk; it += 3) {
+    // whole trips of three in the loop, the rest after it: an iteration skipped inside the
+    // loop would leave a path on which fewer loads were issued, and the compiler's wait
+    // before the first store of a trip then counts for that path (waiting for the loads
+    // of the previous iteration instead of those of three iterations back)
+    int it = 0;
+    for (; it + 3 <= nk; it += 3) {
       iteration(it, std::integral_constant<int, 1>{});
-      if (it + 1 < nk) iteration(it + 1, std::integral_constant<int, 2>{});
-      if (it + 2 < nk) iteration(it + 2, std::integral_constant<int, 0>{});
+      iteration(it + 1, std::integral_constant<int, 2>{});
+      iteration(it + 2, std::integral_constant<int, 0>{});
     }
+    if (it < nk) iteration(it, std::integral_constant<int, 1>{});
+    if (it + 1 < nk) iteration(it + 1, std::integral_constant<int, 2>{});
   }
 
   float* outp = g.partial ? g.out + (size_t)blockIdx.z * g.M * g.N : g.out;

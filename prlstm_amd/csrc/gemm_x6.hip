@@ -361,20 +361,30 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
         for (int j = 0; j < S::FN; ++j) acc[i][j] = mfma_bf16(fa[qa][i], fb[qb][j], acc[i][j]);
     }
     if constexpr (FULL) {
-      // fragment reads first, then the products with the split and the LDS writes spread
-      // between them, then the next slice's loads
+      // fragment reads first; then A's split and LDS writes, with one product each (the
+      // fragments are still arriving), and A's next loads as soon as those writes have
+      // freed its registers, a whole iteration before their use (A streams from memory);
+      // then B's writes with the other products between them, B's loads (B is mostly a
+      // cache-resident weight), the rest of the products
       constexpr int kMfma = NPP * S::FM * S::FN;
-      constexpr int kWrites = OpA::kWrites + OpB::kWrites;
-      constexpr int kLoads = OpA::kLoads + OpB::kLoads;
-      constexpr int kValu = 28 * kLoads;
+      constexpr int kWA = OpA::kWrites, kWB = OpB::kWrites;
+      constexpr int kValuA = 28 * OpA::kLoads, kValuB = 28 * OpB::kLoads;
+      constexpr int kMfmaB = (kMfma - kWA + kWB - 1) / kWB;
       __builtin_amdgcn_sched_group_barrier(0x100, 3 * (S::FM + S::FN), 0);
 #pragma unroll
-      for (int w = 0; w < kWrites; ++w) {
-        __builtin_amdgcn_sched_group_barrier(0x008, (kMfma + kWrites - 1) / kWrites, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, (kValu + kWrites - 1) / kWrites, 0);
+      for (int w = 0; w < kWA; ++w) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, (kValuA + kWA - 1) / kWA, 0);
         __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x020, kLoads, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, OpA::kLoads, 0);
+#pragma unroll
+      for (int w = 0; w < kWB; ++w) {
+        __builtin_amdgcn_sched_group_barrier(0x008, kMfmaB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, (kValuB + kWB - 1) / kWB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x020, OpB::kLoads, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
     }
     __syncthreads();

@@ -82,59 +82,6 @@ struct WFwdArgs {
   long long spin;
 };
 
-// Four k-steps of one quad for the wave's row tiles: acc[rt][e % 2] += W[e][rt] h[e] on
-// v_mfma_f32_16x16x4_f32, W read from the accumulator registers (a product depends on the
-// one 2 RT instructions back).
-__device__ __forceinline__ void wide_quad16(f4 (&acc)[4][2], const float (&w)[4][4], f4 h) {
-  asm volatile(
-      "s_nop 1\n\t"
-      "v_mfma_f32_16x16x4_f32 %0, %8, %24, %0\n\t"
-      "v_mfma_f32_16x16x4_f32 %2, %9, %24, %2\n\t"
-      "v_mfma_f32_16x16x4_f32 %4, %10, %24, %4\n\t"
-      "v_mfma_f32_16x16x4_f32 %6, %11, %24, %6\n\t"
-      "v_mfma_f32_16x16x4_f32 %1, %12, %25, %1\n\t"
-      "v_mfma_f32_16x16x4_f32 %3, %13, %25, %3\n\t"
-      "v_mfma_f32_16x16x4_f32 %5, %14, %25, %5\n\t"
-      "v_mfma_f32_16x16x4_f32 %7, %15, %25, %7\n\t"
-      "v_mfma_f32_16x16x4_f32 %0, %16, %26, %0\n\t"
-      "v_mfma_f32_16x16x4_f32 %2, %17, %26, %2\n\t"
-      "v_mfma_f32_16x16x4_f32 %4, %18, %26, %4\n\t"
-      "v_mfma_f32_16x16x4_f32 %6, %19, %26, %6\n\t"
-      "v_mfma_f32_16x16x4_f32 %1, %20, %27, %1\n\t"
-      "v_mfma_f32_16x16x4_f32 %3, %21, %27, %3\n\t"
-      "v_mfma_f32_16x16x4_f32 %5, %22, %27, %5\n\t"
-      "v_mfma_f32_16x16x4_f32 %7, %23, %27, %7"
-      : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(acc[2][0]), "+v"(acc[2][1]),
-        "+v"(acc[3][0]), "+v"(acc[3][1])
-      : "a"(w[0][0]), "a"(w[0][1]), "a"(w[0][2]), "a"(w[0][3]), "a"(w[1][0]), "a"(w[1][1]), "a"(w[1][2]),
-        "a"(w[1][3]), "a"(w[2][0]), "a"(w[2][1]), "a"(w[2][2]), "a"(w[2][3]), "a"(w[3][0]), "a"(w[3][1]),
-        "a"(w[3][2]), "a"(w[3][3]), "v"(h[0]), "v"(h[1]), "v"(h[2]), "v"(h[3]));
-}
-__device__ __forceinline__ void wide_quad16(f4 (&acc)[2][2], const float (&w)[4][2], f4 h) {
-  asm volatile(
-      "s_nop 1\n\t"
-      "v_mfma_f32_16x16x4_f32 %0, %4, %12, %0\n\t"
-      "v_mfma_f32_16x16x4_f32 %2, %5, %12, %2\n\t"
-      "v_mfma_f32_16x16x4_f32 %1, %6, %13, %1\n\t"
-      "v_mfma_f32_16x16x4_f32 %3, %7, %13, %3\n\t"
-      "v_mfma_f32_16x16x4_f32 %0, %8, %14, %0\n\t"
-      "v_mfma_f32_16x16x4_f32 %2, %9, %14, %2\n\t"
-      "v_mfma_f32_16x16x4_f32 %1, %10, %15, %1\n\t"
-      "v_mfma_f32_16x16x4_f32 %3, %11, %15, %3"
-      : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1])
-      : "a"(w[0][0]), "a"(w[0][1]), "a"(w[1][0]), "a"(w[1][1]), "a"(w[2][0]), "a"(w[2][1]), "a"(w[3][0]),
-        "a"(w[3][1]), "v"(h[0]), "v"(h[1]), "v"(h[2]), "v"(h[3]));
-}
-
-template <int RT>
-__device__ __forceinline__ void wide_drain16(f4 (&acc)[RT][2]) {
-#pragma unroll
-  for (int i = 0; i < RT; ++i) asm volatile("" : "+v"(acc[i][0]), "+v"(acc[i][1]));
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-#pragma unroll
-  for (int i = 0; i < RT; ++i) asm volatile("" : "+v"(acc[i][0]), "+v"(acc[i][1]));
-}
-
 template <int U, bool FAST>
 __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int r, int kb, f4* hs,
                                                    int& abort_flag) {

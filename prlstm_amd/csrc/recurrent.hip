@@ -1993,6 +1993,7 @@ __global__ __launch_bounds__(XT >= 0 ? 512 : 256, 1) void rec_bwd_persistent(PBw
 
 #include "rec_wide.h"
 #include "rec_wide_fwd.h"
+#include "rec_wide_bwd32.h"
 
 // ---------------------------------------------------------------------------------
 // host side
@@ -2141,9 +2142,9 @@ constexpr size_t wide_fwd_lds() {
   return WideFShape<U>::LDS_BYTES > (size_t)kPadLdsBytes ? WideFShape<U>::LDS_BYTES : (size_t)kPadLdsBytes;
 }
 template <int U>
-constexpr size_t wide_bwd_lds() {
-  return (size_t)WideBShape<U>::LDS_BYTES > (size_t)kPadLdsBytes ? (size_t)WideBShape<U>::LDS_BYTES
-                                                                  : (size_t)kPadLdsBytes;
+constexpr size_t wide_bwd_lds() {  // rec_bwd_wide<64> or rec_bwd_wide1<32>
+  constexpr size_t b = U == 32 ? (size_t)WideB1Shape<32>::LDS_BYTES : (size_t)WideBShape<U>::LDS_BYTES;
+  return b > (size_t)kPadLdsBytes ? b : (size_t)kPadLdsBytes;
 }
 
 // exchange words of the wide kernels: forward h blocks then partial inboxes; backward dg
@@ -2158,7 +2159,8 @@ size_t wide_bwd_floats(int U) { return wide_bwd_bfloats(U) + (size_t)kWidePSlots
 template <int U>
 int wide_occupancy(bool bwd, int* occ) {
   if (bwd)
-    HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(occ, rec_bwd_wide<U>, 256, wide_bwd_lds<U>()));
+    HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        occ, U == 32 ? (const void*)rec_bwd_wide1<32> : (const void*)rec_bwd_wide<64>, 256, wide_bwd_lds<U>()));
   else
     HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(occ, rec_fwd_wide<U>, 256, wide_fwd_lds<U>()));
   return HSL_OK;
@@ -2736,7 +2738,7 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     if (wp.U == 64)
       hipLaunchKernelGGL(rec_bwd_wide<64>, dim3(kWideWgs), dim3(256), wide_bwd_lds<64>(), s, wa);
     else
-      hipLaunchKernelGGL(rec_bwd_wide<32>, dim3(kWideWgs), dim3(256), wide_bwd_lds<32>(), s, wa);
+      hipLaunchKernelGGL(rec_bwd_wide1<32>, dim3(kWideWgs), dim3(256), wide_bwd_lds<32>(), s, wa);
     HSL_HIP(hipGetLastError());
     timing_end(slot, s);
     note_recurrent_path(3);

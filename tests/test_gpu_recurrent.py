@@ -194,11 +194,13 @@ def test_h1024_on_the_per_step_path(dev):
 
 @pytest.mark.parametrize("H", [1024, 2048])
 @pytest.mark.parametrize("scope", [0, 1])
-def test_wide_forward_partial_batch_hx(dev, scope, H):
-    """The wide kernels (both widths) with B < 32 (absent batch columns), h0/c0 given,
-    a ~ U(0, 0.5), and with device-scope stores for the partial exchange (scope 1)."""
+@pytest.mark.parametrize("B", [20, 12])
+def test_wide_forward_partial_batch_hx(dev, scope, H, B):
+    """The wide kernels (both widths) with B < 32, h0/c0 given, a ~ U(0, 0.5), and with
+    device-scope stores for the partial exchange (scope 1).  The batch runs as two chains of
+    16 rows: B = 20 leaves 12 rows of the second chain absent, B = 12 runs one chain only."""
     prlstm_amd.set_exchange_scope(scope)
-    check(6, 20, 64, H, dev, 0, a=[0.3, 0.5, 0.1, 0.2], with_hx=True, fwd_path=3)
+    check(6, B, 64, H, dev, 0, a=[0.3, 0.5, 0.1, 0.2], with_hx=True, fwd_path=3)
     assert prlstm_amd.last_recurrent_path() == 3
 
 

@@ -84,7 +84,7 @@ int hsl_set_split_products(int on);
 /* Which path the last hsl_rec_fwd / hsl_rec_bwd in this process (on any host
  * thread; autograd runs the backward on its own thread) used: 1 = per-step,
  * 2 = persistent, 3 = the persistent kernels that hold W_hh in the registers of
- * 256 workgroups (H = 2048, B <= 32). */
+ * 256 workgroups (H = 1024 or 2048, B <= 32). */
 int hsl_last_recurrent_path(void);
 /* Whether the last hsl_rec_bwd (in this process, on any thread) accumulated the
  * weight gradients inside the persistent kernel: 0 = no (separate GEMMs), 1 = dW_hh,

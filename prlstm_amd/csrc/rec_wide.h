@@ -304,12 +304,14 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
     lds_barrier();
     if (abort_flag) return false;
     if (sender && 16 * ch + sb < B) {
-      const __amdgpu_buffer_rsrc_t d = wide_rsrc(inbox(k - 1, ch, dst), S::INBOX);
+      // one descriptor over every workgroup's inbox of the slot (the same for all lanes: a
+      // descriptor that differs between lanes makes the compiler loop over its values)
+      const __amdgpu_buffer_rsrc_t d = wide_rsrc(inbox(k - 1, ch, 0), (size_t)kWideWgs * S::INBOX);
       const int cq = S::QS * c4 + qq;
       f4 sum = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ww = 0; ww < 4; ++ww) sum = sum + *reinterpret_cast<const f4*>(&rb[((ww * (U / 4) + cq) * 16 + sb) * 4]);
-      quad_put<false>(d, (unsigned)(x * 16 * SU + sb * SU + 4 * qq), sum);
+      quad_put<false>(d, (unsigned)(dst * S::INBOX + x * 16 * SU + sb * SU + 4 * qq), sum);
     }
     return true;
   };

@@ -197,14 +197,14 @@ __device__ __forceinline__ void rec_bwd_wide1_body(const WBwdArgs& p, int x, int
       if (abort_flag) return;
       if (sb < B) {
         const __amdgpu_buffer_rsrc_t d =
-            wide_rsrc(p.inbox + (size_t)((k - 1) % kWidePSlots) * islot + (size_t)dst * S::INBOX, S::INBOX);
+            wide_rsrc(p.inbox + (size_t)((k - 1) % kWidePSlots) * islot, (size_t)kWideWgs * S::INBOX);
 #pragma unroll
         for (int qq = 0; qq < SU / 4; ++qq) {
           f4 sum = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int ww = 0; ww < 4; ++ww)
             sum = sum + *reinterpret_cast<const f4*>(&red[((ww * (U / 4) + (SU / 4) * c4 + qq) * 32 + sb) * 4]);
-          quad_put<false>(d, (unsigned)(x * 32 * SU + sb * SU + 4 * qq), sum);
+          quad_put<false>(d, (unsigned)(dst * S::INBOX + x * 32 * SU + sb * SU + 4 * qq), sum);
         }
       }
       // ---- 3a. the reducer's sum of the 8 row XCDs' partials --------------------------

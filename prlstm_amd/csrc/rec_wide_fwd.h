@@ -247,8 +247,10 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
       for (int rt = 0; rt < RT; ++rt) {
         const int ur = U / 4 * w + 4 * rt + lq;  // unit of the row group
         const int dst = x + kWideXcds * (r * kWideKBlocks + ur / SU);
-        const __amdgpu_buffer_rsrc_t d = wide_rsrc(inbox(t % kWidePSlots, c, dst) + (size_t)kb * S::PS, S::PS);
-        quad_put<FAST>(d, 4u * ((ur % SU) * 16 + l16), acc[rt][0] + acc[rt][1]);
+        // one descriptor over every workgroup's inbox of the slot (the same for all lanes: a
+        // descriptor that differs between lanes makes the compiler loop over its values)
+        const __amdgpu_buffer_rsrc_t d = wide_rsrc(inbox(t % kWidePSlots, c, 0), (size_t)kWideWgs * S::IW);
+        quad_put<FAST>(d, (unsigned)(dst * S::IW + kb * S::PS) + 4u * ((ur % SU) * 16 + l16), acc[rt][0] + acc[rt][1]);
       }
     }
   };

@@ -100,11 +100,13 @@ def test_timed_out_waits_in_graph_replay(dev, tiny_spin):
     assert _finite(out) and all(_finite(p.grad) for p in m.parameters())
 
 
-def test_timed_out_waits_wide_kernels(dev, tiny_spin):
-    """The W_hh-resident kernels for H = 2048 (rec_fwd_wide, rec_bwd_wide) bound their waits
-    the same way: an aborting workgroup fills what it owns with NaN and raises the device
-    word.  The forward is checked alone, then forward + backward."""
-    T, B, D, H = 4, 8, 32, 2048
+@pytest.mark.parametrize("H,B", [(2048, 8), (2048, 24), (1024, 24)])
+def test_timed_out_waits_wide_kernels(dev, tiny_spin, H, B):
+    """The W_hh-resident kernels (rec_fwd_wide, and rec_bwd_wide at H = 2048 or rec_bwd_wide1
+    at H = 1024) bound their waits the same way: an aborting workgroup fills what it owns
+    with NaN and raises the device word.  B = 8 runs one batch chain, B = 24 two.  The
+    forward is checked alone, then forward + backward."""
+    T, D = 4, 32
     torch.manual_seed(0)
     m = prlstm_amd.HeadStartLSTM(D, H).to(dev)
     x = torch.randn(T, B, D, device=dev)

@@ -204,6 +204,15 @@ def test_wide_forward_partial_batch_hx(dev, scope, H, B):
     assert prlstm_amd.last_recurrent_path() == 3
 
 
+@pytest.mark.parametrize("H", [1024, 2048])
+@pytest.mark.parametrize("T,B", [(1, 32), (2, 17)])
+def test_wide_short_sequences(dev, T, B, H):
+    """Edge cases of the wide kernels' chain schedule: one step (the second chain's first and
+    last iterations coincide) and two steps with a second chain of a single batch row."""
+    check(T, B, 64, H, dev, 0, a=[0.3, 0.5, 0.1, 0.2], fwd_path=3)
+    assert prlstm_amd.last_recurrent_path() == 3
+
+
 def test_sgd_training_step(dev):
     """test_cpp.py:110-147: one SGD step (MSE loss), updated parameters agree."""
     T, B, D, H, lr = 12, 4, 8, 12, 1e-2

@@ -1,9 +1,10 @@
 // Persistent recurrent kernels for a large hidden size, H = 32 U with U = 64 (H = 2048,
 // configs[3]) or U = 32 (H = 1024, the reference's published T64 B32 D512 H1024 shape),
 // B <= 32.  Included by recurrent.hip: they share that file's hand-off helpers and its
-// device error word.  This file holds what the wide forward (rec_wide_fwd.h) and backward
-// share -- the grid, the hand-off buffers and their access helpers, the slot rotation --
-// and the backward.
+// device error word.  This file holds what the wide forward (rec_wide_fwd.h) and the
+// backwards share -- the grid, the hand-off buffers and their access helpers, the slot
+// rotation, the 16x16x4 product helper -- and the two-chain backward run at H = 2048 (the
+// H = 1024 backward is the single-chain form of rec_wide_bwd32.h).
 //
 // W_hh stays in registers for the whole launch: 4H x H floats over 256 workgroups is
 // 256 KB per CU at H = 2048 and 64 KB at H = 1024, where the per-step path streams it

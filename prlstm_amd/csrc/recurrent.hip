@@ -2128,8 +2128,9 @@ int plan_persistent(int B, int H, int D, bool bwd, PersistentPlan* pl) {
   return HSL_OK;
 }
 
-// The W_hh-resident kernels for large H (rec_wide.h, rec_wide_fwd.h): H = 32 U with U = 64 (2048) or 32
-// (1024), B <= 32, eight XCDs and all 256 workgroups resident at once (one per CU).
+// The W_hh-resident kernels for large H (rec_wide.h, rec_wide_fwd.h, rec_wide_bwd32.h): H = 32 U
+// with U = 64 (2048) or 32 (1024), B <= 32, eight XCDs and all 256 workgroups resident at
+// once (one per CU).
 struct WidePlan {
   bool ok = false;
   int U = 0;

@@ -476,10 +476,18 @@ void x6_launch(X6Args g, bool vec, int splits, hipStream_t s) {
 
 }  // namespace
 
+namespace {
+// tiles of C = A B^T in a shape's tiling
+template <class S>
+long x6_tiles(int M, int N) {
+  return (long)((M + S::BM - 1) / S::BM) * ((N + S::BN - 1) / S::BN);
+}
+}  // namespace
+
 bool gemm_x6_applies(int M, int N, int K) {
-  // one 256 x 256 tile per CU at least, and enough k to amortise the tile's setup
-  const long tiles = (long)((M + ShapeProj::BM - 1) / ShapeProj::BM) * ((N + ShapeProj::BN - 1) / ShapeProj::BN);
-  return tiles >= 256 && K >= 32;
+  // one tile per CU at least (256 x 256, or else 256 x 128), and enough k to amortise the
+  // tile's setup
+  return (x6_tiles<ShapeProj>(M, N) >= 256 || x6_tiles<ShapeWgrad>(M, N) >= 256) && K >= 32;
 }
 
 int gemm_x6_longk_splits(int M, int N, int K) {
@@ -526,8 +534,10 @@ int gemm_x6_run(const float* A, const void* B, const float* bias, float* C, floa
     x6_launch<ShapeWgrad, false, false, 1>(g, vec, n, s);  // dgates^T x with a bf16 x
   else if (b_bf16)
     x6_launch<ShapeWgrad, true, false, 1>(g, vec, n, s);  // dgates W_ih with a bf16 W_ih
-  else if (!trans_a && trans_b)
+  else if (!trans_a && trans_b && x6_tiles<ShapeProj>(M, N) >= 256)
     x6_launch<ShapeProj, true, true>(g, vec, n, s);  // x W^T: both operands k-contiguous
+  else if (!trans_a && trans_b)
+    x6_launch<ShapeWgrad, true, true>(g, vec, n, s);  // the same on 256 x 128 tiles (fewer than 256 of 256 x 256)
   else if (trans_a)
     x6_launch<ShapeWgrad, false, false>(g, vec, n, s);  // A^T B: both row-contiguous
   else

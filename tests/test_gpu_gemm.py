@@ -97,9 +97,11 @@ def _both(A, B, bias, M, N, K, lda=None, ldb=None, ta=0, tb=1):
 
 
 @pytest.mark.parametrize("M,N,K,pad_a,pad_b", [(4096, 4096, 256, 0, 0), (4096 + 37, 4096 + 100, 207, 0, 0),
-                                               (4352, 4096, 96, 3, 1), (2048, 8192, 1024, 0, 0)])
+                                               (4352, 4096, 96, 3, 1), (2048, 8192, 1024, 0, 0),
+                                               (2048, 4096, 512, 0, 0), (2048 + 5, 4096 - 64, 300, 1, 0)])
 def test_split_products_as_accurate_as_fp32(dev, split_products, M, N, K, pad_a, pad_b):
-    """Large A B^T products (>= 256 tiles of 256x256) take the split-bf16 kernel: every
+    """Large A B^T products (>= 256 tiles of 256x256, or of 256x128: the last two shapes)
+    take the split-bf16 kernel: every
     fp32 operand is split exactly into three bf16 pieces and the six largest piece
     products are accumulated in fp32.  Against the fp64 product it must meet the fp32
     bound, and its error statistics must match those of the fp32 MFMA kernel on the
@@ -186,7 +188,7 @@ def test_split_products_weight_gradient_layout(dev, split_products, M, N, K, pad
     assert float(ex6.max()) <= 2.0 * float(e32.max()) + 1e-12
 
 
-@pytest.mark.parametrize("layout", ["abt", "atb", "ab"])
+@pytest.mark.parametrize("layout", ["abt", "abt_narrow", "atb", "ab"])
 @pytest.mark.parametrize("three_piece", ["a", "b"])
 def test_split_products_exact_on_representable_sums(dev, split_products, layout, three_piece):
     """Pins the piece bookkeeping of the split-bf16 kernels by exact arithmetic.  One
@@ -208,8 +210,8 @@ def test_split_products_exact_on_representable_sums(dev, split_products, layout,
     def pair(shape_a, shape_b):
         return (fine(*shape_a), sign(*shape_b)) if three_piece == "a" else (sign(*shape_a), fine(*shape_b))
 
-    if layout == "abt":  # C = A B^T, A [M,K], B [N,K]
-        M, N, K = 4096, 4096, 32
+    if layout.startswith("abt"):  # C = A B^T, A [M,K], B [N,K]; narrow: 256 tiles of 256x128
+        M, N, K = (4096, 4096, 32) if layout == "abt" else (2048, 4096, 32)
         a, b = pair((M, K), (N, K))
         exact, ta = a @ b.t(), 0
     else:
@@ -225,6 +227,6 @@ def test_split_products_exact_on_representable_sums(dev, split_products, layout,
             a, b = a * band[None, :], b * band[:, None]
             exact, ta = a @ b, 0
     print(f"exact sums layout={layout} three-piece operand={three_piece} M={M} N={N} K={K}", flush=True)
-    cx6, c32 = _both(a.float().to(dev), b.float().to(dev), None, M, N, K, ta=ta, tb=int(layout == "abt"))
+    cx6, c32 = _both(a.float().to(dev), b.float().to(dev), None, M, N, K, ta=ta, tb=int(layout.startswith("abt")))
     assert torch.equal(cx6, exact)
     assert torch.equal(c32, exact)

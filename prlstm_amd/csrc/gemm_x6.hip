@@ -80,6 +80,7 @@ struct X6Args {
   int kps;            // k per split (a multiple of kBK)
   int partial;
   int tiles_m, tiles_n;
+  int out_vec;  // output base and row stride 16-byte aligned (and the bias, if any)
 };
 
 
@@ -424,6 +425,41 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
 
   float* outp = g.partial ? g.out + (size_t)blockIdx.z * g.M * g.N : g.out;
   const int ldo = g.partial ? g.N : g.ldc;
+  if constexpr (FULL) {
+    if (g.out_vec) {
+      // Rows through LDS, written as 16-byte stores: a lane of the product layout holds
+      // one column of 16 rows, so direct stores are 4 bytes each (128 per lane for a
+      // 256x256 tile) and a wave cannot have more than 63 in flight; it then waits for
+      // stores before it can issue the next.  Each wave stages its 32-row slab of each
+      // 32-row block (32 x TN floats) in its own LDS region (the operand buffers, free
+      // after the last slice's barrier) and reads it back as rows: 16 lanes per 256-byte
+      // row segment, 4 rows per instruction, TN/16 instructions per slab.
+      static_assert(S::TN == 64, "16 lanes x 4 columns per slab row");
+      constexpr int kLds = S::TN + 4;  // padded slab row (floats)
+      static_assert(8 * 32 * kLds * sizeof(float) <= S::LDS, "slabs fit the operand buffers");
+      float* const slab = reinterpret_cast<float*>(sm) + wave * 32 * kLds;
+      const int rl = lane >> 4, cl = 4 * (lane & 15);
+      const int nb = n0 + wn * S::TN + cl;
+      const f4 bv = (!g.partial && g.bias) ? *reinterpret_cast<const f4*>(g.bias + nb) : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < S::FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < S::FN; ++j) {
+          const f16v& res = S::FOLD ? tot[S::FOLD ? i : 0][S::FOLD ? j : 0] : acc[i][j];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) slab[(8 * (r >> 2) + 4 * half + (r & 3)) * kLds + 32 * j + r32] = res[r];
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int row = 4 * q + rl;
+          const f4 v = *reinterpret_cast<const f4*>(&slab[row * kLds + cl]) + bv;
+          const int m = m0 + wm * S::TM + i * 32 + row;
+          __builtin_nontemporal_store(v, reinterpret_cast<f4*>(outp + (size_t)m * ldo + nb));
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < S::FM; ++i)
 #pragma unroll
@@ -530,6 +566,7 @@ int gemm_x6_run(const float* A, const void* B, const float* bias, float* C, floa
   const int n = (K + kps - 1) / kps;
   if (used) *used = n;
   const bool vec = aligned16(A) && aligned16(B) && lda % 4 == 0 && ldb % 4 == 0;
+  g.out_vec = aligned16(g.out) && (partial ? N % 4 == 0 : ldc % 4 == 0) && (g.bias == nullptr || aligned16(g.bias));
   if (b_bf16 && trans_a)
     x6_launch<ShapeWgrad, false, false, 1>(g, vec, n, s);  // dgates^T x with a bf16 x
   else if (b_bf16)

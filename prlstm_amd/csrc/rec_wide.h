@@ -262,10 +262,13 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
   // P: chain ch's operand of iteration k (a_g dg of iteration k-1), all NQ groups of the
   // wave, received with the first half of the products (the second half then waits for no
   // memory)
-  auto fetch = [&](int ch, int k, u4v (&q)[NQ]) -> bool {
+  auto fetch_issue = [&](int ch, int k, u4v (&q)[NQ]) {
     const __amdgpu_buffer_rsrc_t src = wide_rsrc(xbuf(k - 1, ch) + 64 * U * w, 64 * U);
 #pragma unroll
     for (int j = 0; j < NQ; ++j) q[j] = quad_load(src, 256u * j + 4u * lane);
+  };
+  auto fetch_settle = [&](int ch, int k, u4v (&q)[NQ]) -> bool {
+    const __amdgpu_buffer_rsrc_t src = wide_rsrc(xbuf(k - 1, ch) + 64 * U * w, 64 * U);
     const long long t0 = wall_clock64();
     while (true) {  // all of the lane's groups reloaded while any word is kEmpty
       unsigned m = 0u;
@@ -296,6 +299,10 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
   // S: chain ch's partials of iteration k summed over the waves, sent to the reducers.  D of
   // tile ct: lane l, register i -> column 16 ct + 4 (l/16) + i, batch row l%16; the chain's
   // red[w][column quad][batch row] holds 4 columns
+  auto fetch = [&](int ch, int k, u4v (&q)[NQ]) -> bool {
+    fetch_issue(ch, k, q);
+    return fetch_settle(ch, k, q);
+  };
   auto send = [&](int ch, int k, f4 (&acc)[CT][2]) -> bool {
     wide_drain16<CT>(acc);
     float* const rb = red + ch * 4 * S::RED;
@@ -304,15 +311,18 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
       *reinterpret_cast<f4*>(&rb[((w * (U / 4) + 4 * ct + lq) * 16 + l16) * 4]) = acc[ct][0] + acc[ct][1];
     lds_barrier();
     if (abort_flag) return false;
-    if (sender && 16 * ch + sb < B) {
+    {
       // one descriptor over every workgroup's inbox of the slot (the same for all lanes: a
-      // descriptor that differs between lanes makes the compiler loop over its values)
+      // descriptor that differs between lanes makes the compiler loop over its values);
+      // every lane stores, lanes without a partial past the descriptor's end (dropped), so
+      // that the store's count in the completion counter does not depend on the lane
       const __amdgpu_buffer_rsrc_t d = wide_rsrc(inbox(k - 1, ch, 0), (size_t)kWideWgs * S::INBOX);
+      const bool mine = sender && 16 * ch + sb < B;
       const int cq = S::QS * c4 + qq;
       f4 sum = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ww = 0; ww < 4; ++ww) sum = sum + *reinterpret_cast<const f4*>(&rb[((ww * (U / 4) + cq) * 16 + sb) * 4]);
-      quad_put<false>(d, (unsigned)(dst * S::INBOX + x * 16 * SU + sb * SU + 4 * qq), sum);
+      for (int ww = 0; ww < 4; ++ww) sum = sum + *reinterpret_cast<const f4*>(&rb[((ww * (U / 4) + (mine ? cq : 0)) * 16 + (mine ? sb : 0)) * 4]);
+      quad_put<false>(d, mine ? (unsigned)(dst * S::INBOX + x * 16 * SU + sb * SU + 4 * qq) : (unsigned)(kWideWgs * S::INBOX), sum);
     }
     return true;
   };
@@ -401,10 +411,16 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
       if (!reduce(1, k - 1)) return false;  // 2
     }
     mult(q, IC1{}, acc);  // 3
+    if constexpr (NCH > 1) {
+      // chain 1's operand requested before chain 0's send, whose first instructions wait
+      // for the last products' results (q's last readers were issued 24 wait states before)
+      wide_drain16<CT>(acc);
+      fetch_issue(1, k, q);
+    }
     if (!send(0, k, acc)) return false;
     if constexpr (NCH > 1) {
       zero_acc(acc);
-      if (!fetch(1, k, q)) return false;  // 4
+      if (!fetch_settle(1, k, q)) return false;  // 4
       mult(q, IC0{}, acc);
     }
     if (!reduce(0, k)) return false;  // 5

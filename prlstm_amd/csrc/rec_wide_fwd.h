@@ -182,13 +182,18 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
   // Poll loads are issued by every lane, unconditionally: a lane without a value reads
   // from past the end of the buffer (0, never kEmpty).
   auto recv_off = [&](int c, int j) { return 16 * c + l16 < B ? 256u * j + 4u * lane : (unsigned)S::HB; };
-  auto recv = [&](int c, int tin) -> bool {
+  // recv_issue requests the words (at H = 2048 right after the last products of a phase,
+  // so that their latency overlaps the wait of the following send for those products'
+  // results), recv_settle polls until none is kEmpty and writes them to LDS
+  auto recv_issue = [&](int c, int tin, u4v (&q4)[BQ]) {
+    const __amdgpu_buffer_rsrc_t src = recv_src(c, tin);
+#pragma unroll
+    for (int j = 0; j < BQ; ++j) q4[j] = quad_load(src, recv_off(c, j));
+  };
+  auto recv_settle = [&](int c, int tin, u4v (&q4)[BQ]) -> bool {
     f4* const buf = hs + (size_t)c * NQ * 64;
     const __amdgpu_buffer_rsrc_t src = recv_src(c, tin);
     const bool h_ok = 16 * c + l16 < B;
-    u4v q4[BQ];
-#pragma unroll
-    for (int j = 0; j < BQ; ++j) q4[j] = quad_load(src, recv_off(c, j));
     const long long t0 = wall_clock64();
     while (true) {  // all of the lane's groups reloaded while any word is kEmpty
       unsigned m = 0u;
@@ -240,18 +245,21 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
     for (int rt = 0; rt < RT; ++rt) acc[rt][0] = acc[rt][1] = f4{0.f, 0.f, 0.f, 0.f};
   };
   // chain c's partials of step t to the cell workgroups
+  // (every lane stores: a lane of an absent batch row past the descriptor's end, where the
+  // store is dropped, so that the stores' count in the completion counter does not depend
+  // on the lane)
   auto send = [&](int c, int t, f4 (&acc)[RT][2]) {
     wide_drain16<RT>(acc);
-    if (16 * c + l16 < B) {
+    const bool mine = 16 * c + l16 < B;
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const int ur = U / 4 * w + 4 * rt + lq;  // unit of the row group
-        const int dst = x + kWideXcds * (r * kWideKBlocks + ur / SU);
-        // one descriptor over every workgroup's inbox of the slot (the same for all lanes: a
-        // descriptor that differs between lanes makes the compiler loop over its values)
-        const __amdgpu_buffer_rsrc_t d = wide_rsrc(inbox(t % kWidePSlots, c, 0), (size_t)kWideWgs * S::IW);
-        quad_put<FAST>(d, (unsigned)(dst * S::IW + kb * S::PS) + 4u * ((ur % SU) * 16 + l16), acc[rt][0] + acc[rt][1]);
-      }
+    for (int rt = 0; rt < RT; ++rt) {
+      const int ur = U / 4 * w + 4 * rt + lq;  // unit of the row group
+      const int dst = x + kWideXcds * (r * kWideKBlocks + ur / SU);
+      // one descriptor over every workgroup's inbox of the slot (the same for all lanes: a
+      // descriptor that differs between lanes makes the compiler loop over its values)
+      const __amdgpu_buffer_rsrc_t d = wide_rsrc(inbox(t % kWidePSlots, c, 0), (size_t)kWideWgs * S::IW);
+      quad_put<FAST>(d, mine ? (unsigned)(dst * S::IW + kb * S::PS) + 4u * ((ur % SU) * 16 + l16) : (unsigned)(kWideWgs * S::IW),
+                     acc[rt][0] + acc[rt][1]);
     }
   };
 
@@ -342,10 +350,20 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
       if (!cells(1, t - 1, gin1)) return false;
     }
     products(0, ICH{}, ICN{}, acc);                                     // 3
+    // At H = 2048 a receive's words are requested before the preceding send (configs[3]
+    // 2.43 -> 2.40 ms per step); at H = 1024 that measured slower (1.048 -> 1.067 ms) and
+    // the words are requested after it.
+    constexpr bool kAhead = U == 64;
+    u4v hq[BQ];
+    if constexpr (NCH > 1 && !FIRST && kAhead) {
+      wide_drain16<RT>(acc);  // the products' last operand reads are done
+      recv_issue(1, t - 1, hq);
+    }
     send(0, t, acc);
     if constexpr (NCH > 1) {
       if constexpr (!FIRST) {                                           // 4
-        if (!recv(1, t - 1)) return false;
+        if constexpr (!kAhead) recv_issue(1, t - 1, hq);
+        if (!recv_settle(1, t - 1, hq)) return false;
         lds_barrier();
         if (abort_flag) return false;
       }
@@ -356,9 +374,16 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
     if (!cells(0, t, gin0)) return false;                               // 6
     if constexpr (NCH > 1) {
       products(1, ICH{}, ICN{}, acc);                                   // 7
+      if constexpr (kAhead) {
+        wide_drain16<RT>(acc);
+        recv_issue(0, t, hq);
+      }
       send(1, t, acc);
+      if constexpr (!kAhead) recv_issue(0, t, hq);
+    } else {
+      recv_issue(0, t, hq);
     }
-    if (!recv(0, t)) return false;                                      // 8
+    if (!recv_settle(0, t, hq)) return false;                           // 8
     lds_barrier();
     return !abort_flag;
   };

@@ -28,7 +28,8 @@
 //   6. chain 0's cells of step t (partials sent in step 3), h0_t published;
 //   7. second half of chain 1's products, partials sent;
 //   8. h0_t received into LDS (its hand-off ran under step 7).
-// Chain 1's cells of the last step follow the loop.
+// Chain 1's cells of the last step follow the loop.  At H = 2048 the words of the receives
+// in steps 4 and 8 are requested before the sends of steps 3 and 7.
 //
 // Wave w holds the rows of units [U w / 4, +U/4) (U/16 row tiles of 16) for all 4U k of the
 // workgroup (U k-steps of 4): U^2/16 values per lane in the accumulator registers.

@@ -546,13 +546,6 @@ __device__ __forceinline__ unsigned xcc_id() {
 }
 
 
-// Within-wave ordering of LDS writes before reads by other lanes of the same wave.
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // Every workgroup of the group publishes its XCD id (device-scope) and reads all of
 // the group's; returns true when they are all equal.  All members see the same words,
 // so they all choose the same store mode.  Returns false and sets *abort on timeout.
@@ -2544,7 +2537,7 @@ int hsl_rec_fwd(const float* x, const float* h0, const float* c0, const float* w
   }
   if (!(pl.ok && pl.XP)) {
     // input projection for all T at once (_torch.py:96)
-    GemmDesc g1{x, w_ih, b_ih, w.gih, T * B, 4 * H, D, D, D, 4 * H, 0, 1};
+    GemmDesc g1{x, w_ih, b_ih, w.gih, T * B, 4 * H, D, D, D, 4 * H, 0, 1, 0};
     const int tslot = timing_begin(kTimeInputProj, s);
     HSL_CHECK(gemm_run(g1, nullptr, 0, s));
     timing_end(tslot, s);

@@ -438,7 +438,7 @@ int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float*
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (T == 0 || B == 0 || H == 0) return HSL_OK;
   if (!x || !w_ih || !b_ih || !gates || !out || !c_seq) return fail(HSL_ERR_ARG, "hsl_par_fwd: null pointer");
-  GemmDesc g1{x, w_ih, b_ih, gates, T * B, 4 * H, D, D, D, 4 * H, 0, 1};
+  GemmDesc g1{x, w_ih, b_ih, gates, T * B, 4 * H, D, D, D, 4 * H, 0, 1, 0};
   const int slot = timing_begin(kTimeInputProj, s);
   HSL_CHECK(gemm_run(g1, nullptr, 0, s));
   timing_end(slot, s);

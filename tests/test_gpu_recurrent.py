@@ -205,10 +205,11 @@ def test_wide_forward_partial_batch_hx(dev, scope, H, B):
 
 
 @pytest.mark.parametrize("H", [1024, 2048])
-@pytest.mark.parametrize("T,B", [(1, 32), (2, 17)])
+@pytest.mark.parametrize("T,B", [(1, 32), (2, 17), (3, 1), (3, 16), (3, 31)])
 def test_wide_short_sequences(dev, T, B, H):
     """Edge cases of the wide kernels' chain schedule: one step (the second chain's first and
-    last iterations coincide) and two steps with a second chain of a single batch row."""
+    last iterations coincide), a second chain of a single batch row, one batch row in all,
+    exactly one full chain, and a second chain one row short."""
     check(T, B, 64, H, dev, 0, a=[0.3, 0.5, 0.1, 0.2], fwd_path=3)
     assert prlstm_amd.last_recurrent_path() == 3
 

@@ -166,14 +166,14 @@ def bench_scan(args):
     c0 = torch.zeros(SB, SH, device=dev)
     gates = torch.empty(ST, SB, 4 * SH, device=dev)
     out = torch.empty(ST, SB, SH, device=dev)
-    c_seq = torch.empty(ST, SB, SH, device=dev)
+    c_ck = torch.empty(_lib.load().hsl_scan_ck_rows(ST), SB, SH, device=dev)
     dout = torch.randn(ST, SB, SH, device=dev)
     dh_n = torch.zeros(SB, SH, device=dev)
     dc_n = torch.zeros(SB, SH, device=dev)
     dgates = torch.empty(ST, SB, 4 * SH, device=dev)
     db_part = torch.empty(SB, 4 * SH, dtype=torch.float64, device=dev)
     P, s = _lib.ptr, _lib.stream_of(dev)
-    _lib.call("hsl_par_fwd", P(x), P(c0), P(w_ih), P(b_ih), 1e-6, P(gates), P(out), P(c_seq),
+    _lib.call("hsl_par_fwd", P(x), P(c0), P(w_ih), P(b_ih), 1e-6, P(gates), P(out), P(c_ck),
               ST, SB, SD, SH, s)
     reps = max(3, args.steps // 2)
     for warm in (True, False):
@@ -182,21 +182,24 @@ def bench_scan(args):
             _lib.timing_collect("scan_fwd")
             _lib.timing_collect("scan_bwd")
         for _ in range(1 if warm else reps):
-            _lib.call("hsl_scan_fwd", P(gates), P(c0), 1e-6, P(out), P(c_seq), ST, SB, SH, s)
-            _lib.call("hsl_scan_bwd", P(gates), P(c0), P(c_seq), P(dout), P(dh_n), P(dc_n), 1e-6,
+            _lib.call("hsl_scan_fwd", P(gates), P(c0), 1e-6, P(out), P(c_ck), ST, SB, SH, s)
+            _lib.call("hsl_scan_bwd", P(gates), P(c0), P(c_ck), P(dout), P(dh_n), P(dc_n), 1e-6,
                       P(dgates), P(db_part), None, ST, SB, SH, s)
     torch.cuda.synchronize()
     # known-size elementwise kernel (reads and writes 256 MiB each) for calibrating
     # the FETCH_SIZE / WRITE_SIZE counters of rocprofv3 --pmc runs of this script
     calib = out.view(-1)[: 64 * 2 ** 20]
-    torch.mul(c_seq.view(-1)[: 64 * 2 ** 20], 1.0, out=calib)
+    torch.mul(dout.view(-1)[: 64 * 2 ** 20], 1.0, out=calib)
     torch.cuda.synchronize()
     tf, nf = _lib.timing_collect("scan_fwd")
     tb, nb = _lib.timing_collect("scan_bwd")
     _lib.set_timing(False)
     fwd_ms, bwd_ms = tf / nf, tb / nb
     n = ST * SB * SH
-    fwd_b, bwd_b = 24 * n, 40 * n
+    # per element: forward reads 4 gates, writes out; backward reads 4 gates and dout, writes
+    # 4 dgates; plus the rows of c kept every 8th step (written once, read back once)
+    ck = _lib.load().hsl_scan_ck_rows(ST) * SB * SH
+    fwd_b, bwd_b = 20 * n + 4 * ck, 36 * n + 4 * (ck - SB * SH)
     res = {
         "config": {"workload": "parallel scan fwd+bwd kernels, configs[4]", "T": ST, "B": SB, "H": SH},
         "fwd_ms": round(fwd_ms, 5), "bwd_ms": round(bwd_ms, 5),

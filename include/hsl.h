@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define HSL_ABI_VERSION 1
+#define HSL_ABI_VERSION 2
 
 enum hsl_status {
   HSL_OK = 0,
@@ -194,10 +194,14 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n,
 /* Forward: gates = x W_ih^T + b_ih ([T,B,4H], kept for the backward), then the
  * scan c_t = max(f_t,eps) c_{t-1} + max(i_t g_t, eps), c_{-1} = max(c0,eps)
  * (the recurrence _parallel.py:21-35 evaluates in the log domain), and
- * out_t = o_t tanh(c_t).  Writes gates, out [T,B,H], c_seq [T,B,H].
- * h_n = out[T-1], c_n = c_seq[T-1] (_parallel.py:74). */
+ * out_t = o_t tanh(c_t).  Writes gates, out [T,B,H] and c_ck
+ * [hsl_scan_ck_rows(T), B, H]: the cell state at every 8th step, kept for the
+ * backward (row m < R-1 is the state carried into step 8m, row 0 = max(c0,eps)),
+ * and c_n in its last row R-1.
+ * h_n = out[T-1], c_n = c_ck[R-1] (_parallel.py:74). */
+int hsl_scan_ck_rows(int T); /* R = ceil(T/8) + 1 */
 int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float* b_ih,
-                float eps, float* gates, float* out, float* c_seq,
+                float eps, float* gates, float* out, float* c_ck,
                 int T, int B, int D, int H, void* stream);
 
 /* hsl_par_fwd for a half-precision module: x [T,B,D] and w_ih [4H,D] are bf16
@@ -208,7 +212,7 @@ int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float*
  * hsl_par_fwd (_parallel.py:38-74) for modules moved to bf16/fp16 (the way
  * test_parallel.py:22-38 runs bf16). */
 int hsl_par_fwd_b16(const void* x, const float* c0, const void* w_ih, const float* b_ih,
-                    float eps, float* gates, float* out, float* c_seq,
+                    float eps, float* gates, float* out, float* c_ck,
                     int T, int B, int D, int H, int fmt, void* stream);
 
 size_t hsl_par_bwd_ws_bytes(int T, int B, int D, int H);
@@ -218,7 +222,7 @@ size_t hsl_par_bwd_ws_bytes(int T, int B, int D, int H);
  * dout [T,B,H], dh_n/dc_n [B,H] are the gradients of out, h_n, c_n.
  * dx and dc0 may be NULL (then they are not computed). */
 int hsl_par_bwd(const float* dout, const float* dh_n, const float* dc_n,
-                const float* x, const float* c0, const float* gates, const float* c_seq,
+                const float* x, const float* c0, const float* gates, const float* c_ck,
                 const float* w_ih, float eps,
                 float* dx, float* dw_ih, float* db_ih, float* dc0,
                 void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream);
@@ -233,19 +237,20 @@ int hsl_par_bwd(const float* dout, const float* dh_n, const float* dc_n,
  * test_parallel.py:22-38). */
 size_t hsl_par_bwd_b16_ws_bytes(int T, int B, int D, int H);
 int hsl_par_bwd_b16(const float* dout, const float* dh_n, const float* dc_n,
-                    const void* x, const float* c0, const float* gates, const float* c_seq,
+                    const void* x, const float* c0, const float* gates, const float* c_ck,
                     const void* w_ih, float eps,
                     float* dx, float* dw_ih, float* db_ih, float* dc0,
                     void* ws, size_t ws_bytes, int T, int B, int D, int H, int fmt, void* stream);
 
 /* The scan kernels on their own (used by hsl_par_fwd / hsl_par_bwd).
- * hsl_scan_fwd: gates [T,B,4H] pre-activations -> out, c_seq [T,B,H].
+ * hsl_scan_fwd: gates [T,B,4H] pre-activations -> out [T,B,H], c_ck (as in
+ * hsl_par_fwd).
  * hsl_scan_bwd: -> dgates [T,B,4H] (pre-activation gradients) and, when
  * db_part is non-NULL, per-batch column sums of dgates as doubles [B,4H];
  * dc0 may be NULL. */
 int hsl_scan_fwd(const float* gates, const float* c0, float eps,
-                 float* out, float* c_seq, int T, int B, int H, void* stream);
-int hsl_scan_bwd(const float* gates, const float* c0, const float* c_seq,
+                 float* out, float* c_ck, int T, int B, int H, void* stream);
+int hsl_scan_bwd(const float* gates, const float* c0, const float* c_ck,
                  const float* dout, const float* dh_n, const float* dc_n, float eps,
                  float* dgates, double* db_part, float* dc0,
                  int T, int B, int H, void* stream);

@@ -11,7 +11,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libhsl.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -45,6 +45,7 @@ SIGNATURES = {
     "hsl_par_bwd": (_I, [_P] * 8 + [_F, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _P]),
     "hsl_par_bwd_b16_ws_bytes": (_Z, [_I, _I, _I, _I]),
     "hsl_par_bwd_b16": (_I, [_P] * 8 + [_F, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _P]),
+    "hsl_scan_ck_rows": (_I, [_I]),
     "hsl_scan_fwd": (_I, [_P, _P, _F, _P, _P, _I, _I, _I, _P]),
     "hsl_scan_bwd": (_I, [_P] * 6 + [_F, _P, _P, _P, _I, _I, _I, _P]),
     "hsl_gemm_ws_bytes": (_Z, [_I, _I, _I]),

@@ -15,7 +15,7 @@
 // scan G_t = e_t + f~_{t+1} G_{t+1} of the total gradient G_t = dL/dc_t; the clamps
 // pass gradient where their input is >= eps (torch's clamp_min rule).
 //
-// Layout: gates [T,B,4H] (the GEMM output, never transposed), out/c [T,B,H].  One
+// Layout: gates [T,B,4H] (the GEMM output, never transposed), out [T,B,H].  One
 // workgroup owns 64 consecutive channels (b,j) = one wave-width, so every load and
 // store is a 256-byte row segment, and walks all of T in chunks of NW*L steps: each
 // of the NW waves takes L consecutive steps, composes them into one map, the maps
@@ -23,6 +23,13 @@
 // next chunk's loads are issued before the current chunk is processed.  Every [T,...]
 // stream is read or written once, with non-temporal accesses (the streams bypass the
 // caches' retention; measured 9% faster forward on MI355X).
+//
+// The cell state is not stored per step.  The forward writes c_ck [ceil(T/8)+1, B, H]:
+// row m is the state carried into step 8m (row 0 = max(c0, eps)), i.e. the carry-in from
+// which the wave holding steps 8m .. 8m+7 runs them, and the last row is c_{T-1} = c_n.
+// The backward's waves hold the same 8-step groups and re-run c_t from the row with the
+// forward's own operations, so its c_t equal the forward's bit for bit, and the scans move
+// 20.5 + 36.5 bytes per element instead of 24 + 40.
 //
 // The streams are raw buffer accesses with a uniform base per time step (no 64-bit
 // address arithmetic per lane; the kernels then run at the HBM rate this access pattern
@@ -41,11 +48,13 @@ namespace {
 
 constexpr int kFwdWaves = 16, kFwdSteps = 8;
 constexpr int kBwdWaves = 8, kBwdSteps = 8;
+constexpr int kCkSteps = 8;  // steps per checkpoint row of c (one wave's group in both scans)
 
 template <int NW, int L>
 __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restrict__ gates, const float* __restrict__ c0,
-                                                          float eps, float* __restrict__ out, float* __restrict__ cseq,
+                                                          float eps, float* __restrict__ out, float* __restrict__ cck,
                                                           int T, int B, int H) {
+  static_assert(L == kCkSteps, "checkpoint rows are one per L-step group");
   __shared__ float2 sAV[NW][64];  // each wave's composed map (A, V) of the chunk
   __shared__ float sC[64];
   const int lane = threadIdx.x & 63;
@@ -63,6 +72,7 @@ __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restri
 
   constexpr int CH = NW * L;
   const int nchunks = (T + CH - 1) / CH, nfull = T / CH;
+  const int nck = (T + L - 1) / L;  // the c_n row
   // the step loads: rows past T have size 0 (they read 0)
   auto load = [&](int chunk, float(&r)[4][L]) {
 #pragma unroll
@@ -109,15 +119,19 @@ __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restri
       for (int i = 0; i < 4; ++i)
         if (u0 + i < w) c = m[i].x * c + m[i].y;
     }
+    // the carry-in is this group's checkpoint row (groups past T store nothing)
+    const int t0 = k * CH + w * L;
+    row_store_nt(c, row_rsrc(cck + (size_t)(k * NW + w) * ostride, t0 < T ? orow : 0u), ov, 0);
 #pragma unroll
     for (int s = 0; s < L; ++s) {
-      const int t = k * CH + w * L + s;
+      const int t = t0 + s;
       const unsigned obytes = (!TAIL || t < T) ? orow : 0u;
-      c = fv[s] * c + bv[s];
+      c = __builtin_fmaf(fv[s], c, bv[s]);  // the backward repeats exactly this from the carry-in
       // c >= eps > 0 (a positive combination of positive terms)
       row_store_nt(ogv[s] * tanh_pos_f(c), row_rsrc(out + (size_t)t * ostride, obytes), ov, 0);
-      row_store_nt(c, row_rsrc(cseq + (size_t)t * ostride, obytes), ov, 0);
     }
+    // the group holding step T-1 writes c_{T-1} (steps past T are identity maps)
+    row_store_nt(c, row_rsrc(cck + (size_t)nck * ostride, (t0 < T && T <= t0 + L) ? orow : 0u), ov, 0);
     lds_barrier();
     if (w == NW - 1) sC[lane] = c;
   };
@@ -139,9 +153,10 @@ __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restri
 // Then df~_t = G_t c_{t-1}, db~_t = G_t and the sigmoid/clamp chain gives dgates.
 template <int NW, int L>
 __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
-    const float* __restrict__ gates, const float* __restrict__ c0, const float* __restrict__ cseq,
+    const float* __restrict__ gates, const float* __restrict__ c0, const float* __restrict__ cck,
     const float* __restrict__ dout, const float* __restrict__ dh_n, const float* __restrict__ dc_n, float eps,
     float* __restrict__ dgates, double* __restrict__ db_part, float* __restrict__ dc0, int T, int B, int H) {
+  static_assert(L == kCkSteps, "a wave's steps are one checkpoint group");
   __shared__ float2 sAV[NW][64];  // each wave's composed reverse map (A, V) of the chunk
   __shared__ float sG[64];
   __shared__ double sdb[NW][4][64];
@@ -157,16 +172,15 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
   const unsigned ov = ok ? (unsigned)ch * 4u : kOffNone;
   const int hb = 4 * H;
   const float c0v = (ok && c0) ? c0[ch] : 0.f;
-  const float c0c = ok ? fmaxf(c0v, eps) : 0.f;
   const bool c0_pass = ok && c0v >= eps;
   const float dhn = (ok && dh_n) ? dh_n[ch] : 0.f, dcn = (ok && dc_n) ? dc_n[ch] : 0.f;
   if (w == 0) sG[lane] = 0.f;
 
   constexpr int CH = NW * L;
   const int nchunks = (T + CH - 1) / CH;
-  // per step: zi zf zg zo c dout; plus zf at we+1 (fnext) and c at ws-1 (cprev); rows past
-  // T read 0
-  auto load = [&](int chunk, float(&r)[6][L], float& fnext, float& cprev) {
+  // per step: zi zf zg zo dout; plus zf at we+1 (fnext) and the group's checkpoint row, the
+  // c carried into its first step (cin); rows past T read 0
+  auto load = [&](int chunk, float(&r)[5][L], float& fnext, float& cin) {
     const int ws = chunk * CH + w * L;
 #pragma unroll
     for (int s = 0; s < L; ++s) {
@@ -174,39 +188,40 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
       const auto rg = row_rsrc(gates + (size_t)t * gstride, t < T ? grow : 0u);
 #pragma unroll
       for (int g = 0; g < 4; ++g) r[g][s] = row_load(rg, gv, g * hb);
-      r[4][s] = row_load(row_rsrc(cseq + (size_t)t * ostride, t < T ? orow : 0u), ov, 0);
-      r[5][s] = row_load(row_rsrc(dout + (size_t)t * ostride, t < T ? orow : 0u), ov, 0);
+      r[4][s] = row_load(row_rsrc(dout + (size_t)t * ostride, t < T ? orow : 0u), ov, 0);
     }
     const int tn = ws + L;
     fnext = row_load<0>(row_rsrc(gates + (size_t)tn * gstride, tn < T ? grow : 0u), gv, hb);
-    const int tp = ws > 0 ? ws - 1 : 0;
-    const float cp = row_load<0>(row_rsrc(cseq + (size_t)tp * ostride, (ws > 0 && tp < T) ? orow : 0u), ov, 0);
-    cprev = ws == 0 ? c0c : cp;
+    cin = row_load(row_rsrc(cck + (size_t)(chunk * NW + w) * ostride, ws < T ? orow : 0u), ov, 0);
   };
   double dbacc[4] = {0.0, 0.0, 0.0, 0.0};
   float g_first = 0.f, f_first = 0.f;  // G and f~ at this wave's first step (for dc0)
   // one chunk (reverse); LAST: the chunk holding step T-1, the only one with steps at or
   // past T-1 (dh_n, dc_n, f~_T = 0, identity maps past T)
-  auto chunk = [&](auto last, int k, float(&cur)[6][L], float cur_fn, float cur_cp, float(&nxt)[6][L],
-                   float& nxt_fn, float& nxt_cp) {
+  auto chunk = [&](auto last, int k, float(&cur)[5][L], float cur_fn, float cur_cin, float(&nxt)[5][L],
+                   float& nxt_fn, float& nxt_cin) {
     constexpr bool LAST = decltype(last)::value;
-    if (k > 0) load(k - 1, nxt, nxt_fn, nxt_cp);
+    if (k > 0) load(k - 1, nxt, nxt_fn, nxt_cin);
     const int ws = k * CH + w * L;
-    // sigma(z_f), sigma(z_o) and tanh(c) of each step, computed once and used by both
-    // passes; f~_{t+1} (0 beyond T) is step s+1's sigma(z_f), e_t
-    float fgv[L], ogv[L], tcv[L], fn[L], ev[L];
+    // sigma(z_f), sigma(z_o), c and tanh(c) of each step, computed once and used by both
+    // passes; c_t is recomputed from the carry-in by the forward's own operations, so it
+    // equals the forward's bit for bit; f~_{t+1} (0 beyond T) is step s+1's sigma(z_f), e_t
+    float fgv[L], ogv[L], cv[L], tcv[L], fn[L], ev[L];
+    float c = cur_cin;
 #pragma unroll
     for (int s = 0; s < L; ++s) {
       fgv[s] = sigmoid_f(cur[1][s]);
       ogv[s] = sigmoid_f(cur[3][s]);
-      tcv[s] = tanh_pos_f(cur[4][s]);  // c >= eps > 0
+      c = __builtin_fmaf(fmaxf(fgv[s], eps), c, fmaxf(sigmoid_prod_f(cur[0][s], cur[2][s]), eps));
+      cv[s] = c;
+      tcv[s] = tanh_pos_f(c);  // c >= eps > 0
     }
     const float fg_after = sigmoid_f(cur_fn);
 #pragma unroll
     for (int s = 0; s < L; ++s) {
       const int t = ws + s;
       fn[s] = (!LAST || t + 1 < T) ? fmaxf(s + 1 < L ? fgv[s + 1] : fg_after, eps) : 0.f;
-      float d = cur[5][s];
+      float d = cur[4][s];
       if (LAST && t == T - 1) d = d + dhn;
       float e = d * ogv[s] * (1.0f - tcv[s] * tcv[s]);
       if (LAST && t == T - 1) e = e + dcn;
@@ -242,8 +257,8 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
         G = ev[s] + fn[s] * G;
         const float ig = sigmoid_f(cur[0][s]), gg = sigmoid_f(cur[2][s]);
         const float fg = fgv[s], og = ogv[s], tc = tcv[s];
-        const float cprev = s > 0 ? cur[4][s - 1] : cur_cp;
-        float d = cur[5][s];
+        const float cprev = s > 0 ? cv[s - 1] : cur_cin;
+        float d = cur[4][s];
         if (LAST && t == T - 1) d = d + dhn;
         const float bb = ig * gg;
         const float dbb = bb >= eps ? G : 0.f;
@@ -273,7 +288,7 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
     if (w == 0) sG[lane] = G;
   };
   // chunks alternate between two register sets, so no copies between them
-  float ra[6][L], rb[6][L];
+  float ra[5][L], rb[5][L];
   float fa = 0.f, pa = 0.f, fb = 0.f, pb = 0.f;
   if (nchunks > 0) {
     load(nchunks - 1, ra, fa, pa);
@@ -305,19 +320,19 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
 // one time step of gates (16 B H bytes) is addressed as a buffer of < 2^31 bytes
 int check_scan_dims(int T, int B, int H, int D = 0) { return check_shape("parallel mode", T, B, D, H); }
 
-int scan_fwd(const float* gates, const float* c0, float eps, float* out, float* cseq, int T, int B, int H,
+int scan_fwd(const float* gates, const float* c0, float eps, float* out, float* cck, int T, int B, int H,
              hipStream_t s) {
   const int C = B * H;
   if (C == 0 || T == 0) return HSL_OK;
   const int slot = timing_begin(kTimeScanFwd, s);
   hipLaunchKernelGGL((scan_fwd_kernel<kFwdWaves, kFwdSteps>), dim3((C + 63) / 64), dim3(kFwdWaves * 64), 0, s, gates,
-                     c0, eps, out, cseq, T, B, H);
+                     c0, eps, out, cck, T, B, H);
   HSL_HIP(hipGetLastError());
   timing_end(slot, s);
   return HSL_OK;
 }
 
-int scan_bwd(const float* gates, const float* c0, const float* cseq, const float* dout, const float* dh_n,
+int scan_bwd(const float* gates, const float* c0, const float* cck, const float* dout, const float* dh_n,
              const float* dc_n, float eps, float* dgates, double* db_part, float* dc0, int T, int B, int H,
              hipStream_t s) {
   const int C = B * H;
@@ -329,7 +344,7 @@ int scan_bwd(const float* gates, const float* c0, const float* cseq, const float
   }
   const int slot = timing_begin(kTimeScanBwd, s);
   hipLaunchKernelGGL((scan_bwd_kernel<kBwdWaves, kBwdSteps>), dim3((C + 63) / 64), dim3(kBwdWaves * 64), 0, s, gates,
-                     c0, cseq, dout, dh_n, dc_n, eps, dgates, db_part, dc0, T, B, H);
+                     c0, cck, dout, dh_n, dc_n, eps, dgates, db_part, dc0, T, B, H);
   HSL_HIP(hipGetLastError());
   timing_end(slot, s);
   return HSL_OK;
@@ -368,7 +383,7 @@ size_t carve_par_b16(void* ws, size_t cap, int T, int B, int D, int H, ParWs* o,
 }
 
 int par_bwd_impl(const float* dout, const float* dh_n, const float* dc_n, const void* x, const float* c0,
-                 const float* gates, const float* c_seq, const void* w_ih, float eps, float* dx, float* dw_ih,
+                 const float* gates, const float* c_ck, const void* w_ih, float eps, float* dx, float* dw_ih,
                  float* db_ih, float* dc0, void* ws, size_t ws_bytes, int T, int B, int D, int H, int fmt,
                  hipStream_t s) {
   const char* fn = fmt < 0 ? "hsl_par_bwd" : "hsl_par_bwd_b16";
@@ -386,8 +401,8 @@ int par_bwd_impl(const float* dout, const float* dh_n, const float* dc_n, const 
     if (dc0) HSL_CHECK(copy_f32(dc0, nullptr, (size_t)B * H, s));
     return HSL_OK;
   }
-  if (!dout || !x || !gates || !c_seq) return fail(HSL_ERR_ARG, "%s: null pointer", fn);
-  HSL_CHECK(scan_bwd(gates, c0, c_seq, dout, dh_n, dc_n, eps, w.dgates, w.db_part, dc0, T, B, H, s));
+  if (!dout || !x || !gates || !c_ck) return fail(HSL_ERR_ARG, "%s: null pointer", fn);
+  HSL_CHECK(scan_bwd(gates, c0, c_ck, dout, dh_n, dc_n, eps, w.dgates, w.db_part, dc0, T, B, H, s));
   HSL_CHECK(bias_grads_from_parts(w.db_part, B, nullptr, nullptr, nullptr, db_ih, nullptr, nullptr, H, s));
   const int TB = T * B;
   if (D > 0) {
@@ -415,46 +430,48 @@ using namespace hsl;
 
 extern "C" {
 
-int hsl_scan_fwd(const float* gates, const float* c0, float eps, float* out, float* c_seq, int T, int B, int H,
+int hsl_scan_ck_rows(int T) { return T < 0 ? 0 : (T + kCkSteps - 1) / kCkSteps + 1; }
+
+int hsl_scan_fwd(const float* gates, const float* c0, float eps, float* out, float* c_ck, int T, int B, int H,
                  void* stream) {
   HSL_CHECK(check_scan_dims(T, B, H));
-  if (T > 0 && B > 0 && H > 0 && (!gates || !out || !c_seq)) return fail(HSL_ERR_ARG, "hsl_scan_fwd: null pointer");
-  return scan_fwd(gates, c0, eps, out, c_seq, T, B, H, static_cast<hipStream_t>(stream));
+  if (T > 0 && B > 0 && H > 0 && (!gates || !out || !c_ck)) return fail(HSL_ERR_ARG, "hsl_scan_fwd: null pointer");
+  return scan_fwd(gates, c0, eps, out, c_ck, T, B, H, static_cast<hipStream_t>(stream));
 }
 
-int hsl_scan_bwd(const float* gates, const float* c0, const float* c_seq, const float* dout, const float* dh_n,
+int hsl_scan_bwd(const float* gates, const float* c0, const float* c_ck, const float* dout, const float* dh_n,
                  const float* dc_n, float eps, float* dgates, double* db_part, float* dc0, int T, int B, int H,
                  void* stream) {
   HSL_CHECK(check_scan_dims(T, B, H));
-  if (B > 0 && H > 0 && T > 0 && (!gates || !c_seq || !dout || !dgates))
+  if (B > 0 && H > 0 && T > 0 && (!gates || !c_ck || !dout || !dgates))
     return fail(HSL_ERR_ARG, "hsl_scan_bwd: null pointer");
-  return scan_bwd(gates, c0, c_seq, dout, dh_n, dc_n, eps, dgates, db_part, dc0, T, B, H,
+  return scan_bwd(gates, c0, c_ck, dout, dh_n, dc_n, eps, dgates, db_part, dc0, T, B, H,
                   static_cast<hipStream_t>(stream));
 }
 
 int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float* b_ih, float eps, float* gates,
-                float* out, float* c_seq, int T, int B, int D, int H, void* stream) {
+                float* out, float* c_ck, int T, int B, int D, int H, void* stream) {
   HSL_CHECK(check_scan_dims(T, B, H, D));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (T == 0 || B == 0 || H == 0) return HSL_OK;
-  if (!x || !w_ih || !b_ih || !gates || !out || !c_seq) return fail(HSL_ERR_ARG, "hsl_par_fwd: null pointer");
+  if (!x || !w_ih || !b_ih || !gates || !out || !c_ck) return fail(HSL_ERR_ARG, "hsl_par_fwd: null pointer");
   GemmDesc g1{x, w_ih, b_ih, gates, T * B, 4 * H, D, D, D, 4 * H, 0, 1, 0};
   const int slot = timing_begin(kTimeInputProj, s);
   HSL_CHECK(gemm_run(g1, nullptr, 0, s));
   timing_end(slot, s);
-  return scan_fwd(gates, c0, eps, out, c_seq, T, B, H, s);
+  return scan_fwd(gates, c0, eps, out, c_ck, T, B, H, s);
 }
 
 int hsl_par_fwd_b16(const void* x, const float* c0, const void* w_ih, const float* b_ih, float eps, float* gates,
-                    float* out, float* c_seq, int T, int B, int D, int H, int fmt, void* stream) {
+                    float* out, float* c_ck, int T, int B, int D, int H, int fmt, void* stream) {
   HSL_CHECK(check_scan_dims(T, B, H, D));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (T == 0 || B == 0 || H == 0) return HSL_OK;
-  if (!x || !w_ih || !b_ih || !gates || !out || !c_seq) return fail(HSL_ERR_ARG, "hsl_par_fwd_b16: null pointer");
+  if (!x || !w_ih || !b_ih || !gates || !out || !c_ck) return fail(HSL_ERR_ARG, "hsl_par_fwd_b16: null pointer");
   const int slot = timing_begin(kTimeInputProj, s);
   HSL_CHECK(gemm_b16_run(x, w_ih, b_ih, gates, T * B, 4 * H, D, D, D, 4 * H, fmt, s));
   timing_end(slot, s);
-  return scan_fwd(gates, c0, eps, out, c_seq, T, B, H, s);
+  return scan_fwd(gates, c0, eps, out, c_ck, T, B, H, s);
 }
 
 size_t hsl_par_bwd_ws_bytes(int T, int B, int D, int H) {
@@ -470,18 +487,18 @@ size_t hsl_par_bwd_b16_ws_bytes(int T, int B, int D, int H) {
 }
 
 int hsl_par_bwd(const float* dout, const float* dh_n, const float* dc_n, const float* x, const float* c0,
-                const float* gates, const float* c_seq, const float* w_ih, float eps, float* dx, float* dw_ih,
+                const float* gates, const float* c_ck, const float* w_ih, float eps, float* dx, float* dw_ih,
                 float* db_ih, float* dc0, void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream) {
-  return par_bwd_impl(dout, dh_n, dc_n, x, c0, gates, c_seq, w_ih, eps, dx, dw_ih, db_ih, dc0, ws, ws_bytes, T, B, D,
+  return par_bwd_impl(dout, dh_n, dc_n, x, c0, gates, c_ck, w_ih, eps, dx, dw_ih, db_ih, dc0, ws, ws_bytes, T, B, D,
                       H, -1, static_cast<hipStream_t>(stream));
 }
 
 int hsl_par_bwd_b16(const float* dout, const float* dh_n, const float* dc_n, const void* x, const float* c0,
-                    const float* gates, const float* c_seq, const void* w_ih, float eps, float* dx, float* dw_ih,
+                    const float* gates, const float* c_ck, const void* w_ih, float eps, float* dx, float* dw_ih,
                     float* db_ih, float* dc0, void* ws, size_t ws_bytes, int T, int B, int D, int H, int fmt,
                     void* stream) {
   if (fmt != 0 && fmt != 1) return fail(HSL_ERR_ARG, "hsl_par_bwd_b16: format must be 0 (bf16) or 1 (fp16)");
-  return par_bwd_impl(dout, dh_n, dc_n, x, c0, gates, c_seq, w_ih, eps, dx, dw_ih, db_ih, dc0, ws, ws_bytes, T, B, D,
+  return par_bwd_impl(dout, dh_n, dc_n, x, c0, gates, c_ck, w_ih, eps, dx, dw_ih, db_ih, dc0, ws, ws_bytes, T, B, D,
                       H, fmt, static_cast<hipStream_t>(stream));
 }
 

@@ -150,20 +150,20 @@ class ParallelFn(torch.autograd.Function):
         ctx.set_materialize_grads(False)
         gates = x.new_empty(T, B, 4 * H)
         out = x.new_empty(T, B, H)
-        c_seq = x.new_empty(T, B, H)
+        c_ck = x.new_empty(_lib.load().hsl_scan_ck_rows(T), B, H)
         P = _lib.ptr
         _lib.call("hsl_par_fwd", P(x), P(c0), P(w_ih), P(b_ih), float(eps), P(gates), P(out),
-                  P(c_seq), T, B, D, H, _lib.stream_of(x.device))
-        ctx.save_for_backward(x, c0, w_ih, gates, c_seq)
+                  P(c_ck), T, B, D, H, _lib.stream_of(x.device))
+        ctx.save_for_backward(x, c0, w_ih, gates, c_ck)
         ctx.dims = (T, B, D, H)
         ctx.eps = float(eps)
-        return out, out[T - 1], c_seq[T - 1]
+        return out, out[T - 1], c_ck[-1]
 
     @staticmethod
     def backward(ctx, dout, dh_n, dc_n):
-        x, c0, w_ih, gates, c_seq = ctx.saved_tensors
+        x, c0, w_ih, gates, c_ck = ctx.saved_tensors
         T, B, D, H = ctx.dims
-        dout = _grad_or_zeros(dout, c_seq)
+        dout = _c(dout) if dout is not None else x.new_zeros(T, B, H)
         dh_n, dc_n = _c(dh_n), _c(dc_n)
         need = ctx.needs_input_grad
         dx = torch.empty_like(x) if need[0] else None
@@ -174,7 +174,7 @@ class ParallelFn(torch.autograd.Function):
         nbytes = lib.hsl_par_bwd_ws_bytes(T, B, D, H)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
         P = _lib.ptr
-        _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(x), P(c0), P(gates), P(c_seq),
+        _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(x), P(c0), P(gates), P(c_ck),
                   P(w_ih), ctx.eps, P(dx), P(dw_ih), P(db_ih), P(dc0), P(ws), nbytes, T, B, D, H,
                   _lib.stream_of(x.device))
         return dx, None, dc0, dw_ih, None, db_ih, None, None, None
@@ -208,21 +208,21 @@ class ParallelHalfFn(torch.autograd.Function):
         ctx.set_materialize_grads(False)
         gates = x.new_empty(T, B, 4 * H, dtype=torch.float32)
         out = x.new_empty(T, B, H, dtype=torch.float32)
-        c_seq = x.new_empty(T, B, H, dtype=torch.float32)
+        c_ck = x.new_empty(_lib.load().hsl_scan_ck_rows(T), B, H, dtype=torch.float32)
         fmt = 0 if x.dtype == torch.bfloat16 else 1
         P = _lib.ptr
         _lib.call("hsl_par_fwd_b16", P(x), P(c0), P(w_ih), P(b_ih), float(eps), P(gates), P(out),
-                  P(c_seq), T, B, D, H, fmt, _lib.stream_of(x.device))
-        ctx.save_for_backward(x, c0, w_ih, gates, c_seq)
+                  P(c_ck), T, B, D, H, fmt, _lib.stream_of(x.device))
+        ctx.save_for_backward(x, c0, w_ih, gates, c_ck)
         ctx.dims = (T, B, D, H)
         ctx.eps = float(eps)
-        return out, out[T - 1], c_seq[T - 1]
+        return out, out[T - 1], c_ck[-1]
 
     @staticmethod
     def backward(ctx, dout, dh_n, dc_n):
-        x, c0, w_ih, gates, c_seq = ctx.saved_tensors
+        x, c0, w_ih, gates, c_ck = ctx.saved_tensors
         T, B, D, H = ctx.dims
-        dout = _grad_or_zeros(dout, c_seq)
+        dout = _c(dout) if dout is not None else c_ck.new_zeros(T, B, H)
         dh_n, dc_n = _c(dh_n), _c(dc_n)
         need = ctx.needs_input_grad
         f32 = dict(device=x.device, dtype=torch.float32)
@@ -235,7 +235,7 @@ class ParallelHalfFn(torch.autograd.Function):
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
         P = _lib.ptr
         fmt = 0 if x.dtype == torch.bfloat16 else 1
-        _lib.call("hsl_par_bwd_b16", P(dout), P(dh_n), P(dc_n), P(x), P(c0), P(gates), P(c_seq),
+        _lib.call("hsl_par_bwd_b16", P(dout), P(dh_n), P(dc_n), P(x), P(c0), P(gates), P(c_ck),
                   P(w_ih), ctx.eps, P(dx), P(dw_ih), P(db_ih), P(dc0), P(ws), nbytes, T, B, D, H, fmt,
                   _lib.stream_of(x.device))
         # autograd casts each gradient to its input's dtype (x and W_ih: 16-bit)

@@ -168,8 +168,8 @@ def test_parallel_backward_16bit_operands_equal_widened(dev, fmt, T, B, D, H):
     c0 = (torch.randn(B, H, generator=g) * 0.5).to(dev)
     gates = torch.empty(T, B, 4 * H, device=dev)
     out = torch.empty(T, B, H, device=dev)
-    c_seq = torch.empty(T, B, H, device=dev)
-    _lib.call("hsl_par_fwd_b16", P(x16), P(c0), P(w16), P(b_ih), 1e-6, P(gates), P(out), P(c_seq),
+    c_ck = torch.empty(_lib.load().hsl_scan_ck_rows(T), B, H, device=dev)
+    _lib.call("hsl_par_fwd_b16", P(x16), P(c0), P(w16), P(b_ih), 1e-6, P(gates), P(out), P(c_ck),
               T, B, D, H, fmt, s)
     dout = torch.randn(T, B, H, generator=g).to(dev)
     dh_n = torch.randn(B, H, generator=g).to(dev)
@@ -184,12 +184,12 @@ def test_parallel_backward_16bit_operands_equal_widened(dev, fmt, T, B, D, H):
             xw, ww = x16.float(), w16.float()
             n = _lib.load().hsl_par_bwd_ws_bytes(T, B, D, H)
             ws = torch.empty(n, dtype=torch.uint8, device=dev)
-            _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(xw), P(c0), P(gates), P(c_seq), P(ww), 1e-6,
+            _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(xw), P(c0), P(gates), P(c_ck), P(ww), 1e-6,
                       P(dx), P(dw), P(db), P(dc0), P(ws), n, T, B, D, H, s)
         else:
             n = _lib.load().hsl_par_bwd_b16_ws_bytes(T, B, D, H)
             ws = torch.empty(n, dtype=torch.uint8, device=dev)
-            _lib.call("hsl_par_bwd_b16", P(dout), P(dh_n), P(dc_n), P(x16), P(c0), P(gates), P(c_seq), P(w16),
+            _lib.call("hsl_par_bwd_b16", P(dout), P(dh_n), P(dc_n), P(x16), P(c0), P(gates), P(c_ck), P(w16),
                       1e-6, P(dx), P(dw), P(db), P(dc0), P(ws), n, T, B, D, H, fmt, s)
         torch.cuda.synchronize()
         res.append((dx.clone(), dw.clone(), db.clone(), dc0.clone()))

@@ -137,11 +137,59 @@ def _par_fwd(x, c0, w_ih, b_ih, T, B, D, H):
     dev = x.device
     gates = torch.empty(T, B, 4 * H, device=dev)
     out = torch.empty(T, B, H, device=dev)
-    c_seq = torch.empty(T, B, H, device=dev)
+    c_ck = torch.empty(_lib.load().hsl_scan_ck_rows(T), B, H, device=dev)
     P = _lib.ptr
-    _lib.call("hsl_par_fwd", P(x), P(c0), P(w_ih), P(b_ih), 1e-6, P(gates), P(out), P(c_seq),
+    _lib.call("hsl_par_fwd", P(x), P(c0), P(w_ih), P(b_ih), 1e-6, P(gates), P(out), P(c_ck),
               T, B, D, H, _lib.stream_of(dev))
-    return gates, out, c_seq
+    return gates, out, c_ck
+
+
+def _ck_ref(c_ref, c0c, T):
+    """The checkpoint rows hsl_par_fwd writes, from a reference c [ch, T]: the state carried
+    into steps 0, 8, 16, ... (max(c0, eps) first), then c_{T-1}."""
+    return torch.cat([c0c.view(-1, 1), c_ref[:, 7:T - 1:8], c_ref[:, T - 1:]], dim=1)
+
+
+@pytest.mark.parametrize("T", [1, 7, 8, 9, 63, 64, 65, 127, 128, 129, 300])
+def test_checkpoint_rows(dev, T):
+    """hsl_scan_fwd keeps c at every 8th step only (the backward re-runs the steps in
+    between): the rows against the fp64 reference formula (_parallel.py:21-35) on the
+    GPU's gates, and the backward's dgates for the loss out . dout + c_n . dc_n against
+    fp64 autograd of it, at lengths around the 8-step groups and the scans' chunks (128
+    steps forward, 64 backward).  c0 has entries below eps (clamped rows)."""
+    B, H = 3, 50
+    n = B * H
+    g = torch.Generator().manual_seed(T)
+    gates = (2.0 * torch.randn(T, B, 4 * H, generator=g)).to(dev)
+    c0 = torch.rand(B, H, generator=g)
+    c0[0, :7] = 0.0
+    c0d = c0.to(dev)
+    rows = _lib.load().hsl_scan_ck_rows(T)
+    assert rows == (T + 7) // 8 + 1
+    out = torch.empty(T, B, H, device=dev)
+    c_ck = torch.full((rows, B, H), float("nan"), device=dev)
+    P, s = _lib.ptr, _lib.stream_of(dev)
+    _lib.call("hsl_scan_fwd", P(gates), P(c0d), 1e-6, P(out), P(c_ck), T, B, H, s)
+    dout = torch.randn(T, B, H, generator=g)
+    dc_n = torch.randn(B, H, generator=g)
+    dout_d, dc_d = dout.to(dev), dc_n.to(dev)
+    dgates = torch.empty(T, B, 4 * H, device=dev)
+    _lib.call("hsl_scan_bwd", P(gates), P(c0d), P(c_ck), P(dout_d), None, P(dc_d), 1e-6,
+              P(dgates), None, None, T, B, H, s)
+    torch.cuda.synchronize()
+    gsub = gates.view(T, B, 4, H).permute(1, 3, 0, 2).reshape(n, T, 4).cpu().double().requires_grad_(True)
+    i, f, gg, o = (torch.sigmoid(gsub[..., k]) for k in range(4))
+    c_ref = O.heinsen_scan(f.unsqueeze(-1), c0.reshape(n, 1, 1).double(), (i * gg).unsqueeze(-1))[..., 0]
+    c0c = c0.reshape(n, 1).double().clamp_min(1e-6)
+    out_ref = o * torch.tanh(c_ref)
+    ck = c_ck.permute(1, 2, 0).reshape(n, rows).cpu()
+    assert lim_ratio(ck, _ck_ref(c_ref, c0c, T), RTOL, ATOL) <= 1.0
+    assert lim_ratio(out.permute(1, 2, 0).reshape(n, T).cpu(), out_ref, RTOL, ATOL) <= 1.0
+    loss = (out_ref * dout.permute(1, 2, 0).reshape(n, T).double()).sum() \
+        + (c_ref[:, -1] * dc_n.reshape(n).double()).sum()
+    loss.backward()
+    dgv = dgates.view(T, B, 4, H).permute(1, 3, 0, 2).reshape(n, T, 4).cpu()
+    assert lim_ratio(dgv, gsub.grad, RTOL, ATOL) <= 1.0
 
 
 def test_config4_full_size_all_channels(dev):
@@ -158,7 +206,7 @@ def test_config4_full_size_all_channels(dev):
     c0 = torch.zeros(B, H, device=dev)
     w_ih = ref.weight_ih_l0.detach().to(dev)
     b_ih = ref.bias_ih_l0.detach().to(dev)
-    gates, out, c_seq = _par_fwd(xd, c0, w_ih, b_ih, T, B, D, H)
+    gates, out, c_ck = _par_fwd(xd, c0, w_ih, b_ih, T, B, D, H)
     g = torch.Generator().manual_seed(1)
     # input projection: random (t, b) rows, all 4H columns, vs fp64
     rows = torch.randint(0, T * B, (256,), generator=g)
@@ -177,14 +225,15 @@ def test_config4_full_size_all_channels(dev):
     # keep device copies referenced until the kernel has run (a temporary's memory
     # could be handed to the next allocation before the enqueued kernel reads it)
     dout_d, dh_d, dc_d = dout.to(dev), dh_n.to(dev), dc_n.to(dev)
-    _lib.call("hsl_scan_bwd", P(gates), P(c0), P(c_seq), P(dout_d), P(dh_d), P(dc_d), 1e-6,
+    _lib.call("hsl_scan_bwd", P(gates), P(c0), P(c_ck), P(dout_d), P(dh_d), P(dc_d), 1e-6,
               P(dgates), P(db_part), P(dc0), T, B, H, _lib.stream_of(dev))
     torch.cuda.synchronize()
-    # channel-major copies: [B*H, T, 4] gates and gradients, [B*H, T] states
+    # channel-major copies: [B*H, T, 4] gates and gradients, [B*H, T] outputs, [B*H, rows]
+    # checkpoint states
     n = B * H
     gv = gates.view(T, B, 4, H).permute(1, 3, 0, 2).reshape(n, T, 4).cpu()
     dgv = dgates.view(T, B, 4, H).permute(1, 3, 0, 2).reshape(n, T, 4).cpu()
-    cv = c_seq.permute(1, 2, 0).reshape(n, T).cpu()
+    cv = c_ck.permute(1, 2, 0).reshape(n, c_ck.shape[0]).cpu()
     ov = out.permute(1, 2, 0).reshape(n, T).cpu()
     dv = dout.permute(1, 2, 0).reshape(n, T)
     dbp = db_part.cpu().view(B, 4, H).permute(0, 2, 1).reshape(n, 4)
@@ -198,7 +247,8 @@ def test_config4_full_size_all_channels(dev):
         c0_sub = torch.zeros(gsub.shape[0], 1, 1, dtype=torch.float64)
         c_ref = O.heinsen_scan(f.unsqueeze(-1), c0_sub, (i * gg).unsqueeze(-1))[..., 0]  # [ch, T]
         out_ref = o * torch.tanh(c_ref)
-        worst["c"] = max(worst["c"], lim_ratio(cv[sl], c_ref, RTOL, ATOL))
+        c0c = torch.full((c_ref.shape[0], 1), 1e-6, dtype=torch.float64)  # max(c0 = 0, eps)
+        worst["c"] = max(worst["c"], lim_ratio(cv[sl], _ck_ref(c_ref, c0c, T), RTOL, ATOL))
         worst["out"] = max(worst["out"], lim_ratio(ov[sl], out_ref, RTOL, ATOL))
         loss = (out_ref * dv[sl].double()).sum() + (out_ref[:, -1] * dhv[sl].double()).sum() \
             + (c_ref[:, -1] * dcv[sl].double()).sum()
@@ -242,7 +292,7 @@ def test_config4_weight_gradient_full_size(dev):
     c0 = torch.zeros(B, H, device=dev)
     w_ih = ref.weight_ih_l0.detach().to(dev)
     b_ih = ref.bias_ih_l0.detach().to(dev)
-    gates, out, c_seq = _par_fwd(xd, c0, w_ih, b_ih, T, B, D, H)
+    gates, out, c_ck = _par_fwd(xd, c0, w_ih, b_ih, T, B, D, H)
     g = torch.Generator().manual_seed(2)
     dout = torch.randn(T, B, H, generator=g).to(dev)
     dh_n = torch.zeros(B, H, device=dev)
@@ -250,14 +300,14 @@ def test_config4_weight_gradient_full_size(dev):
     P, s = _lib.ptr, _lib.stream_of(dev)
     dgates = torch.empty(T, B, 4 * H, device=dev)
     db_part = torch.empty(B, 4 * H, dtype=torch.float64, device=dev)
-    _lib.call("hsl_scan_bwd", P(gates), P(c0), P(c_seq), P(dout), P(dh_n), P(dc_n), 1e-6,
+    _lib.call("hsl_scan_bwd", P(gates), P(c0), P(c_ck), P(dout), P(dh_n), P(dc_n), 1e-6,
               P(dgates), P(db_part), None, T, B, H, s)
     nbytes = _lib.load().hsl_par_bwd_ws_bytes(T, B, D, H)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     dw = torch.empty(4 * H, D, device=dev)
     db = torch.empty(4 * H, device=dev)
     dx = torch.empty(T, B, D, device=dev)
-    _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(xd), P(c0), P(gates), P(c_seq), P(w_ih), 1e-6,
+    _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(xd), P(c0), P(gates), P(c_ck), P(w_ih), 1e-6,
               P(dx), P(dw), P(db), None, P(ws), nbytes, T, B, D, H, s)
     torch.cuda.synchronize()
     rows = torch.arange(0, 4 * H, 29)

@@ -81,6 +81,14 @@ struct X6Args {
   int partial;
   int tiles_m, tiles_n;
   int out_vec;  // output base and row stride 16-byte aligned (and the bias, if any)
+  // Weight-gradient finalisation in the epilogue (direct output, staged path only): with
+  // dotw != null, every row of C is scaled by rs[row / rs_rows] (a tile's rows share one
+  // group) and each wave adds up dotw . C (unscaled, fp64) over its part of the tile into
+  // dotp[(tile_m * tiles_n + tile_n) * 8 + wave].
+  const float* rs;
+  int rs_rows;
+  const float* dotw;
+  double* dotp;
 };
 
 
@@ -441,8 +449,20 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
       const int rl = lane >> 4, cl = 4 * (lane & 15);
       const int nb = n0 + wn * S::TN + cl;
       const f4 bv = (!g.partial && g.bias) ? *reinterpret_cast<const f4*>(g.bias + nb) : f4{0.f, 0.f, 0.f, 0.f};
+      const bool fin = g.dotw != nullptr;  // uniform
+      const float sc = fin ? g.rs[m0 / g.rs_rows] : 1.f;
+      double dacc = 0.0;
 #pragma unroll
       for (int i = 0; i < S::FM; ++i) {
+        // the dot operand's rows of this slab, requested before the slab goes through LDS
+        f4 wv[8];
+        if (fin) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const int m = m0 + wm * S::TM + i * 32 + 4 * q + rl;
+            wv[q] = *reinterpret_cast<const f4*>(g.dotw + (size_t)m * ldo + nb);
+          }
+        }
 #pragma unroll
         for (int j = 0; j < S::FN; ++j) {
           const f16v& res = S::FOLD ? tot[S::FOLD ? i : 0][S::FOLD ? j : 0] : acc[i][j];
@@ -452,10 +472,20 @@ __device__ __forceinline__ void x6_tile(const X6Args& g, int m0, int n0, unsigne
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           const int row = 4 * q + rl;
-          const f4 v = *reinterpret_cast<const f4*>(&slab[row * kLds + cl]) + bv;
+          f4 v = *reinterpret_cast<const f4*>(&slab[row * kLds + cl]) + bv;
+          if (fin) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dacc += (double)wv[q][e] * (double)v[e];
+            v = v * sc;
+          }
           const int m = m0 + wm * S::TM + i * 32 + row;
           __builtin_nontemporal_store(v, reinterpret_cast<f4*>(outp + (size_t)m * ldo + nb));
         }
+      }
+      if (fin) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) dacc += __shfl_xor(dacc, off);
+        if (lane == 0) g.dotp[((size_t)(m0 / S::BM) * g.tiles_n + n0 / S::BN) * 8 + wave] = dacc;
       }
       return;
     }
@@ -540,6 +570,39 @@ int gemm_x6_longk_splits(int M, int N, int K) {
   if (s > K / kBK) s = K / kBK;
   if (s > 64) s = 64;
   return s < 1 ? 1 : (int)s;
+}
+
+int gemm_x6_wgrad_fin(const float* A, const float* B, float* C, const float* a_group, int group_rows,
+                      const float* W, double* dotp, size_t dotp_cap, int M, int N, int K, int lda, int ldb, int ldc,
+                      hipStream_t s, int* parts) {
+  // A^T B on one split of whole 256 x 128 tiles, aligned rows, tiles within one row group
+  using S = ShapeWgrad;
+  *parts = 0;
+  if (!split_products_mode() || gemm_x6_longk_splits(M, N, K) != 1) return HSL_OK;
+  if (M % S::BM || N % S::BN || K % kBK || group_rows <= 0 || group_rows % S::BM) return HSL_OK;
+  if (!aligned16(A) || !aligned16(B) || !aligned16(C) || !aligned16(W) || lda % 4 || ldb % 4 || ldc % 4) return HSL_OK;
+  const size_t n = (size_t)(M / S::BM) * (N / S::BN) * 8;
+  if (!dotp || n > dotp_cap) return HSL_OK;
+  X6Args g{};
+  g.A = A;
+  g.B = B;
+  g.out = C;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.lda = lda;
+  g.ldb = ldb;
+  g.ldc = ldc;
+  g.kps = K;
+  g.out_vec = 1;
+  g.rs = a_group;
+  g.rs_rows = group_rows;
+  g.dotw = W;
+  g.dotp = dotp;
+  x6_launch<S, false, false>(g, true, 1, s);
+  HSL_HIP(hipGetLastError());
+  *parts = (int)(n / (M / group_rows));
+  return HSL_OK;
 }
 
 int gemm_x6_run(const float* A, const void* B, const float* bias, float* C, float* partial, int M, int N, int K,

@@ -119,14 +119,22 @@ int gemm_x6_longk_splits(int M, int N, int K);  // C = A^T B or A B: split count
 int gemm_x6_run(const float* A, const void* B, const float* bias, float* C, float* partial, int M, int N, int K,
                 int lda, int ldb, int ldc, int trans_a, int trans_b, int splits, hipStream_t s, int* used,
                 int b_bf16 = 0);
+// dW = A^T B written with its finalisation (one split of the split-bf16 kernel): row r of
+// C = a_group[r / group_rows] * (A^T B)[r], and per group the fp64 sum of W . (A^T B) in
+// parts[group][*parts] of dotp.  *parts = 0: the shape does not qualify and nothing ran.
+int gemm_x6_wgrad_fin(const float* A, const float* B, float* C, const float* a_group, int group_rows,
+                      const float* W, double* dotp, size_t dotp_cap, int M, int N, int K, int lda, int ldb, int ldc,
+                      hipStream_t s, int* parts);
 int gemm_b16_run(const void* A, const void* B, const float* bias, float* C, int M, int N, int K, int lda, int ldb,
                  int ldc, int fmt, hipStream_t s);
 
 // ---- shared finalisation (recurrent.hip) ------------------------------------------
 // db = sum_b db_part[b][:] ; db_ih = db ; db_hh = a_g db ; da[g] = sum_{n in g} rowdot[n] + b_hh[n] db[n].
 // Any of rowdot, b_hh, a, db_hh, da may be null (parallel mode only wants db_ih).
+// rowdot [4H] (or dotp [4][dot_parts], from gemm_x6_wgrad_fin): the fp64 sums of W_hh . dW_hh_s
 int bias_grads_from_parts(const double* db_part, int B, const double* rowdot, const float* b_hh, const float* a,
-                          float* db_ih, float* db_hh, float* da, int H, hipStream_t s);
+                          float* db_ih, float* db_hh, float* da, int H, hipStream_t s, const double* dotp = nullptr,
+                          int dot_parts = 0);
 int zero_words(unsigned long long* p, size_t n, hipStream_t s);
 int copy_f32(float* dst, const float* src, size_t n, hipStream_t s);
 

@@ -222,7 +222,8 @@ __global__ __launch_bounds__(1024) void bias_da_finalize_kernel(const double* __
                                                                 const double* __restrict__ rowdot,
                                                                 const float* __restrict__ b_hh,
                                                                 const float* __restrict__ a, float* __restrict__ db_ih,
-                                                                float* __restrict__ db_hh, float* __restrict__ da, int H) {
+                                                                float* __restrict__ db_hh, float* __restrict__ da, int H,
+                                                                const double* __restrict__ dotp, int dot_parts) {
   __shared__ double red[1024];
   const int g = blockIdx.x;
   const float ag = a ? a[g] : 1.0f;
@@ -242,6 +243,8 @@ __global__ __launch_bounds__(1024) void bias_da_finalize_kernel(const double* __
     if (db_hh) db_hh[n] = ag * db;
     acc += (rowdot ? rowdot[n] : 0.0) + (b_hh ? (double)b_hh[n] * (double)db : 0.0);
   }
+  if (dotp)
+    for (int i = threadIdx.x; i < dot_parts; i += blockDim.x) acc += dotp[(size_t)g * dot_parts + i];
   red[threadIdx.x] = acc;
   __syncthreads();
   for (int w = blockDim.x / 2; w > 0; w >>= 1) {
@@ -2430,10 +2433,11 @@ int zero_words(unsigned long long* p, size_t n, hipStream_t s) { return fill_wor
 int copy_f32(float* dst, const float* src, size_t n, hipStream_t s) { return copy_f32_impl(dst, src, n, s); }
 
 int bias_grads_from_parts(const double* db_part, int B, const double* rowdot, const float* b_hh, const float* a,
-                          float* db_ih, float* db_hh, float* da, int H, hipStream_t s) {
+                          float* db_ih, float* db_hh, float* da, int H, hipStream_t s, const double* dotp,
+                          int dot_parts) {
   if (H == 0) return HSL_OK;
   hipLaunchKernelGGL(bias_da_finalize_kernel, dim3(4), dim3(1024), 0, s, db_part, B, rowdot, b_hh, a, db_ih, db_hh,
-                     da, H);
+                     da, H, dotp, dot_parts);
   HSL_HIP(hipGetLastError());
   return HSL_OK;
 }
@@ -2784,16 +2788,20 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     note_recurrent_path(1);
   }
 
-  // dW_hh_s = dg^T h_prev (staged partials), then dW_hh = a dW_hh_s and the da row sums
-  int splits = nsplit;
-  if (!fused) {
+  // dW_hh_s = dg^T h_prev (staged partials), then dW_hh = a dW_hh_s and the da row sums.
+  // A one-split product does the second part in its own epilogue (dot_parts > 0).
+  int splits = nsplit, dot_parts = 0;
+  if (!fused)
+    HSL_CHECK(gemm_x6_wgrad_fin(w.dgates, h_save, dw_hh, a, H, w_hh, w.rowdot, (size_t)4 * H, 4 * H, H, TB, 4 * H, H,
+                                H, s, &dot_parts));
+  if (!fused && !dot_parts) {
     GemmDesc g4{w.dgates, h_save, nullptr, w.gemm, 4 * H, H, TB, 4 * H, H, H, 1, 0, 1};
     // as many planes as asked for and as the region holds (the mode may have changed
     // since the workspace was sized)
     const int fit = (int)std::min<size_t>(w.gemm_bytes / (sizeof(float) * (size_t)4 * H * H), 1 << 20);
     HSL_CHECK(gemm_partials(g4, w.gemm, std::max(1, std::min(gemm_tn_planes(4 * H, H, TB), fit)), s, &splits));
   }
-  {  // dW_hh (and the fused dW_ih planes in extra blocks of the same launch)
+  if (!dot_parts) {  // dW_hh (and the fused dW_ih planes in extra blocks of the same launch)
     const size_t xn = fused_ih ? (size_t)4 * H * D : 0;
     auto al16 = [](const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
     const bool vec = H % 4 == 0 && al16(wph) && al16(w_hh) && al16(dw_hh) &&
@@ -2811,7 +2819,8 @@ int hsl_rec_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
     }
     HSL_HIP(hipGetLastError());
   }
-  HSL_CHECK(bias_grads_from_parts(w.db_part, B, w.rowdot, b_hh, a, db_ih, db_hh, da, H, s));
+  HSL_CHECK(bias_grads_from_parts(w.db_part, B, dot_parts ? nullptr : w.rowdot, b_hh, a, db_ih, db_hh, da, H, s,
+                                  dot_parts ? w.rowdot : nullptr, dot_parts));
   // dW_ih = dg^T x ; dx = dg W_ih
   if (D > 0) {
     if (!fused_ih) {

@@ -32,17 +32,19 @@
 // in steps 4 and 8 are requested before the sends of steps 3 and 7.
 //
 // Wave w holds the rows of units [U w / 4, +U/4) (U/16 row tiles of 16) for all 4U k of the
-// workgroup (U k-steps of 4): U^2/16 values per lane in the accumulator registers.
-//   A operand (W): lane l of k-step i, tile rt: row 16 rt + l%16 of the wave (unit
-//     4 rt + (l%16)/4, gate l%4), k = 4U kb + 4 i + l/16.
-//   B operand (h): lane l of k-step i: h[batch 16c + l%16][k = 4U kb + 4 i + l/16].
+// workgroup (U k-steps of 4): U^2/16 values per lane in the accumulator registers.  Inside
+// each quad j of four k-steps (16 k), lane l's k-step e takes k = 16 j + 4 (l/16) + e, so a
+// lane's four values of a quad are four consecutive k (one 16-byte load of W per row tile).
+//   A operand (W): lane l of k-step 4j + e, tile rt: row 16 rt + l%16 of the wave (unit
+//     4 rt + (l%16)/4, gate l%4), k = 4U kb + 16 j + 4 (l/16) + e.
+//   B operand (h): lane l of k-step 4j + e: h[batch 16c + l%16][k = 4U kb + 16 j + 4 (l/16) + e].
 //   D: lane l, register g: gate g of unit 4 rt + l/16, batch row l%16 of the chain.
-// LDS holds one buffer per chain: quad j (k-steps 4j .. 4j+3) of lane l at [j][l].  An h
-// block (16 batch rows x U units of a row group, one chain) has the same layout over its
-// U/4 k-steps: k-step i of lane l is word 256 (i/4) + 4 l + i%4, with l = 16 (unit % 4) +
-// batch row; wave w receives block (kb, w), LDS quads [w U/16, +U/16).  Row-group member kb
-// publishes its slice of U/8 units: words 256 (kb WPL / 4) + (kb WPL) % 4 + 4 l .. +WPL of
-// each lane position l (WPL = U/32).
+// LDS holds one buffer per chain: quad j of lane l at [j][l].  An h block (16 batch rows x U
+// units of a row group, one chain) has the same layout: unit u (of the block) of batch row n
+// is word 256 (u/16) + 4 l + u%4 with l = 16 ((u%16)/4) + n; wave w receives block (kb, w),
+// LDS quads [w U/16, +U/16).  Row-group member kb publishes its slice of U/8 units
+// (u0 = U kb / 8 onwards) as whole quads: lanes l < U/2 write words 256 (u0/16) +
+// 64 ((u0%16)/4) + 4 l .. +3.
 // Slots per chain: h_t in slot t%4, the owner clears (t+2)%4 after publishing; partials of
 // step t in slot t%3, cleared by their one reader.  The cell lanes' h values are gathered in
 // LDS and published by one wave in whole cache lines (scattered 4-byte device-scope stores
@@ -56,7 +58,6 @@ struct WideFShape {
   static constexpr int SU = U / 8;         // units per slice
   static constexpr int CELLS = SU * 16;    // cells per chain and workgroup
   static constexpr int CPW = CELLS / 4;    // cells per wave (lanes 0 .. CPW-1)
-  static constexpr int WPL = SU / 4;       // published words per lane position
   static constexpr int HB = 256 * BQ;      // words of one h block
   static constexpr int PS = SU * 16 * 4;   // words of one source's partial slice
   static constexpr int IW = 8 * PS;        // inbox words per chain and workgroup
@@ -97,23 +98,35 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
   const int ubase = 4 * U * x + U * r;  // first unit of the workgroup's rows
   const int kbase = 4 * U * kb;         // first k (unit) of the workgroup's k block
   // W block: quad j, k-step e, tile rt -> row (gate l%4, unit ubase + U w/4 + 4 rt + (l%16)/4),
-  // k = kbase + 4 (4 j + e) + l/16; unscaled (a scales the summed product in the cell)
+  // k = kbase + 16 j + 4 (l/16) + e; unscaled (a scales the summed product in the cell).  A
+  // lane's quad is 16 consecutive bytes of its row: one load of four rows' 64-byte segments
+  // per 16 lanes (4-byte loads of k-steps 4 apart touched 16 rows per instruction and took
+  // the first step 31 us after launch at configs[3], against 10 us for the backward's slice)
   float wreg[NQ][4][RT];
   {
     const float* rows[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const int u = ubase + U / 4 * w + 4 * rt + (l16 >> 2);
-      rows[rt] = p.w_hh + ((size_t)(l16 & 3) * H + u) * H + kbase + lq;
+      rows[rt] = p.w_hh + ((size_t)(l16 & 3) * H + u) * H + kbase + 4 * lq;
     }
+    const bool w16 = reinterpret_cast<uintptr_t>(p.w_hh) % 16 == 0;  // uniform
 #pragma unroll
     for (int j8 = 0; j8 < NQ; j8 += 4) {
 #pragma unroll
       for (int j = j8; j < j8 + 4; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
+        for (int rt = 0; rt < RT; ++rt) {
+          f4 v;
+          if (w16) {
+            v = *reinterpret_cast<const f4*>(rows[rt] + 16 * j);
+          } else {
 #pragma unroll
-          for (int rt = 0; rt < RT; ++rt) wreg[j][e][rt] = rows[rt][4 * (4 * j + e)];
+            for (int e = 0; e < 4; ++e) v[e] = rows[rt][16 * j + e];
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) wreg[j][e][rt] = v[e];
+        }
 #pragma unroll
       for (int j = j8; j < j8 + 4; ++j)
 #pragma unroll
@@ -155,10 +168,10 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
   auto inbox = [&](int slot, int c, int wg) { return p.inbox + ((size_t)(slot * 2 + c) * kWideWgs + wg) * S::IW; };
   // each chain's published h values, in the order of the group; entries of absent batch
   // rows are never written and publish 0
-  __shared__ float hst[2][128];
+  __shared__ __attribute__((aligned(16))) float hst[2][128];
   if (tid < 128) hst[0][tid] = hst[1][tid] = 0.f;
-  // the published words of this workgroup's slice inside block (x, r)
-  const unsigned pub_off = 256u * (kb * S::WPL / 4) + (kb * S::WPL) % 4;
+  // the published quads of this workgroup's slice inside block (x, r)
+  const unsigned pub_u0 = SU * kb, pub_off = 256u * (pub_u0 / 16) + 64u * ((pub_u0 % 16) / 4);
 
   // h of chain c for the step after `tin` (its values h_tin) into the chain's LDS buffer:
   // wave w takes block (kb, w) and polls until none of its words is kEmpty.  recv_h0 takes
@@ -170,9 +183,9 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
     for (int j = 0; j < BQ; ++j) {
       f4 v = f4{0.f, 0.f, 0.f, 0.f};
       if (h_ok && p.h0) {
-        const float* row = p.h0 + (size_t)(16 * c + l16) * H + kbase + U * w + lq;
+        const float* row = p.h0 + (size_t)(16 * c + l16) * H + kbase + U * w + 4 * lq;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = row[4 * (4 * j + e)];
+        for (int e = 0; e < 4; ++e) v[e] = row[16 * j + e];
       }
       buf[(w * BQ + j) * 64 + lane] = v;
     }
@@ -303,7 +316,7 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
         const float tc = tanh_f(cc);
         const float h = act[3] * tc;
         c_reg[c] = cc;
-        hst[c][S::WPL * (16 * (su & 3) + cn) + (su >> 2)] = canon_nan(h);
+        hst[c][4 * (16 * (su >> 2) + cn) + (su & 3)] = canon_nan(h);
         const size_t e = (size_t)(16 * c + cn) * H + unit;
         __builtin_nontemporal_store(h, p.h_save + (size_t)(t + 1) * plane + e);
         __builtin_nontemporal_store(cc, p.c_save + (size_t)(t + 1) * plane + e);
@@ -319,13 +332,13 @@ __device__ __forceinline__ void rec_fwd_wide_body(const WFwdArgs& p, int x, int 
       const size_t hslot = (size_t)2 * 32 * S::HB;  // words between slots
       const __amdgpu_buffer_rsrc_t hp = wide_rsrc(own + (size_t)(t % kWideHSlots) * hslot, 256);
       const __amdgpu_buffer_rsrc_t hc = wide_rsrc(own + (size_t)((t + 2) % kWideHSlots) * hslot, 256);
-      if constexpr (S::WPL == 2) {
-        pair_store<false>(hp, 4u * lane, u2v{__float_as_uint(hst[c][2 * lane]), __float_as_uint(hst[c][2 * lane + 1])});
-        pair_store<false>(hc, 4u * lane, u2v{kEmpty, kEmpty});
-      } else {
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(hst[c][lane]), hp, (int)(16u * lane), 0, kCpolSc1);
-        __builtin_amdgcn_raw_buffer_store_b32(kEmpty, hc, (int)(16u * lane), 0, kCpolSc1);
-      }
+      // U/2 lanes, one quad each; the other lanes store past the descriptors' end (dropped),
+      // so that no store depends on a lane condition
+      const unsigned lw = lane < 4 * SU ? 4u * lane : 256u;
+      const f4 hv = *reinterpret_cast<const f4*>(&hst[c][4 * min(lane, 4 * SU - 1)]);
+      quad_store<false>(hp, lw, u4v{__float_as_uint(hv[0]), __float_as_uint(hv[1]), __float_as_uint(hv[2]),
+                                    __float_as_uint(hv[3])});
+      quad_store<false>(hc, lw, u4v{kEmpty, kEmpty, kEmpty, kEmpty});
     }
     return true;
   };

@@ -658,6 +658,14 @@ typedef float SaveBuf[2][4][kUnits][8];
 __device__ __forceinline__ SaveBuf* save_buf(XinBuf* xin) {
   return reinterpret_cast<SaveBuf*>(reinterpret_cast<char*>(xin) + sizeof(XinBuf));
 }
+// The recurrent waves' staging blocks for loading the W_hh slice (used before the first
+// step only), after xin and the saves; the forward's dynamic LDS holds all three.
+constexpr size_t kFwdWStageBytes = 4 * 64 * (64 + 4) * sizeof(float);
+constexpr size_t kFwdLdsBytes = sizeof(XinBuf) + sizeof(SaveBuf) + kFwdWStageBytes;
+static_assert(kFwdLdsBytes >= (size_t)kPadLdsBytes && kFwdLdsBytes <= 150 * 1024, "one workgroup per CU, LDS left for the rest");
+__device__ __forceinline__ float* fwd_wstage(XinBuf* xin) {
+  return reinterpret_cast<float*>(reinterpret_cast<char*>(xin) + sizeof(XinBuf) + sizeof(SaveBuf));
+}
 
 // Projection wave w stores the activations of step ts that recurrent wave w staged
 // (batch slot w, the workgroup's 16 units; lanes 0-15).
@@ -709,19 +717,40 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
   const bool row_ok = ru < H;
   float wreg[KQ];
   {
-    // unconditional loads at clamped addresses, so that all of them are in flight at once;
-    // 16-byte loads when the rows allow them (each load touches 64 rows, so a quarter of
-    // the instructions is a quarter of the cache-line requests: the slice loads in about a
-    // quarter of the time)
     const float ag = p.a[rgate];
     const float* wrow = p.w_hh + (size_t)(row_ok ? rgate * H + ru : 0) * H;
     if (H % 4 == 0 && reinterpret_cast<uintptr_t>(p.w_hh) % 16 == 0) {
+      // A lane holds KQ consecutive k of its own row, so loading its registers directly
+      // touches 64 rows per instruction.  Instead the wave loads whole row segments (LPR
+      // lanes x 16 bytes per row, RPI rows per instruction) into its own LDS staging
+      // block and each lane reads its row back: an eighth of the cache-line requests.
+      // At configs[2] the slice is in registers 9.3-9.7 us after launch instead of 11.2
+      // (the rest is the 32 MiB that the eight XCDs' copies of W_hh read).
+      constexpr int KC = KQ < 64 ? KQ : 64;  // k per round
+      constexpr int LPR = KC / 4, RPI = 64 / LPR, PITCH = KC + 4;
+      float* const stg = fwd_wstage(xin) + q * 64 * PITCH;
+      static_assert(4 * 64 * PITCH * sizeof(float) <= kFwdWStageBytes, "staging fits");
 #pragma unroll
-      for (int m = 0; m < KQ / 4; ++m) {
-        const int k = q * KQ + 4 * m;  // a multiple of 4: k < H implies k + 3 < H
-        const f4 v = *reinterpret_cast<const f4*>(wrow + (k < H ? k : H - 4));
+      for (int r0 = 0; r0 < KQ; r0 += KC) {
+        f4 v[64 / RPI];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) wreg[4 * m + e] = (row_ok && k < H) ? ag * v[e] : 0.f;
+        for (int i = 0; i < 64 / RPI; ++i) {
+          const int sr = RPI * i + lane / LPR;  // staged row = the lane that owns it
+          const int su = wg * kUnits + (sr & 15);
+          const int k = q * KQ + r0 + 4 * (lane % LPR);  // a multiple of 4: k < H implies k + 3 < H
+          const float* const src = p.w_hh + (size_t)(su < H ? (sr >> 4) * H + su : 0) * H;
+          v[i] = *reinterpret_cast<const f4*>(src + (k < H ? k : H - 4));
+        }
+#pragma unroll
+        for (int i = 0; i < 64 / RPI; ++i)
+          *reinterpret_cast<f4*>(stg + (RPI * i + lane / LPR) * PITCH + 4 * (lane % LPR)) = v[i];
+#pragma unroll
+        for (int m = 0; m < KC / 4; ++m) {
+          const f4 w4 = *reinterpret_cast<const f4*>(stg + lane * PITCH + 4 * m);
+          const int k = q * KQ + r0 + 4 * m;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) wreg[r0 + 4 * m + e] = (row_ok && k < H) ? ag * w4[e] : 0.f;
+        }
       }
     } else {
 #pragma unroll
@@ -1093,7 +1122,7 @@ __global__ __launch_bounds__(XP ? 512 : 256, 1) void rec_fwd_persistent(PFwdArgs
   constexpr int HP = 4 * KQ;
   __shared__ f4 red[2][4][64];  // [step parity][batch slot][gate row] -> 4 wave partials
   __shared__ int abort_flag;
-  extern __shared__ char dyn_lds[];  // keeps one workgroup per CU; holds xin when XP
+  extern __shared__ char dyn_lds[];  // keeps one workgroup per CU; xin (XP), the saves, the W_hh staging
   XinBuf* const xin = reinterpret_cast<XinBuf*>(dyn_lds);
   const int grp = blockIdx.x % p.NGX, wg = blockIdx.x / p.NGX;
   if (grp >= p.NG) return;  // unused XCD slot (groups are padded to a multiple of 8)
@@ -2014,7 +2043,7 @@ int pick_kq(int H) {
 template <class K>
 int max_resident(K kernel, int threads, int* out) {
   int occ = 0;
-  HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, kPadLdsBytes));
+  HSL_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, kFwdLdsBytes));
   *out = occ;
   return HSL_OK;
 }
@@ -2398,11 +2427,10 @@ int check_dims(int T, int B, int D, int H) { return check_shape("recurrent mode"
 
 template <int KQ>
 void launch_fwd_persistent(const PFwdArgs& a, int grid, int xp, hipStream_t s) {
-  static_assert(sizeof(XinBuf) + sizeof(SaveBuf) <= (size_t)kPadLdsBytes, "xin and the staged saves live in the padding LDS");
   switch (xp) {
-    case 0: hipLaunchKernelGGL((rec_fwd_persistent<KQ, 0>), dim3(grid), dim3(256), kPadLdsBytes, s, a); break;
-    case 1: hipLaunchKernelGGL((rec_fwd_persistent<KQ, 1>), dim3(grid), dim3(512), kPadLdsBytes, s, a); break;
-    default: hipLaunchKernelGGL((rec_fwd_persistent<KQ, 2>), dim3(grid), dim3(512), kPadLdsBytes, s, a); break;
+    case 0: hipLaunchKernelGGL((rec_fwd_persistent<KQ, 0>), dim3(grid), dim3(256), kFwdLdsBytes, s, a); break;
+    case 1: hipLaunchKernelGGL((rec_fwd_persistent<KQ, 1>), dim3(grid), dim3(512), kFwdLdsBytes, s, a); break;
+    default: hipLaunchKernelGGL((rec_fwd_persistent<KQ, 2>), dim3(grid), dim3(512), kFwdLdsBytes, s, a); break;
   }
 }
 template <int KQ, bool WS>

@@ -55,6 +55,9 @@ def test_workspace_queries():
     assert lib.hsl_rec_fwd_ws_bytes(-1, 1, 1, 1) == 0
     assert lib.hsl_gemm_ws_bytes(2048, 512, 8192) > 0   # split-K for a long reduction
     assert lib.hsl_gemm_ws_bytes(8192, 2048, 256) == 0  # enough tiles: no split
+    # parallel mode keeps c every 8th step: ceil(T/8) carry-in rows, then c_n
+    for T, rows in ((1, 2), (7, 2), (8, 2), (9, 3), (128, 17), (4096, 513), (0, 1), (-1, 0)):
+        assert lib.hsl_scan_ck_rows(T) == rows, (T, lib.hsl_scan_ck_rows(T))
 
 
 def test_argument_errors_are_reported_without_a_gpu():

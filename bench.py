@@ -212,6 +212,10 @@ def bench_scan(args):
                      + (measured_traffic("scan_bwd_kernel")[0] or 0) or None,
                      "traffic_source": measured_traffic("scan_fwd_kernel")[1],
                      "algorithmic_bytes": fwd_b + bwd_b},
+        # the target's own byte count stores c at every step (24 + 40 B per element); these
+        # kernels keep c every 8th step, so the same time moves fewer bytes
+        "target_bytes_64B": 64 * n,
+        "target_ms": round(64 * n / (0.5 * HBM_PEAK_GBS) / 1e6, 4),
     }
     log(f"scan fwd {fwd_ms:.4f} ms ({res['fwd_GBps']} GB/s) bwd {bwd_ms:.4f} ms ({res['bwd_GBps']} GB/s)")
     return res

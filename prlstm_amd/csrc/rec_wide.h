@@ -153,7 +153,11 @@ __device__ __forceinline__ void wide_drain16(f4 (&acc)[RT][2]) {
 //   3. second half of chain 0's products, its S;   4. first half of chain 1's products;
 //   5. chain 0's R of iteration k;   6. second half of chain 1's products, its S.
 // At k = 0 only step 5 runs; chain 1's R of iteration T follows the loop.  R of iteration
-// T writes dh0 (the last products' sum), dc0 and the bias partials instead of a cell.
+// T writes dh0 (the last products' sum), dc0 and the bias partials instead of a cell.  The
+// cell inputs of an R (dout, c, tanh c, the gate activations) are requested after the
+// operand of the products before it has arrived, so their HBM latency runs under those
+// products and not under R's poll (requested just before the poll, the wait for the poll
+// included them: configs[3] +55 us; a phase ahead: -26 us).
 // Slots per chain as in the forward: the broadcast of iteration k in slot k%4, its owner
 // clears slot (k+2)%4 after publishing; partials of iteration k in slot (k-1)%3, cleared
 // by their one reader.
@@ -327,7 +331,25 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
     return true;
   };
   // R: chain ch's reducers of iteration k
-  auto reduce = [&](int ch, int k) -> bool {
+  struct CellIn {
+    float dout, c, tc, dhn;
+    f4 ga;
+  };
+  // the cell's inputs of chain ch's step t = T-1-k, requested a product phase before the
+  // reducer uses them (lanes without a cell read clamped addresses)
+  auto cell_in = [&](int ch, int k, CellIn& in) {
+    in = CellIn{0.f, 0.f, 0.f, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
+    if (rc == ch && k < T) {
+      const size_t ec = c_ok ? (size_t)brow * H + unit : 0, tp = (size_t)(T - 1 - k) * plane + ec;
+      in.dout = p.dout[tp];
+      in.ga = *reinterpret_cast<const f4*>(p.gact + tp * 4);
+      in.c = p.c_save[tp];
+      in.tc = p.tanh_c[tp];
+      if (k == 0 && p.dh_n) in.dhn = p.dh_n[ec];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // requested here, not sunk to their use
+  };
+  auto reduce = [&](int ch, int k, const CellIn& in) -> bool {
     const bool mine = rc == ch;  // wave-uniform
     float dsum = 0.f;
     if (k > 0 && mine && c_ok) {
@@ -367,10 +389,8 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
     const int t = T - 1 - k;
     float d[4] = {0.f, 0.f, 0.f, 0.f};
     if (mine && c_ok) {
-      const size_t e = (size_t)brow * H + unit;
-      const float dh = (k > 0 ? dsum : (p.dh_n ? p.dh_n[e] : 0.f)) + p.dout[(size_t)t * plane + e];
-      const f4 ga = *reinterpret_cast<const f4*>(p.gact + ((size_t)t * plane + e) * 4);
-      cell_bwd(dh, dc, p.c_save[(size_t)t * plane + e], ga[0], ga[1], ga[2], ga[3], p.tanh_c[(size_t)t * plane + e], d);
+      const float dh = (k > 0 ? dsum : in.dhn) + in.dout;
+      cell_bwd(dh, dc, in.c, in.ga[0], in.ga[1], in.ga[2], in.ga[3], in.tc, d);
       float* const dg = p.dgates + (size_t)t * plane4 + (size_t)brow * 4 * H + unit;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -404,11 +424,13 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
     constexpr int NCH = decltype(nchc)::value;
     f4 acc[CT][2];
     u4v q[NQ];
+    CellIn in;
     zero_acc(acc);
     if (!fetch(0, k, q)) return false;  // 1
+    if constexpr (NCH > 1) cell_in(1, k - 1, in);
     mult(q, IC0{}, acc);
     if constexpr (NCH > 1) {
-      if (!reduce(1, k - 1)) return false;  // 2
+      if (!reduce(1, k - 1, in)) return false;  // 2
     }
     mult(q, IC1{}, acc);  // 3
     if constexpr (NCH > 1) {
@@ -421,20 +443,29 @@ __device__ __forceinline__ void rec_bwd_wide_body(const WBwdArgs& p, int x, int 
     if constexpr (NCH > 1) {
       zero_acc(acc);
       if (!fetch_settle(1, k, q)) return false;  // 4
+      cell_in(0, k, in);
       mult(q, IC0{}, acc);
+    } else {
+      cell_in(0, k, in);
     }
-    if (!reduce(0, k)) return false;  // 5
+    if (!reduce(0, k, in)) return false;  // 5
     if constexpr (NCH > 1) {
       mult(q, IC1{}, acc);  // 6
       if (!send(1, k, acc)) return false;
     }
     return true;
   };
-  if (!reduce(0, 0)) return;
+  {
+    CellIn in0;
+    cell_in(0, 0, in0);
+    if (!reduce(0, 0, in0)) return;
+  }
   if (nch > 1) {
     for (int k = 1; k <= T; ++k)
       if (!step(k, std::integral_constant<int, 2>{})) return;
-    reduce(1, T);
+    CellIn inT;
+    cell_in(1, T, inT);
+    reduce(1, T, inT);
   } else {
     for (int k = 1; k <= T; ++k)
       if (!step(k, std::integral_constant<int, 1>{})) return;

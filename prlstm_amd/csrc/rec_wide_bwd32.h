@@ -142,6 +142,18 @@ __device__ __forceinline__ void rec_bwd_wide1_body(const WBwdArgs& p, int x, int
   const size_t islot = (size_t)kWideWgs * S::INBOX;
   for (int k = 0; k <= T; ++k) {
     const int t = T - 1 - k;  // the cell's step (-1 after the last product: dh0)
+    // the cell's inputs of step t, requested before the products so that their latency runs
+    // under them (lanes without a cell read clamped addresses)
+    float in_do = 0.f, in_c = 0.f, in_tc = 0.f, in_dhn = 0.f;
+    f4 in_ga = f4{0.f, 0.f, 0.f, 0.f};
+    if (reducer && k < T) {
+      const size_t ec = c_ok ? (size_t)cb * H + unit : 0, tp = (size_t)t * plane + ec;
+      in_do = p.dout[tp];
+      in_ga = *reinterpret_cast<const f4*>(p.gact + tp * 4);
+      in_c = p.c_save[tp];
+      in_tc = p.tanh_c[tp];
+      if (k == 0 && p.dh_n) in_dhn = p.dh_n[ec];
+    }
     float dsum = 0.f;
     if (k > 0) {
       // ---- 1. products with a_g dg_{t+1} of the wave's rows ---------------------------
@@ -246,10 +258,8 @@ __device__ __forceinline__ void rec_bwd_wide1_body(const WBwdArgs& p, int x, int
     // ---- 3b. cell backward of step t, dgates_t, the broadcast of a_g dg_t ---------------
     float d[4] = {0.f, 0.f, 0.f, 0.f};
     if (c_ok) {
-      const size_t e = (size_t)cb * H + unit;
-      float dh = (k > 0 ? dsum : (p.dh_n ? p.dh_n[e] : 0.f)) + p.dout[(size_t)t * plane + e];
-      const f4 ga = *reinterpret_cast<const f4*>(p.gact + ((size_t)t * plane + e) * 4);
-      cell_bwd(dh, dc, p.c_save[(size_t)t * plane + e], ga[0], ga[1], ga[2], ga[3], p.tanh_c[(size_t)t * plane + e], d);
+      const float dh = (k > 0 ? dsum : in_dhn) + in_do;
+      cell_bwd(dh, dc, in_c, in_ga[0], in_ga[1], in_ga[2], in_ga[3], in_tc, d);
       float* const dg = p.dgates + (size_t)t * plane4 + (size_t)cb * 4 * H + unit;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {

@@ -726,7 +726,7 @@ __device__ __forceinline__ void rec_fwd_body(const PFwdArgs& p, int grp, int wg,
       // block and each lane reads its row back: an eighth of the cache-line requests.
       // At configs[2] the slice is in registers 9.3-9.7 us after launch instead of 11.2
       // (the rest is the 32 MiB that the eight XCDs' copies of W_hh read).
-      constexpr int KC = KQ < 64 ? KQ : 64;  // k per round
+      constexpr int KC = KQ < 64 ? KQ : 64;  // k per staging pass
       constexpr int LPR = KC / 4, RPI = 64 / LPR, PITCH = KC + 4;
       float* const stg = fwd_wstage(xin) + q * 64 * PITCH;
       static_assert(4 * 64 * PITCH * sizeof(float) <= kFwdWStageBytes, "staging fits");

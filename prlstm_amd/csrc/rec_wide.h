@@ -49,12 +49,6 @@ template <bool FAST>
 __device__ __forceinline__ void quad_store(__amdgpu_buffer_rsrc_t r, unsigned word, u4v v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)(4u * word), 0, FAST ? kCpolSc0 : kCpolSc1);
 }
-typedef unsigned u2v __attribute__((ext_vector_type(2)));
-template <bool FAST>
-__device__ __forceinline__ void pair_store(__amdgpu_buffer_rsrc_t r, unsigned word, u2v v) {
-  __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)(4u * word), 0, FAST ? kCpolSc0 : kCpolSc1);
-}
-
 template <bool FAST>
 __device__ __forceinline__ void quad_put(__amdgpu_buffer_rsrc_t r, unsigned word, f4 v) {
   quad_store<FAST>(r, word, u4v{__float_as_uint(canon_nan(v[0])), __float_as_uint(canon_nan(v[1])),

@@ -1838,14 +1838,21 @@ __device__ __forceinline__ bool rec_bwd_wgrad_win(const PBwdArgs& p, int grp, in
     *reinterpret_cast<__bf16*>(dst + 2048) = p2;
   };
 
-  // Slot (m, j), m = 0..M (M windows): step s = 8m + j when s < T, and runs tiles j and
-  // j + 8 of window m-1.  Slots with s >= T come after the loop's last step: the first
-  // of them (s == T) zeroes the A elements of the missing steps of the last window and
-  // takes part in the final barrier, and they run the rest of the products without
-  // waiting for anything.
+  // Slot (m, j), m = 0..M (M windows): step s = 8m + j when s < T, and runs tile j of
+  // window m-1 and, in the odd slots, one of the tiles past the eighth (xtile: the dW_ih
+  // tiles when the workgroup has 12).  Slot 0 also reads the window's A pieces, so the
+  // extra tiles go to the odd slots: put in slots 0-3 (tiles j and j+8) they made the
+  // weight-gradient waves reach the recurrent waves' barrier 1.2 us late after slot 0 and
+  // 0.24 us late after slots 1-3 (barrier-arrival stamps), and the configs[2] step took
+  // 0.968-0.972 ms instead of 0.948-0.953.  Slots with s >= T come after the loop's last
+  // step: the first of them (s == T) zeroes the A elements of the missing steps of the
+  // last window and takes part in the final barrier, and they run the rest of the products
+  // without waiting for anything.
   const int M = (T + kWin - 1) / kWin;
   const int last = M - 1, nvalid = T - kWin * last;  // steps of the last window
-  float nb[2][kWin];  // B of the next slot's tiles (j and j + 8)
+  static_assert(C - kWin <= kWin / 2, "one extra tile per odd slot");
+  auto xtile = [](int j) constexpr { return (j % 2 == 1 && kWin + j / 2 < C) ? kWin + j / 2 : -1; };
+  float nb[2][kWin];  // B of the next slot's tiles (j and xtile(j))
   u32x4 apc[4][3];    // A pieces of the window whose products the slots run
   bool final_done = false;
   auto slot = [&](int m, auto jc) __attribute__((always_inline)) -> bool {
@@ -1873,10 +1880,10 @@ __device__ __forceinline__ bool rec_bwd_wgrad_win(const PBwdArgs& p, int grp, in
       }
       if (j == 0 || s == T) read_a(max(m - 1, 0), apc);
     }
-    if (m > 0) {  // window m-1's tiles j and j + 8
+    if (m > 0) {  // window m-1's tiles j and xtile(j)
       const int nv = m - 1 == last ? nvalid : kWin;
       if constexpr (j < C) products(j, m - 1, nb[0], nv, apc);
-      if constexpr (j + kWin < C) products(j + kWin, m - 1, nb[1], nv, apc);
+      if constexpr (xtile(j) >= 0) products(xtile(j), m - 1, nb[1], nv, apc);
       if constexpr (j == kWin - 1)
         if (m == M || (kWin * m) % TS == 0) dump_h(kWin * (m - 1) / TS);
     }
@@ -1885,7 +1892,7 @@ __device__ __forceinline__ bool rec_bwd_wgrad_win(const PBwdArgs& p, int grp, in
       constexpr int jn = (j + 1) % kWin;
       const int wn = min(max(j + 1 < kWin ? m - 1 : m, 0), M - 1);
       if constexpr (jn < C) load_b(jn, wn, nb[0]);
-      if constexpr (jn + kWin < C) load_b(jn + kWin, wn, nb[1]);
+      if constexpr (xtile(jn) >= 0) load_b(xtile(jn), wn, nb[1]);
       // the loads stay here, a slot ahead of their use: without this the compiler sinks
       // them past the next barrier to the products, and each slot waits for memory twice
       asm volatile("" ::: "memory");

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define HSL_ABI_VERSION 2
+#define HSL_ABI_VERSION 3
 
 enum hsl_status {
   HSL_OK = 0,
@@ -205,14 +205,15 @@ int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float*
                 int T, int B, int D, int H, void* stream);
 
 /* hsl_par_fwd for a half-precision module: x [T,B,D] and w_ih [4H,D] are bf16
- * (fmt 0) or fp16 (fmt 1); b_ih, c0 and everything written are fp32.  The input
- * projection runs on 16-bit MFMA with fp32 accumulation: each product of two 16-bit
- * values is exact in fp32, so gates equal the fp32 projection of the widened
- * operands up to the order of the fp32 additions.  Replaces the same call sites as
- * hsl_par_fwd (_parallel.py:38-74) for modules moved to bf16/fp16 (the way
- * test_parallel.py:22-38 runs bf16). */
+ * (fmt 0) or fp16 (fmt 1); b_ih, c0, gates and c_ck are fp32, and out [T,B,H] is in
+ * the module's format (x's): the fp32 scan output rounded to nearest even when it is
+ * stored, as the module's output conversion rounds it.  The input projection runs on
+ * 16-bit MFMA with fp32 accumulation: each product of two 16-bit values is exact in
+ * fp32, so gates equal the fp32 projection of the widened operands up to the order of
+ * the fp32 additions.  Replaces the same call sites as hsl_par_fwd (_parallel.py:38-74)
+ * for modules moved to bf16/fp16 (the way test_parallel.py:22-38 runs bf16). */
 int hsl_par_fwd_b16(const void* x, const float* c0, const void* w_ih, const float* b_ih,
-                    float eps, float* gates, float* out, float* c_ck,
+                    float eps, float* gates, void* out, float* c_ck,
                     int T, int B, int D, int H, int fmt, void* stream);
 
 size_t hsl_par_bwd_ws_bytes(int T, int B, int D, int H);
@@ -227,16 +228,17 @@ int hsl_par_bwd(const float* dout, const float* dh_n, const float* dc_n,
                 float* dx, float* dw_ih, float* db_ih, float* dc0,
                 void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream);
 
-/* hsl_par_bwd for a bf16 (fmt 0) or fp16 (fmt 1) module: x and w_ih are 16-bit,
- * everything else as in hsl_par_bwd (fp32 gradients).  The results equal
- * hsl_par_bwd's on the widened x and w_ih bit for bit.  A bf16 x / w_ih is read by
+/* hsl_par_bwd for a bf16 (fmt 0) or fp16 (fmt 1) module: x, w_ih and dout (the
+ * gradient of hsl_par_fwd_b16's out) are 16-bit, everything else as in hsl_par_bwd
+ * (fp32 gradients).  The results equal hsl_par_bwd's on the widened x, w_ih and dout
+ * bit for bit.  A bf16 x / w_ih is read by
  * the split-product kernel as it is (one bf16 piece, three products per k-step
  * instead of six); otherwise (fp16, or products too small for that kernel) it is
  * widened into the workspace first.  Backward of the reference's parallel path for
  * a module moved to bf16/fp16 (_parallel.py:38-74, run that way by
  * test_parallel.py:22-38). */
 size_t hsl_par_bwd_b16_ws_bytes(int T, int B, int D, int H);
-int hsl_par_bwd_b16(const float* dout, const float* dh_n, const float* dc_n,
+int hsl_par_bwd_b16(const void* dout, const float* dh_n, const float* dc_n,
                     const void* x, const float* c0, const float* gates, const float* c_ck,
                     const void* w_ih, float eps,
                     float* dx, float* dw_ih, float* db_ih, float* dc0,

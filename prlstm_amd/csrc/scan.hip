@@ -46,13 +46,50 @@
 namespace hsl {
 namespace {
 
+// Element formats of the out / dout streams: fp32, or the 16-bit format of a half module's
+// output (bf16, fp16), converted with round-to-nearest-even as torch's .to() does.
+enum StreamFmt { kF32 = 0, kBf16 = 1, kF16 = 2 };
+template <int F>
+constexpr unsigned fmt_bytes() {
+  return F == kF32 ? 4u : 2u;
+}
+template <int F>
+__device__ __forceinline__ void out_store(float v, __amdgpu_buffer_rsrc_t r, unsigned voff) {
+  if constexpr (F == kF32) {
+    row_store_nt(v, r, voff, 0);
+  } else {
+    // v is first rounded to fp32 (kept from fusing into a mixed-precision multiply that
+    // would round the product to 16 bits once), so the result is the fp32 value's
+    // conversion, as torch's .to() of the fp32 output gives
+    asm volatile("" : "+v"(v));
+    unsigned short u;
+    if constexpr (F == kBf16)
+      u = __builtin_bit_cast(unsigned short, (__bf16)v);
+    else
+      u = __builtin_bit_cast(unsigned short, (_Float16)v);
+    __builtin_amdgcn_raw_buffer_store_b16(u, r, (int)voff, 0, kCpolNt);
+  }
+}
+template <int F>
+__device__ __forceinline__ float in_load(__amdgpu_buffer_rsrc_t r, unsigned voff, int soff) {
+  if constexpr (F == kF32) {
+    return row_load(r, voff, soff);
+  } else {
+    const unsigned short u = __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, soff, kCpolNt);
+    if constexpr (F == kBf16)
+      return __uint_as_float((unsigned)u << 16);
+    else
+      return (float)__builtin_bit_cast(_Float16, u);
+  }
+}
+
 constexpr int kFwdWaves = 16, kFwdSteps = 8;
 constexpr int kBwdWaves = 8, kBwdSteps = 8;
 constexpr int kCkSteps = 8;  // steps per checkpoint row of c (one wave's group in both scans)
 
-template <int NW, int L>
+template <int NW, int L, int OF>
 __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restrict__ gates, const float* __restrict__ c0,
-                                                          float eps, float* __restrict__ out, float* __restrict__ cck,
+                                                          float eps, void* __restrict__ out, float* __restrict__ cck,
                                                           int T, int B, int H) {
   static_assert(L == kCkSteps, "checkpoint rows are one per L-step group");
   __shared__ float2 sAV[NW][64];  // each wave's composed map (A, V) of the chunk
@@ -67,6 +104,10 @@ __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restri
   const unsigned grow = (unsigned)(gstride * 4), orow = (unsigned)(ostride * 4);
   const unsigned gv = ok ? (unsigned)(b * 4 * H + j) * 4u : kOffNone;  // lane offsets in a row
   const unsigned ov = ok ? (unsigned)ch * 4u : kOffNone;
+  // out rows in their own element format
+  constexpr unsigned OB = fmt_bytes<OF>();
+  const unsigned orow_o = (unsigned)ostride * OB, ov_o = ok ? (unsigned)ch * OB : kOffNone;
+  char* const outb = static_cast<char*>(out);
   const int hb = 4 * H;  // bytes between gate planes
   if (w == 0) sC[lane] = ok ? fmaxf(c0 ? c0[ch] : 0.f, eps) : 0.f;
 
@@ -125,10 +166,11 @@ __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restri
 #pragma unroll
     for (int s = 0; s < L; ++s) {
       const int t = t0 + s;
-      const unsigned obytes = (!TAIL || t < T) ? orow : 0u;
+      const unsigned obytes = (!TAIL || t < T) ? orow_o : 0u;
       c = __builtin_fmaf(fv[s], c, bv[s]);  // the backward repeats exactly this from the carry-in
       // c >= eps > 0 (a positive combination of positive terms)
-      row_store_nt(ogv[s] * tanh_pos_f(c), row_rsrc(out + (size_t)t * ostride, obytes), ov, 0);
+      out_store<OF>(ogv[s] * tanh_pos_f(c),
+                    row_rsrc(reinterpret_cast<const float*>(outb + (size_t)t * orow_o), obytes), ov_o);
     }
     // the group holding step T-1 writes c_{T-1} (steps past T are identity maps)
     row_store_nt(c, row_rsrc(cck + (size_t)nck * ostride, (t0 < T && T <= t0 + L) ? orow : 0u), ov, 0);
@@ -151,10 +193,10 @@ __global__ __launch_bounds__(NW * 64) void scan_fwd_kernel(const float* __restri
 //   G_t = e_t + f~_{t+1} G_{t+1},  e_t = dout'_t o_t (1 - tanh^2 c_t) (+ dc_n at T-1),
 //   dout'_t = dout_t (+ dh_n at T-1),  f~_T = 0.
 // Then df~_t = G_t c_{t-1}, db~_t = G_t and the sigmoid/clamp chain gives dgates.
-template <int NW, int L>
+template <int NW, int L, int DF>
 __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
     const float* __restrict__ gates, const float* __restrict__ c0, const float* __restrict__ cck,
-    const float* __restrict__ dout, const float* __restrict__ dh_n, const float* __restrict__ dc_n, float eps,
+    const void* __restrict__ dout, const float* __restrict__ dh_n, const float* __restrict__ dc_n, float eps,
     float* __restrict__ dgates, double* __restrict__ db_part, float* __restrict__ dc0, int T, int B, int H) {
   static_assert(L == kCkSteps, "a wave's steps are one checkpoint group");
   __shared__ float2 sAV[NW][64];  // each wave's composed reverse map (A, V) of the chunk
@@ -170,6 +212,10 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
   const unsigned grow = (unsigned)(gstride * 4), orow = (unsigned)(ostride * 4);
   const unsigned gv = ok ? (unsigned)(b * 4 * H + j) * 4u : kOffNone;
   const unsigned ov = ok ? (unsigned)ch * 4u : kOffNone;
+  // dout rows in their own element format
+  constexpr unsigned DB = fmt_bytes<DF>();
+  const unsigned drow = (unsigned)ostride * DB, dv = ok ? (unsigned)ch * DB : kOffNone;
+  const char* const doutb = static_cast<const char*>(dout);
   const int hb = 4 * H;
   const float c0v = (ok && c0) ? c0[ch] : 0.f;
   const bool c0_pass = ok && c0v >= eps;
@@ -182,13 +228,21 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
   // c carried into its first step (cin); rows past T read 0
   auto load = [&](int chunk, float(&r)[5][L], float& fnext, float& cin) {
     const int ws = chunk * CH + w * L;
+    // a 16-bit dout: the wave's L rows as one buffer (fewer scalar registers than a buffer
+    // per row, which made that instance spill them; the fp32 one keeps a buffer per row)
+    const int nd = min(T - ws, L);
+    const auto rd = row_rsrc(reinterpret_cast<const float*>(doutb + (size_t)ws * drow), nd > 0 ? (unsigned)nd * drow : 0u);
 #pragma unroll
     for (int s = 0; s < L; ++s) {
       const int t = ws + s;
       const auto rg = row_rsrc(gates + (size_t)t * gstride, t < T ? grow : 0u);
 #pragma unroll
       for (int g = 0; g < 4; ++g) r[g][s] = row_load(rg, gv, g * hb);
-      r[4][s] = row_load(row_rsrc(dout + (size_t)t * ostride, t < T ? orow : 0u), ov, 0);
+      if constexpr (DF == kF32)
+        r[4][s] = in_load<DF>(row_rsrc(reinterpret_cast<const float*>(doutb + (size_t)t * drow), t < T ? drow : 0u),
+                              dv, 0);
+      else
+        r[4][s] = in_load<DF>(rd, dv, s * (int)drow);
     }
     const int tn = ws + L;
     fnext = row_load<0>(row_rsrc(gates + (size_t)tn * gstride, tn < T ? grow : 0u), gv, hb);
@@ -320,21 +374,30 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd_kernel(
 // one time step of gates (16 B H bytes) is addressed as a buffer of < 2^31 bytes
 int check_scan_dims(int T, int B, int H, int D = 0) { return check_shape("parallel mode", T, B, D, H); }
 
-int scan_fwd(const float* gates, const float* c0, float eps, float* out, float* cck, int T, int B, int H,
-             hipStream_t s) {
+// out (forward) and dout (backward) in format sf (StreamFmt); everything else fp32.
+int scan_fwd(const float* gates, const float* c0, float eps, void* out, float* cck, int T, int B, int H,
+             hipStream_t s, int sf = kF32) {
   const int C = B * H;
   if (C == 0 || T == 0) return HSL_OK;
   const int slot = timing_begin(kTimeScanFwd, s);
-  hipLaunchKernelGGL((scan_fwd_kernel<kFwdWaves, kFwdSteps>), dim3((C + 63) / 64), dim3(kFwdWaves * 64), 0, s, gates,
-                     c0, eps, out, cck, T, B, H);
+  const dim3 grid((C + 63) / 64), block(kFwdWaves * 64);
+  if (sf == kBf16)
+    hipLaunchKernelGGL((scan_fwd_kernel<kFwdWaves, kFwdSteps, kBf16>), grid, block, 0, s, gates, c0, eps, out, cck,
+                       T, B, H);
+  else if (sf == kF16)
+    hipLaunchKernelGGL((scan_fwd_kernel<kFwdWaves, kFwdSteps, kF16>), grid, block, 0, s, gates, c0, eps, out, cck,
+                       T, B, H);
+  else
+    hipLaunchKernelGGL((scan_fwd_kernel<kFwdWaves, kFwdSteps, kF32>), grid, block, 0, s, gates, c0, eps, out, cck,
+                       T, B, H);
   HSL_HIP(hipGetLastError());
   timing_end(slot, s);
   return HSL_OK;
 }
 
-int scan_bwd(const float* gates, const float* c0, const float* cck, const float* dout, const float* dh_n,
+int scan_bwd(const float* gates, const float* c0, const float* cck, const void* dout, const float* dh_n,
              const float* dc_n, float eps, float* dgates, double* db_part, float* dc0, int T, int B, int H,
-             hipStream_t s) {
+             hipStream_t s, int sf = kF32) {
   const int C = B * H;
   if (C == 0) return HSL_OK;
   if (T == 0) {  // no steps: dc0 = dc_n through the clamp is not reached; all zero
@@ -343,8 +406,16 @@ int scan_bwd(const float* gates, const float* c0, const float* cck, const float*
     return HSL_OK;
   }
   const int slot = timing_begin(kTimeScanBwd, s);
-  hipLaunchKernelGGL((scan_bwd_kernel<kBwdWaves, kBwdSteps>), dim3((C + 63) / 64), dim3(kBwdWaves * 64), 0, s, gates,
-                     c0, cck, dout, dh_n, dc_n, eps, dgates, db_part, dc0, T, B, H);
+  const dim3 grid((C + 63) / 64), block(kBwdWaves * 64);
+  if (sf == kBf16)
+    hipLaunchKernelGGL((scan_bwd_kernel<kBwdWaves, kBwdSteps, kBf16>), grid, block, 0, s, gates, c0, cck, dout, dh_n,
+                       dc_n, eps, dgates, db_part, dc0, T, B, H);
+  else if (sf == kF16)
+    hipLaunchKernelGGL((scan_bwd_kernel<kBwdWaves, kBwdSteps, kF16>), grid, block, 0, s, gates, c0, cck, dout, dh_n,
+                       dc_n, eps, dgates, db_part, dc0, T, B, H);
+  else
+    hipLaunchKernelGGL((scan_bwd_kernel<kBwdWaves, kBwdSteps, kF32>), grid, block, 0, s, gates, c0, cck, dout, dh_n,
+                       dc_n, eps, dgates, db_part, dc0, T, B, H);
   HSL_HIP(hipGetLastError());
   timing_end(slot, s);
   return HSL_OK;
@@ -382,7 +453,7 @@ size_t carve_par_b16(void* ws, size_t cap, int T, int B, int D, int H, ParWs* o,
   return c.off;
 }
 
-int par_bwd_impl(const float* dout, const float* dh_n, const float* dc_n, const void* x, const float* c0,
+int par_bwd_impl(const void* dout, const float* dh_n, const float* dc_n, const void* x, const float* c0,
                  const float* gates, const float* c_ck, const void* w_ih, float eps, float* dx, float* dw_ih,
                  float* db_ih, float* dc0, void* ws, size_t ws_bytes, int T, int B, int D, int H, int fmt,
                  hipStream_t s) {
@@ -402,7 +473,8 @@ int par_bwd_impl(const float* dout, const float* dh_n, const float* dc_n, const 
     return HSL_OK;
   }
   if (!dout || !x || !gates || !c_ck) return fail(HSL_ERR_ARG, "%s: null pointer", fn);
-  HSL_CHECK(scan_bwd(gates, c0, c_ck, dout, dh_n, dc_n, eps, w.dgates, w.db_part, dc0, T, B, H, s));
+  HSL_CHECK(scan_bwd(gates, c0, c_ck, dout, dh_n, dc_n, eps, w.dgates, w.db_part, dc0, T, B, H, s,
+                     fmt < 0 ? kF32 : (fmt == 0 ? kBf16 : kF16)));
   HSL_CHECK(bias_grads_from_parts(w.db_part, B, nullptr, nullptr, nullptr, db_ih, nullptr, nullptr, H, s));
   const int TB = T * B;
   if (D > 0) {
@@ -463,7 +535,8 @@ int hsl_par_fwd(const float* x, const float* c0, const float* w_ih, const float*
 }
 
 int hsl_par_fwd_b16(const void* x, const float* c0, const void* w_ih, const float* b_ih, float eps, float* gates,
-                    float* out, float* c_ck, int T, int B, int D, int H, int fmt, void* stream) {
+                    void* out, float* c_ck, int T, int B, int D, int H, int fmt, void* stream) {
+  if (fmt != 0 && fmt != 1) return fail(HSL_ERR_ARG, "hsl_par_fwd_b16: format must be 0 (bf16) or 1 (fp16)");
   HSL_CHECK(check_scan_dims(T, B, H, D));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (T == 0 || B == 0 || H == 0) return HSL_OK;
@@ -471,7 +544,7 @@ int hsl_par_fwd_b16(const void* x, const float* c0, const void* w_ih, const floa
   const int slot = timing_begin(kTimeInputProj, s);
   HSL_CHECK(gemm_b16_run(x, w_ih, b_ih, gates, T * B, 4 * H, D, D, D, 4 * H, fmt, s));
   timing_end(slot, s);
-  return scan_fwd(gates, c0, eps, out, c_ck, T, B, H, s);
+  return scan_fwd(gates, c0, eps, out, c_ck, T, B, H, s, fmt == 0 ? kBf16 : kF16);
 }
 
 size_t hsl_par_bwd_ws_bytes(int T, int B, int D, int H) {
@@ -493,7 +566,7 @@ int hsl_par_bwd(const float* dout, const float* dh_n, const float* dc_n, const f
                       H, -1, static_cast<hipStream_t>(stream));
 }
 
-int hsl_par_bwd_b16(const float* dout, const float* dh_n, const float* dc_n, const void* x, const float* c0,
+int hsl_par_bwd_b16(const void* dout, const float* dh_n, const float* dc_n, const void* x, const float* c0,
                     const float* gates, const float* c_ck, const void* w_ih, float eps, float* dx, float* dw_ih,
                     float* db_ih, float* dc0, void* ws, size_t ws_bytes, int T, int B, int D, int H, int fmt,
                     void* stream) {

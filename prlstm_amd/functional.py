@@ -186,10 +186,12 @@ _HALF = (torch.bfloat16, torch.float16)
 class ParallelHalfFn(torch.autograd.Function):
     """Parallel mode of a bf16/fp16 module: x and W_ih stay 16-bit for the input
     projection, which runs on 16-bit MFMA with fp32 accumulation (each product of two
-    16-bit values is exact in fp32); c0 and b_ih arrive widened, and the scan, the
-    outputs and the whole backward are fp32, as in ``ParallelFn``; the backward reads
-    the 16-bit x and W_ih itself (``hsl_par_bwd_b16``, results equal to those on the
-    widened operands)."""
+    16-bit values is exact in fp32); c0 and b_ih arrive widened, and the scan and the
+    whole backward compute in fp32, as in ``ParallelFn``.  The scan stores ``out`` in the
+    module's 16-bit format (the rounding the module's output conversion would apply) and
+    its backward reads the 16-bit ``dout`` as it is, so no [T,B,H] conversion pass runs
+    either way; the backward also reads the 16-bit x and W_ih itself (``hsl_par_bwd_b16``,
+    results equal to those on the widened operands)."""
 
     @staticmethod
     def forward(ctx, x, c0, w_ih, b_ih, eps):
@@ -207,7 +209,7 @@ class ParallelHalfFn(torch.autograd.Function):
         x, c0, w_ih, b_ih = map(_c, (x, c0, w_ih, b_ih))
         ctx.set_materialize_grads(False)
         gates = x.new_empty(T, B, 4 * H, dtype=torch.float32)
-        out = x.new_empty(T, B, H, dtype=torch.float32)
+        out = x.new_empty(T, B, H)  # the module's 16-bit format
         c_ck = x.new_empty(_lib.load().hsl_scan_ck_rows(T), B, H, dtype=torch.float32)
         fmt = 0 if x.dtype == torch.bfloat16 else 1
         P = _lib.ptr
@@ -222,8 +224,10 @@ class ParallelHalfFn(torch.autograd.Function):
     def backward(ctx, dout, dh_n, dc_n):
         x, c0, w_ih, gates, c_ck = ctx.saved_tensors
         T, B, D, H = ctx.dims
-        dout = _c(dout) if dout is not None else c_ck.new_zeros(T, B, H)
-        dh_n, dc_n = _c(dh_n), _c(dc_n)
+        # dout in out's 16-bit format (read as it is); dh_n and dc_n widened to fp32
+        dout = _c(dout.to(x.dtype)) if dout is not None else x.new_zeros(T, B, H)
+        dh_n = _c(dh_n.float()) if dh_n is not None else None
+        dc_n = _c(dc_n.float()) if dc_n is not None else None
         need = ctx.needs_input_grad
         f32 = dict(device=x.device, dtype=torch.float32)
         dx = torch.empty(T, B, D, **f32) if need[0] else None

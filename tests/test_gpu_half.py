@@ -156,7 +156,9 @@ def test_parallel_backward_16bit_operands_equal_widened(dev, fmt, T, B, D, H):
     so the split-product kernel issues three products per k-step instead of six (at
     configs[4] size), and otherwise the operand is widened into the workspace.  Either way
     the gradients must equal hsl_par_bwd's on the widened operands bit for bit (the six
-    products' extra terms are exact zeros added in the same order)."""
+    products' extra terms are exact zeros added in the same order).  hsl_par_fwd_b16 writes
+    out in the 16-bit format: the fp32 scan output of the same gates (hsl_scan_fwd)
+    rounded to nearest even, bit for bit; the backward reads the 16-bit dout."""
     dt = torch.bfloat16 if fmt == 0 else torch.float16
     print(f"par bwd 16-bit fmt={fmt} T={T} B={B} D={D} H={H}", flush=True)
     from prlstm_amd import _lib
@@ -167,11 +169,18 @@ def test_parallel_backward_16bit_operands_equal_widened(dev, fmt, T, B, D, H):
     b_ih = (torch.randn(4 * H, generator=g) * 0.05).to(dev)
     c0 = (torch.randn(B, H, generator=g) * 0.5).to(dev)
     gates = torch.empty(T, B, 4 * H, device=dev)
-    out = torch.empty(T, B, H, device=dev)
+    out = torch.empty(T, B, H, dtype=dt, device=dev)
     c_ck = torch.empty(_lib.load().hsl_scan_ck_rows(T), B, H, device=dev)
     _lib.call("hsl_par_fwd_b16", P(x16), P(c0), P(w16), P(b_ih), 1e-6, P(gates), P(out), P(c_ck),
               T, B, D, H, fmt, s)
-    dout = torch.randn(T, B, H, generator=g).to(dev)
+    out32 = torch.empty(T, B, H, device=dev)
+    ck32 = torch.empty_like(c_ck)
+    _lib.call("hsl_scan_fwd", P(gates), P(c0), 1e-6, P(out32), P(ck32), T, B, H, s)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out32.to(dt))
+    assert torch.equal(c_ck, ck32)
+    dout16 = torch.randn(T, B, H, generator=g).to(dt).to(dev)
+    dout32 = dout16.float()
     dh_n = torch.randn(B, H, generator=g).to(dev)
     dc_n = torch.randn(B, H, generator=g).to(dev)
     res = []
@@ -184,12 +193,12 @@ def test_parallel_backward_16bit_operands_equal_widened(dev, fmt, T, B, D, H):
             xw, ww = x16.float(), w16.float()
             n = _lib.load().hsl_par_bwd_ws_bytes(T, B, D, H)
             ws = torch.empty(n, dtype=torch.uint8, device=dev)
-            _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(xw), P(c0), P(gates), P(c_ck), P(ww), 1e-6,
+            _lib.call("hsl_par_bwd", P(dout32), P(dh_n), P(dc_n), P(xw), P(c0), P(gates), P(c_ck), P(ww), 1e-6,
                       P(dx), P(dw), P(db), P(dc0), P(ws), n, T, B, D, H, s)
         else:
             n = _lib.load().hsl_par_bwd_b16_ws_bytes(T, B, D, H)
             ws = torch.empty(n, dtype=torch.uint8, device=dev)
-            _lib.call("hsl_par_bwd_b16", P(dout), P(dh_n), P(dc_n), P(x16), P(c0), P(gates), P(c_ck), P(w16),
+            _lib.call("hsl_par_bwd_b16", P(dout16), P(dh_n), P(dc_n), P(x16), P(c0), P(gates), P(c_ck), P(w16),
                       1e-6, P(dx), P(dw), P(db), P(dc0), P(ws), n, T, B, D, H, fmt, s)
         torch.cuda.synchronize()
         res.append((dx.clone(), dw.clone(), db.clone(), dc0.clone()))

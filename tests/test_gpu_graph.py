@@ -33,18 +33,25 @@ def test_graph_replays_split_products(dev):
     _check_replays(dev, True, (1024, 16, 256, 1024))
 
 
-def _check_replays(dev, parallel, shape):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_graph_replays_half_module_parallel(dev, dtype):
+    """A 16-bit module in parallel mode (16-bit projection, the scan storing out and reading
+    dout in the module's format) replayed as one graph: every replay equals an eager step."""
+    _check_replays(dev, True, (64, 8, 32, 64), dtype)
+
+
+def _check_replays(dev, parallel, shape, dtype=torch.float32):
     T, B, D, H = shape
-    print(f"graph T={T} B={B} D={D} H={H} parallel={parallel}", flush=True)
+    print(f"graph T={T} B={B} D={D} H={H} parallel={parallel} dtype={dtype}", flush=True)
     torch.manual_seed(0)
-    m = prlstm_amd.HeadStartLSTM(D, H, parallel=parallel).to(dev)
+    m = prlstm_amd.HeadStartLSTM(D, H, parallel=parallel).to(dev, dtype)
     with torch.no_grad():
         m.a.fill_(0.3)
     other = prlstm_amd.HeadStartLSTM(D, H).to(dev)
-    x0 = torch.randn(T, B, D, device=dev)
+    x0 = torch.randn(T, B, D, device=dev).to(dtype)
     step = GraphedTrainStep(m, x0)
     for rep in range(4):
-        x = torch.randn(T, B, D, device=dev)
+        x = torch.randn(T, B, D, device=dev).to(dtype)
         out_g = step.step(x).detach().clone()
         grads_g = {n: p.grad.detach().clone() for n, p in m.named_parameters() if p.grad is not None}
         torch.cuda.synchronize()
@@ -52,7 +59,7 @@ def _check_replays(dev, parallel, shape):
         _eager(other, torch.randn(T, B, D, device=dev))
         torch.cuda.synchronize()
         # eager reference on a clone of the module (the graph owns m's .grad tensors)
-        ref = prlstm_amd.HeadStartLSTM(D, H, parallel=parallel).to(dev)
+        ref = prlstm_amd.HeadStartLSTM(D, H, parallel=parallel).to(dev, dtype)
         ref.load_state_dict(m.state_dict())
         out_e, grads_e = _eager(ref, x)
         assert torch.allclose(out_g, out_e, rtol=1e-6, atol=1e-7), rep

@@ -244,6 +244,38 @@ int hsl_par_bwd_b16(const void* dout, const float* dh_n, const float* dc_n,
                     float* dx, float* dw_ih, float* db_ih, float* dc0,
                     void* ws, size_t ws_bytes, int T, int B, int D, int H, int fmt, void* stream);
 
+/* fp64 modules (the reference runs them through its torch backend, test_cpp.py:150-165,
+ * and its parallel functional is dtype-generic, _parallel.py:38-74).  Every argument,
+ * layout and output is that of the fp32 entry point of the same name without "_f64"
+ * (hsl_rec_fwd, hsl_rec_bwd, hsl_par_fwd, hsl_par_bwd), with double for float; all
+ * arithmetic is fp64.  These kernels are written for exactness, not speed: one launch
+ * per time step in recurrent mode, one thread per channel for the scans and a plain
+ * tiled fp64 product; every sum runs in a fixed order (deterministic results).  The
+ * recurrent backward's workspace always holds the [T,B,4H] dgates. */
+size_t hsl_rec_fwd_f64_ws_bytes(int T, int B, int D, int H);
+int hsl_rec_fwd_f64(const double* x, const double* h0, const double* c0,
+                    const double* w_ih, const double* w_hh, const double* b_ih,
+                    const double* b_hh, const double* a,
+                    double* h_save, double* c_save, double* gact, double* tanh_c,
+                    void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream);
+size_t hsl_rec_bwd_f64_ws_bytes(int T, int B, int D, int H);
+int hsl_rec_bwd_f64(const double* dout, const double* dh_n, const double* dc_n,
+                    const double* x, const double* h_save, const double* c_save,
+                    const double* gact, const double* tanh_c,
+                    const double* w_ih, const double* w_hh, const double* b_hh, const double* a,
+                    double* dx, double* dw_ih, double* dw_hh, double* db_ih, double* db_hh,
+                    double* da, double* dh0, double* dc0,
+                    void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream);
+int hsl_par_fwd_f64(const double* x, const double* c0, const double* w_ih, const double* b_ih,
+                    double eps, double* gates, double* out, double* c_ck,
+                    int T, int B, int D, int H, void* stream);
+size_t hsl_par_bwd_f64_ws_bytes(int T, int B, int D, int H);
+int hsl_par_bwd_f64(const double* dout, const double* dh_n, const double* dc_n,
+                    const double* x, const double* c0, const double* gates, const double* c_ck,
+                    const double* w_ih, double eps,
+                    double* dx, double* dw_ih, double* db_ih, double* dc0,
+                    void* ws, size_t ws_bytes, int T, int B, int D, int H, void* stream);
+
 /* The scan kernels on their own (used by hsl_par_fwd / hsl_par_bwd).
  * hsl_scan_fwd: gates [T,B,4H] pre-activations -> out [T,B,H], c_ck (as in
  * hsl_par_fwd).

@@ -17,6 +17,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _Z = ctypes.c_size_t
 _F = ctypes.c_float
+_D = ctypes.c_double
 
 # name -> (restype, argtypes); must match include/hsl.h
 SIGNATURES = {
@@ -45,6 +46,13 @@ SIGNATURES = {
     "hsl_par_bwd": (_I, [_P] * 8 + [_F, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _P]),
     "hsl_par_bwd_b16_ws_bytes": (_Z, [_I, _I, _I, _I]),
     "hsl_par_bwd_b16": (_I, [_P] * 8 + [_F, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _P]),
+    "hsl_rec_fwd_f64_ws_bytes": (_Z, [_I, _I, _I, _I]),
+    "hsl_rec_fwd_f64": (_I, [_P] * 13 + [_Z, _I, _I, _I, _I, _P]),
+    "hsl_rec_bwd_f64_ws_bytes": (_Z, [_I, _I, _I, _I]),
+    "hsl_rec_bwd_f64": (_I, [_P] * 20 + [_P, _Z, _I, _I, _I, _I, _P]),
+    "hsl_par_fwd_f64": (_I, [_P, _P, _P, _P, _D, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "hsl_par_bwd_f64_ws_bytes": (_Z, [_I, _I, _I, _I]),
+    "hsl_par_bwd_f64": (_I, [_P] * 8 + [_D, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _P]),
     "hsl_scan_ck_rows": (_I, [_I]),
     "hsl_scan_fwd": (_I, [_P, _P, _F, _P, _P, _I, _I, _I, _P]),
     "hsl_scan_bwd": (_I, [_P] * 6 + [_F, _P, _P, _P, _I, _I, _I, _P]),

@@ -60,10 +60,16 @@ def _check(x, h0, c0, w_ih, w_hh, b_ih, b_hh, a):
                 "(move the module and inputs to the GPU)")
         if t.device != x.device:
             raise RuntimeError(f"{name} is on {t.device}, x is on {x.device}")
-        if t.dtype != torch.float32:
-            raise RuntimeError(f"prlstm_amd kernels compute in float32 (bf16/fp16 modules are widened "
-                               f"at the functional); {name} is {t.dtype}")
+        if t.dtype != x.dtype or x.dtype not in (torch.float32, torch.float64):
+            raise RuntimeError(f"prlstm_amd kernels compute in float32 or float64 (bf16/fp16 modules are "
+                               f"widened at the functional), every operand in x's dtype; {name} is {t.dtype}, "
+                               f"x is {x.dtype}")
     return T, B, D, H
+
+
+def _entry(name, x):
+    """The C-ABI entry point for x's dtype: name, or its fp64 twin name + '_f64'."""
+    return name + "_f64" if x.dtype == torch.float64 else name
 
 
 def _c(t):
@@ -98,13 +104,15 @@ class RecurrentFn(torch.autograd.Function):
         gact = x.new_empty(T, B, H, 4)
         tanh_c = x.new_empty(T, B, H)
         lib = _lib.load()
-        nbytes = lib.hsl_rec_fwd_ws_bytes(T, B, D, H)
+        f64 = x.dtype == torch.float64
+        nbytes = (lib.hsl_rec_fwd_f64_ws_bytes if f64 else lib.hsl_rec_fwd_ws_bytes)(T, B, D, H)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
         P = _lib.ptr
-        _lib.call("hsl_rec_fwd", P(x), P(h0), P(c0), P(w_ih), P(w_hh), P(b_ih), P(b_hh), P(a),
+        _lib.call(_entry("hsl_rec_fwd", x), P(x), P(h0), P(c0), P(w_ih), P(w_hh), P(b_ih), P(b_hh), P(a),
                   P(h_save), P(c_save), P(gact), P(tanh_c), P(ws), nbytes, T, B, D, H,
                   _lib.stream_of(x.device))
-        _poll(ws, x.device)
+        if not f64:  # the fp64 kernels have no waits between workgroups
+            _poll(ws, x.device)
         ctx.save_for_backward(x, w_ih, w_hh, b_hh, a, h_save, c_save, gact, tanh_c)
         ctx.dims = (T, B, D, H)
         return h_save[1:], h_save[T], c_save[T]
@@ -125,14 +133,17 @@ class RecurrentFn(torch.autograd.Function):
         db_hh = x.new_empty(4 * H)
         da = x.new_empty(4)
         lib = _lib.load()
-        nbytes = lib.hsl_rec_bwd_ws_bytes_for(T, B, D, H, 1 if dx is not None else 0)
+        f64 = x.dtype == torch.float64
+        nbytes = (lib.hsl_rec_bwd_f64_ws_bytes(T, B, D, H) if f64
+                  else lib.hsl_rec_bwd_ws_bytes_for(T, B, D, H, 1 if dx is not None else 0))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
         P = _lib.ptr
-        _lib.call("hsl_rec_bwd", P(dout), P(dh_n), P(dc_n), P(x), P(h_save), P(c_save), P(gact),
+        _lib.call(_entry("hsl_rec_bwd", x), P(dout), P(dh_n), P(dc_n), P(x), P(h_save), P(c_save), P(gact),
                   P(tanh_c), P(w_ih), P(w_hh), P(b_hh), P(a), P(dx), P(dw_ih), P(dw_hh), P(db_ih),
                   P(db_hh), P(da), P(dh0), P(dc0), P(ws), nbytes, T, B, D, H,
                   _lib.stream_of(x.device))
-        _poll(ws, x.device)
+        if not f64:
+            _poll(ws, x.device)
         return dx, dh0, dc0, dw_ih, dw_hh, db_ih, db_hh, da
 
 
@@ -152,7 +163,7 @@ class ParallelFn(torch.autograd.Function):
         out = x.new_empty(T, B, H)
         c_ck = x.new_empty(_lib.load().hsl_scan_ck_rows(T), B, H)
         P = _lib.ptr
-        _lib.call("hsl_par_fwd", P(x), P(c0), P(w_ih), P(b_ih), float(eps), P(gates), P(out),
+        _lib.call(_entry("hsl_par_fwd", x), P(x), P(c0), P(w_ih), P(b_ih), float(eps), P(gates), P(out),
                   P(c_ck), T, B, D, H, _lib.stream_of(x.device))
         ctx.save_for_backward(x, c0, w_ih, gates, c_ck)
         ctx.dims = (T, B, D, H)
@@ -171,10 +182,11 @@ class ParallelFn(torch.autograd.Function):
         dw_ih = torch.empty_like(w_ih)
         db_ih = x.new_empty(4 * H)
         lib = _lib.load()
-        nbytes = lib.hsl_par_bwd_ws_bytes(T, B, D, H)
+        f64 = x.dtype == torch.float64
+        nbytes = (lib.hsl_par_bwd_f64_ws_bytes if f64 else lib.hsl_par_bwd_ws_bytes)(T, B, D, H)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
         P = _lib.ptr
-        _lib.call("hsl_par_bwd", P(dout), P(dh_n), P(dc_n), P(x), P(c0), P(gates), P(c_ck),
+        _lib.call(_entry("hsl_par_bwd", x), P(dout), P(dh_n), P(dc_n), P(x), P(c0), P(gates), P(c_ck),
                   P(w_ih), ctx.eps, P(dx), P(dw_ih), P(db_ih), P(dc0), P(ws), nbytes, T, B, D, H,
                   _lib.stream_of(x.device))
         return dx, None, dc0, dw_ih, None, db_ih, None, None, None

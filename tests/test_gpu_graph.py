@@ -40,6 +40,13 @@ def test_graph_replays_half_module_parallel(dev, dtype):
     _check_replays(dev, True, (64, 8, 32, 64), dtype)
 
 
+@pytest.mark.parametrize("parallel", [False, True])
+def test_graph_replays_f64_module(dev, parallel):
+    """An fp64 module (the *_f64 kernels, one launch per step in recurrent mode) replayed as
+    one graph: every replay equals an eager step."""
+    _check_replays(dev, parallel, (24, 4, 16, 32), torch.float64)
+
+
 def _check_replays(dev, parallel, shape, dtype=torch.float32):
     T, B, D, H = shape
     print(f"graph T={T} B={B} D={D} H={H} parallel={parallel} dtype={dtype}", flush=True)

@@ -336,7 +336,8 @@ def bench_cpu(args):
     res = {"value": round(T * B / med, 1), "unit": "timesteps·batch/s", "cores": cores,
            "kind": "port", "ms_per_step": round(med * 1e3, 2),
            "sample": f"configs[2] fwd+bwd (out.sum() loss), fp32, torch CPU restatement of "
-                     f"_torch.py, median of {n} full steps after 1 warm-up",
+                     f"_torch.py, median of {n} full steps after 1 warm-up; like _torch.py:162 it "
+                     f"always forms dx (a [T*B,4H]x[4H,D] product the GPU step skips, x being data)",
            "affinity_cores": affinity, "cpu_model": model, "cgroup_cpu_max": quota, "torch_parallel_info": pinfo}
     if not args.no_cpu_parallel:
         par = []

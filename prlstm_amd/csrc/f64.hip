@@ -4,9 +4,10 @@
 // its parallel functional is dtype-generic (_parallel.py:38-74).  This path computes
 // every value in fp64 with the same data layouts and C-ABI shapes as the fp32 entry
 // points (include/hsl.h), so the autograd functions only change the entry names.  It
-// is written for exactness, not speed (gradient checks, fp64 training): per-step
-// kernels with one thread per (batch row, unit), a tiled fp64 GEMM and one thread per
-// channel for the scans; every sum runs in a fixed order, so results are deterministic.
+// is written for exactness first (gradient checks, fp64 training): a register-blocked
+// fp64 GEMM for every product (the per-step h W_s^T and dg W_s included), per-step cell
+// kernels with one thread per (batch row, unit) and one thread per channel for the
+// scans; every sum runs in a fixed order, so results are deterministic.
 //
 //   recurrent (_torch.py:86-170): W_s = a (x) W_hh, b_s = a (x) b_hh; gih = x W_ih^T + b_ih;
 //     per step z = gih_t + b_s + h_{t-1} W_s^T, then the cell (_torch.py:27-36);
@@ -28,39 +29,147 @@ constexpr int kCk = 8;  // steps per checkpoint row of c (as the fp32 scan)
 __device__ __forceinline__ double sig64(double z) { return 1.0 / (1.0 + exp(-z)); }
 
 // C[m][n] = (bias ? bias[n] : 0) + sum_k A(m,k) B(k,n), A(m,k) = A[m*sam + k*sak],
-// B(k,n) = B[k*sbk + n*sbn], C row-major with ldc.  16x16 output tiles through LDS, k in
-// increasing order (one fma per k).
+// B(k,n) = B[k*sbk + n*sbn], C row-major with ldc.  64x64 output tiles, 256 threads of
+// 4x4 outputs each, 16-deep k-slices through LDS (loaded along whichever index is
+// contiguous in memory); every output adds its k terms in increasing order (one fma per k).
+// Split K: workgroup z covers k in [z*kc, min(K, (z+1)*kc)) and writes C + z*pst, so
+// each split leaves a partial product that a fixed-order sum adds afterwards.
 struct G64 {
   const double* A;
   const double* Bm;
   const double* bias;
   double* C;
   long long M, N, K, sam, sak, sbk, sbn, ldc;
+  long long kc = 0;   // k per split (a multiple of 16); 0 = all of K
+  long long pst = 0;  // distance between the splits' outputs
 };
 
 __global__ __launch_bounds__(256) void gemm_f64_kernel(G64 g) {
-  __shared__ double As[16][17];
-  __shared__ double Bs[16][17];
-  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-  const long long m = (long long)blockIdx.y * 16 + ty, n = (long long)blockIdx.x * 16 + tx;
-  double acc = 0.0;
-  for (long long k0 = 0; k0 < g.K; k0 += 16) {
-    const long long ka = k0 + tx, kb = k0 + ty;
-    As[ty][tx] = (m < g.M && ka < g.K) ? g.A[m * g.sam + ka * g.sak] : 0.0;
-    Bs[ty][tx] = (kb < g.K && n < g.N) ? g.Bm[kb * g.sbk + n * g.sbn] : 0.0;
+  __shared__ double As[16][65];  // [k][m]
+  __shared__ double Bs[16][65];  // [k][n]
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const long long m0 = (long long)blockIdx.y * 64, n0 = (long long)blockIdx.x * 64;
+  const long long kb0 = g.kc ? (long long)blockIdx.z * g.kc : 0;
+  const long long kend = g.kc ? min(g.K, kb0 + g.kc) : g.K;
+  double* C = g.C + (long long)blockIdx.z * g.pst;
+  const bool a_kc = g.sak == 1, b_nc = g.sbn == 1;  // which index is contiguous
+  double acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
+  for (long long k0 = kb0; k0 < kend; k0 += 16) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int e = tid + 256 * r;
+      const int am = a_kc ? e >> 4 : e & 63, ak = a_kc ? e & 15 : e >> 6;
+      const long long m = m0 + am, ka = k0 + ak;
+      As[ak][am] = (m < g.M && ka < kend) ? g.A[m * g.sam + ka * g.sak] : 0.0;
+      const int bn = b_nc ? e & 63 : e >> 4, bk = b_nc ? e >> 6 : e & 15;
+      const long long n = n0 + bn, kb = k0 + bk;
+      Bs[bk][bn] = (kb < kend && n < g.N) ? g.Bm[kb * g.sbk + n * g.sbn] : 0.0;
+    }
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < 16; ++k) acc = fma(As[ty][k], Bs[k][tx], acc);
+    for (int k = 0; k < 16; ++k) {
+      double av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = As[k][4 * ty + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = Bs[k][4 * tx + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fma(av[i], bv[j], acc[i][j]);
+    }
     __syncthreads();
   }
-  if (m < g.M && n < g.N) g.C[m * g.ldc + n] = (g.bias ? g.bias[n] : 0.0) + acc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const long long m = m0 + 4 * ty + i;
+    if (m >= g.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const long long n = n0 + 4 * tx + j;
+      if (n < g.N) C[m * g.ldc + n] = (g.bias ? g.bias[n] : 0.0) + acc[i][j];
+    }
+  }
+}
+
+// C[m][n] = (bias ? bias[n] : 0) + sum over s < S of part[s][m][n], in increasing s
+__global__ void sum_splits_f64(const double* part, const double* bias, double* C, long long M, long long N,
+                               long long ldc, int S) {
+  const long long MN = M * N;
+  for (long long e = blockIdx.x * 256ll + threadIdx.x; e < MN; e += (long long)gridDim.x * 256) {
+    const long long m = e / N, n = e % N;
+    double acc = 0.0;
+    for (int z = 0; z < S; ++z) acc += part[z * MN + e];
+    C[m * ldc + n] = (bias ? bias[n] : 0.0) + acc;
+  }
+}
+
+constexpr long long kFillBlocks = 1024;  // workgroups that keep every CU busy (4 per CU)
+constexpr long long kMinSplitK = 64;     // k per split at the least
+
+// Splits of K for an M x N x K product: enough workgroups to fill the chip when the
+// output alone has too few tiles, each split at least kMinSplitK deep.
+inline int split_of(long long M, long long N, long long K) {
+  const long long tiles = ((M + 63) / 64) * ((N + 63) / 64);
+  if (tiles <= 0 || tiles >= kFillBlocks || K <= kMinSplitK) return 1;
+  long long S = (kFillBlocks + tiles - 1) / tiles;
+  S = min(S, (K + kMinSplitK - 1) / kMinSplitK);
+  const long long kc = ((K + S - 1) / S + 15) / 16 * 16;
+  return (int)((K + kc - 1) / kc);
+}
+
+inline long long kc_of(long long K, int S) { return S > 1 ? ((K + S - 1) / S + 15) / 16 * 16 : 0; }
+
+// Doubles of partial products for gemm64 with S = split_of(M, N, K) (0 when unsplit).
+inline size_t part_elems(long long M, long long N, long long K) {
+  const int S = split_of(M, N, K);
+  return S > 1 ? (size_t)S * M * N : 0;
+}
+
+int launch_gemm(const G64& g, int S, hipStream_t s) {
+  const long long gy = (g.M + 63) / 64, gx = (g.N + 63) / 64;
+  if (gy > 65535 || gx > (1ll << 31) - 1) return fail(HSL_ERR_UNSUPPORTED, "fp64 GEMM: %lld rows", g.M);
+  hipLaunchKernelGGL(gemm_f64_kernel, dim3((unsigned)gx, (unsigned)gy, (unsigned)S), dim3(256), 0, s, g);
+  HSL_HIP(hipGetLastError());
+  return HSL_OK;
 }
 
 int gemm64(const G64& g, hipStream_t s) {
   if (g.M <= 0 || g.N <= 0) return HSL_OK;
-  const long long gy = (g.M + 15) / 16, gx = (g.N + 15) / 16;
-  if (gy > 65535 || gx > (1ll << 31) - 1) return fail(HSL_ERR_UNSUPPORTED, "fp64 GEMM: %lld rows", g.M);
-  hipLaunchKernelGGL(gemm_f64_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, s, g);
+  G64 u = g;
+  u.kc = 0;
+  u.pst = 0;
+  return launch_gemm(u, 1, s);
+}
+
+// The S = split_of(M, N, K) partial products into part[S][M][N] (nothing is summed);
+// returns S through *S_out.  S == 1 writes g.C directly (with g.bias).
+int gemm64_parts(const G64& g, double* part, int* S_out, hipStream_t s) {
+  const int S = split_of(g.M, g.N, g.K);
+  *S_out = S;
+  if (g.M <= 0 || g.N <= 0) return HSL_OK;
+  if (S == 1) return gemm64(g, s);
+  G64 p = g;
+  p.bias = nullptr;
+  p.C = part;
+  p.ldc = g.N;
+  p.kc = kc_of(g.K, S);
+  p.pst = g.M * g.N;
+  return launch_gemm(p, S, s);
+}
+
+// gemm64 with K split over part (part_elems(M, N, K) doubles) and the fixed-order sum.
+int gemm64_split(const G64& g, double* part, hipStream_t s) {
+  int S = 1;
+  HSL_CHECK(gemm64_parts(g, part, &S, s));
+  if (S == 1 || g.M <= 0 || g.N <= 0) return HSL_OK;
+  const long long MN = g.M * g.N;
+  const long long nb = min((MN + 255) / 256, 4096ll);
+  hipLaunchKernelGGL(sum_splits_f64, dim3((unsigned)nb), dim3(256), 0, s, part, g.bias, g.C, g.M, g.N, g.ldc, S);
   HSL_HIP(hipGetLastError());
   return HSL_OK;
 }
@@ -93,22 +202,22 @@ __global__ void scale_f64_kernel(const double* w_hh, const double* b_hh, const d
   }
 }
 
-// One forward step t: thread (b, u).  h_{t-1} = h_save[t], c_{t-1} = c_save[t].
-__global__ void rec_step_fwd_f64(const double* gih, const double* ws, const double* bs, double* h_save,
+// One forward step t, after the S split-K partials zb[S][B][4H] of h_{t-1} W_s^T
+// (gemm64_parts): thread (b, u) sums them in order, forms the four gates
+// (gih_t + h W_s^T) + b_s and runs the cell.  c_{t-1} = c_save[t].
+__global__ void rec_step_fwd_f64(const double* gih, const double* zb, int S, const double* bs, double* h_save,
                                  double* c_save, double* gact, double* tanh_c, int t, int B, int H) {
   const long long e = blockIdx.x * 256ll + threadIdx.x;
   if (e >= (long long)B * H) return;
   const int b = (int)(e / H), u = (int)(e % H);
   const long long plane = (long long)B * H;
-  const double* hp = h_save + t * plane + (long long)b * H;
   double z[4];
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const long long n = (long long)g * H + u;
-    double acc = 0.0;
-    const double* wr = ws + n * H;
-    for (int k = 0; k < H; ++k) acc = fma(hp[k], wr[k], acc);
-    z[g] = (gih[((long long)t * B + b) * 4 * H + n] + acc) + bs[n];
+    double hw = 0.0;
+    for (int z0 = 0; z0 < S; ++z0) hw += zb[((long long)z0 * B + b) * 4 * H + n];
+    z[g] = (gih[((long long)t * B + b) * 4 * H + n] + hw) + bs[n];
   }
   const double i = sig64(z[0]), f = sig64(z[1]), gg = sig64(z[2]), o = sig64(z[3]);
   const double c = f * c_save[t * plane + e] + i * gg;
@@ -123,18 +232,12 @@ __global__ void rec_step_fwd_f64(const double* gih, const double* ws, const doub
   tanh_c[t * plane + e] = tc;
 }
 
-// dh[b][u] = sum_n dg[b][n] W_s[n][u] over n < 4H, in increasing n
-__device__ __forceinline__ double dh_from_dg(const double* dg_bt, const double* ws, int u, int H) {
-  double acc = 0.0;
-  for (int n = 0; n < 4 * H; ++n) acc = fma(dg_bt[n], ws[(long long)n * H + u], acc);
-  return acc;
-}
-
-// One backward step t (T-1 down to 0): thread (b, u).  dh = (dh_n or dg_{t+1} W_s) +
-// dout_t; the cell backward with dc carried in dcb; writes dg_t.
+// One backward step t (T-1 down to 0): thread (b, u).  dh = (dh_n at T-1, else the
+// in-order sum of the S split-K partials dhb[S][B][H] of dg_{t+1} W_s) + dout_t; the
+// cell backward with dc carried in dcb; writes dg_t.
 __global__ void rec_step_bwd_f64(const double* dout, const double* dh_n, const double* dc_n, const double* c_save,
-                                 const double* gact, const double* tanh_c, const double* ws, double* dg, double* dcb,
-                                 int t, int T, int B, int H) {
+                                 const double* gact, const double* tanh_c, const double* dhb, int S, double* dg,
+                                 double* dcb, int t, int T, int B, int H) {
   const long long e = blockIdx.x * 256ll + threadIdx.x;
   if (e >= (long long)B * H) return;
   const int b = (int)(e / H), u = (int)(e % H);
@@ -145,7 +248,8 @@ __global__ void rec_step_bwd_f64(const double* dout, const double* dh_n, const d
     dh = dh_n ? dh_n[e] : 0.0;
     dc = dc_n ? dc_n[e] : 0.0;
   } else {
-    dh = dh_from_dg(dg + ((long long)(t + 1) * B + b) * row4, ws, u, H);
+    dh = 0.0;
+    for (int z0 = 0; z0 < S; ++z0) dh += dhb[z0 * plane + e];
     dc = dcb[e];
   }
   dh = dh + dout[t * plane + e];
@@ -165,23 +269,38 @@ __global__ void rec_step_bwd_f64(const double* dout, const double* dh_n, const d
   dcb[e] = dct * f;
 }
 
-// dh0 = dg_0 W_s, dc0 = the carried dc
-__global__ void rec_h0_grads_f64(const double* dg, const double* ws, const double* dcb, double* dh0, double* dc0,
-                                 int B, int H) {
-  const long long e = blockIdx.x * 256ll + threadIdx.x;
-  if (e >= (long long)B * H) return;
-  const int b = (int)(e / H), u = (int)(e % H);
-  if (dh0) dh0[e] = dh_from_dg(dg + (long long)b * 4 * H, ws, u, H);
-  if (dc0) dc0[e] = dcb[e];
+// Column sums db[n] = sum over rows r < R of dg[r][n], in two fixed-order levels:
+// colsum_part_f64 sums chunk z (rows [z*rc, min(R, (z+1)*rc)), increasing r) into
+// part[z][n], colsum_fin_f64 adds the chunks in increasing z.
+constexpr long long kColChunk = 256;
+
+inline int col_chunks(long long R) { return (int)max(1ll, (R + kColChunk - 1) / kColChunk); }
+
+__global__ void colsum_part_f64(const double* dg, double* part, long long R, int N) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  const long long r0 = (long long)blockIdx.y * kColChunk, r1 = min(R, r0 + kColChunk);
+  double acc = 0.0;
+  for (long long r = r0; r < r1; ++r) acc += dg[r * N + n];
+  part[(long long)blockIdx.y * N + n] = acc;
 }
 
-// db[n] = sum over rows r < R of dg[r][n], in increasing r
-__global__ void colsum_f64(const double* dg, double* db, long long R, int N) {
+__global__ void colsum_fin_f64(const double* part, double* db, int Z, int N) {
   const int n = blockIdx.x * 256 + threadIdx.x;
   if (n >= N) return;
   double acc = 0.0;
-  for (long long r = 0; r < R; ++r) acc += dg[r * N + n];
+  for (int z = 0; z < Z; ++z) acc += part[(long long)z * N + n];
   db[n] = acc;
+}
+
+int colsum64(const double* dg, double* part, double* db, long long R, int N, hipStream_t s) {
+  const int Z = col_chunks(R);
+  if (Z > 65535) return fail(HSL_ERR_UNSUPPORTED, "fp64 column sum: %lld rows", R);
+  hipLaunchKernelGGL(colsum_part_f64, dim3(blocks_for(N), (unsigned)Z), dim3(256), 0, s, dg, part, R, N);
+  HSL_HIP(hipGetLastError());
+  hipLaunchKernelGGL(colsum_fin_f64, dim3(blocks_for(N)), dim3(256), 0, s, part, db, Z, N);
+  HSL_HIP(hipGetLastError());
+  return HSL_OK;
 }
 
 // dW_hh = a dW_hh_s, db_ih = db, db_hh = a db; rowdot[n] = W_hh[n].dW_hh_s[n] + b_hh[n] db[n]
@@ -211,68 +330,108 @@ __global__ void rec_da_f64(const double* rowdot, double* da, int H) {
   da[g] = acc;
 }
 
-// Parallel forward scan, one thread per channel (b, j): c_t = max(f,eps) c + max(i g,eps),
-// out = o tanh(c); c_ck row m = the state carried into step 8m (row 0 = max(c0, eps)),
-// the last row c_{T-1}.
-__global__ void scan_fwd_f64(const double* gates, const double* c0, double eps, double* out, double* cck, int T,
-                             int B, int H) {
-  const long long ch = blockIdx.x * 256ll + threadIdx.x, C = (long long)B * H;
+// Parallel forward scan, one thread per channel (b, j), 64-thread workgroups so that the
+// channels spread over every CU: c_t = max(f,eps) c + max(i g,eps), out = o tanh(c);
+// c_ck row m = the state carried into step 8m (row 0 = max(c0, eps)), the last row
+// c_{T-1}.  Each 8-step group's gate loads are issued together before its serial chain.
+constexpr int kScanThreads = 64;
+
+__global__ __launch_bounds__(kScanThreads) void scan_fwd_f64(const double* gates, const double* c0, double eps,
+                                                             double* out, double* cck, int T, int B, int H) {
+  const long long ch = blockIdx.x * (long long)kScanThreads + threadIdx.x, C = (long long)B * H;
   if (ch >= C) return;
   const long long b = ch / H, j = ch % H, row4 = 4ll * H;
   double c = fmax(c0 ? c0[ch] : 0.0, eps);
-  for (int t = 0; t < T; ++t) {
-    if (t % kCk == 0) cck[(long long)(t / kCk) * C + ch] = c;
-    const double* z = gates + ((long long)t * B + b) * row4 + j;
-    const double f = fmax(sig64(z[H]), eps), bb = fmax(sig64(z[0]) * sig64(z[2 * H]), eps);
-    c = fma(f, c, bb);
-    out[(long long)t * C + ch] = sig64(z[3 * H]) * tanh(c);
+  for (int t0 = 0; t0 < T; t0 += kCk) {
+    cck[(long long)(t0 / kCk) * C + ch] = c;
+    const int n = min(kCk, T - t0);
+    double zi[kCk], zf[kCk], zg[kCk], zo[kCk];
+#pragma unroll
+    for (int k = 0; k < kCk; ++k) {
+      if (k < n) {
+        const double* z = gates + ((long long)(t0 + k) * B + b) * row4 + j;
+        zi[k] = z[0];
+        zf[k] = z[H];
+        zg[k] = z[2 * H];
+        zo[k] = z[3 * H];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kCk; ++k) {
+      if (k < n) {
+        const double f = fmax(sig64(zf[k]), eps), bb = fmax(sig64(zi[k]) * sig64(zg[k]), eps);
+        c = fma(f, c, bb);
+        out[(long long)(t0 + k) * C + ch] = sig64(zo[k]) * tanh(c);
+      }
+    }
   }
   cck[(long long)((T + kCk - 1) / kCk) * C + ch] = c;
 }
 
 // Parallel backward scan, one thread per channel: for each 8-step group from the last,
-// c is recomputed from the group's checkpoint row, then the group's steps run in
-// reverse: G_t = e_t + f~_{t+1} G_{t+1}, e_t = dout'_t o (1 - tanh^2 c_t) (+ dc_n at T-1),
-// df~ = G c_{t-1}, db~ = G, and the sigmoid / clamp chain gives dgates (the clamps pass
-// gradient where their input is >= eps); dc0 = G_0 f~_0 [c0 >= eps].
-__global__ void scan_bwd_f64(const double* gates, const double* c0, const double* cck, const double* dout,
-                             const double* dh_n, const double* dc_n, double eps, double* dgates, double* dc0, int T,
-                             int B, int H) {
-  const long long ch = blockIdx.x * 256ll + threadIdx.x, C = (long long)B * H;
+// the group's gates and dout are loaded together, c is recomputed from the group's
+// checkpoint row, then the group's steps run in reverse: G_t = e_t + f~_{t+1} G_{t+1},
+// e_t = dout'_t o (1 - tanh^2 c_t) (+ dc_n at T-1), df~ = G c_{t-1}, db~ = G, and the
+// sigmoid / clamp chain gives dgates (the clamps pass gradient where their input is
+// >= eps); dc0 = G_0 f~_0 [c0 >= eps].
+__global__ __launch_bounds__(kScanThreads) void scan_bwd_f64(const double* gates, const double* c0,
+                                                             const double* cck, const double* dout,
+                                                             const double* dh_n, const double* dc_n, double eps,
+                                                             double* dgates, double* dc0, int T, int B, int H) {
+  const long long ch = blockIdx.x * (long long)kScanThreads + threadIdx.x, C = (long long)B * H;
   if (ch >= C) return;
   const long long b = ch / H, j = ch % H, row4 = 4ll * H;
   double G = 0.0, fnext = 0.0;  // G_{t+1} and f~_{t+1} (0 past T-1)
   double first_f = 0.0;
   const int ngroups = (T + kCk - 1) / kCk;
   for (int m = ngroups - 1; m >= 0; --m) {
-    const int t0 = m * kCk, t1 = min(T, t0 + kCk);
+    const int t0 = m * kCk, n = min(kCk, T - t0);
+    double ig[kCk], fg[kCk], gg[kCk], og[kCk], dd[kCk];
+#pragma unroll
+    for (int k = 0; k < kCk; ++k) {
+      if (k < n) {
+        const double* z = gates + ((long long)(t0 + k) * B + b) * row4 + j;
+        ig[k] = z[0];
+        fg[k] = z[H];
+        gg[k] = z[2 * H];
+        og[k] = z[3 * H];
+        dd[k] = dout[(long long)(t0 + k) * C + ch];
+      }
+    }
     double cs[kCk + 1];
     cs[0] = cck[(long long)m * C + ch];  // c_{t0-1} (max(c0, eps) for m = 0)
-    for (int t = t0; t < t1; ++t) {
-      const double* z = gates + ((long long)t * B + b) * row4 + j;
-      const double f = fmax(sig64(z[H]), eps), bb = fmax(sig64(z[0]) * sig64(z[2 * H]), eps);
-      cs[t - t0 + 1] = fma(f, cs[t - t0], bb);
+#pragma unroll
+    for (int k = 0; k < kCk; ++k) {
+      if (k < n) {
+        ig[k] = sig64(ig[k]);
+        fg[k] = sig64(fg[k]);
+        gg[k] = sig64(gg[k]);
+        og[k] = sig64(og[k]);
+        cs[k + 1] = fma(fmax(fg[k], eps), cs[k], fmax(ig[k] * gg[k], eps));
+      }
     }
-    for (int t = t1 - 1; t >= t0; --t) {
-      const double* z = gates + ((long long)t * B + b) * row4 + j;
-      const double ig = sig64(z[0]), fg = sig64(z[H]), gg = sig64(z[2 * H]), og = sig64(z[3 * H]);
-      const double c = cs[t - t0 + 1], cprev = cs[t - t0], tc = tanh(c);
-      double d = dout[(long long)t * C + ch];
-      if (t == T - 1 && dh_n) d += dh_n[ch];
-      double e = d * og * (1.0 - tc * tc);
-      if (t == T - 1 && dc_n) e += dc_n[ch];
-      G = e + fnext * G;
-      const double bb = ig * gg;
-      const double dbb = bb >= eps ? G : 0.0;
-      const double dfp = fg >= eps ? (G * cprev) * fg * (1.0 - fg) : 0.0;
-      const double dbq = dbb * bb;
-      double* dq = dgates + ((long long)t * B + b) * row4 + j;
-      dq[0] = dbq * (1.0 - ig);
-      dq[H] = dfp;
-      dq[2 * H] = dbq * (1.0 - gg);
-      dq[3 * H] = (d * tc) * og * (1.0 - og);
-      fnext = fmax(fg, eps);
-      first_f = fnext;
+#pragma unroll
+    for (int k = kCk - 1; k >= 0; --k) {
+      if (k < n) {
+        const int t = t0 + k;
+        const double c = cs[k + 1], cprev = cs[k], tc = tanh(c);
+        double d = dd[k];
+        if (t == T - 1 && dh_n) d += dh_n[ch];
+        double e = d * og[k] * (1.0 - tc * tc);
+        if (t == T - 1 && dc_n) e += dc_n[ch];
+        G = e + fnext * G;
+        const double bb = ig[k] * gg[k];
+        const double dbb = bb >= eps ? G : 0.0;
+        const double dfp = fg[k] >= eps ? (G * cprev) * fg[k] * (1.0 - fg[k]) : 0.0;
+        const double dbq = dbb * bb;
+        double* dq = dgates + ((long long)t * B + b) * row4 + j;
+        dq[0] = dbq * (1.0 - ig[k]);
+        dq[H] = dfp;
+        dq[2 * H] = dbq * (1.0 - gg[k]);
+        dq[3 * H] = (d * tc) * og[k] * (1.0 - og[k]);
+        fnext = fmax(fg[k], eps);
+        first_f = fnext;
+      }
     }
   }
   if (dc0) {
@@ -285,23 +444,49 @@ struct RecF64Ws {
   double* ws;    // [4H][H] W_s
   double* bs;    // [4H]
   double* big;   // fwd: gih [T][B][4H]; bwd: dg [T][B][4H]
+  double* sb;    // split-K partials: fwd [S][B][4H] of h_{t-1} W_s^T, bwd [S][B][H] of dg_{t+1} W_s
+  double* part;  // split-K partials of the whole-sequence products, and the column sum's chunks
   double* dcb;   // [B][H]
   double* dws;   // [4H][H] dW_hh_s
   double* db;    // [4H]
   double* rowdot;  // [4H]
 };
 
-size_t carve_rec64(void* base, size_t cap, int T, int B, int H, bool bwd, RecF64Ws* o) {
+size_t carve_rec64(void* base, size_t cap, int T, int B, int D, int H, bool bwd, RecF64Ws* o) {
   Carver c(base, cap);
-  o->ws = c.take<double>((size_t)4 * H * H);
-  o->bs = c.take<double>((size_t)4 * H);
-  o->big = c.take<double>((size_t)T * B * 4 * H);
-  if (bwd) {
-    o->dcb = c.take<double>((size_t)B * H);
-    o->dws = c.take<double>((size_t)4 * H * H);
-    o->db = c.take<double>((size_t)4 * H);
-    o->rowdot = c.take<double>((size_t)4 * H);
+  const long long TB = (long long)T * B, N4 = 4ll * H;
+  o->ws = c.take<double>((size_t)N4 * H);
+  o->bs = c.take<double>((size_t)N4);
+  o->big = c.take<double>((size_t)TB * N4);
+  if (!bwd) {
+    o->sb = c.take<double>(max(part_elems(B, N4, H), (size_t)B * N4));  // S == 1 writes [B][4H]
+    o->part = c.take<double>(part_elems(TB, N4, D));
+    return c.off;
   }
+  o->sb = c.take<double>(max(part_elems(B, H, N4), (size_t)B * H));  // S == 1 writes [B][H]
+  size_t np = max(part_elems(N4, H, TB), part_elems(N4, D, TB));
+  np = max(np, part_elems(TB, D, N4));
+  np = max(np, (size_t)col_chunks(TB) * N4);
+  o->part = c.take<double>(np);
+  o->dcb = c.take<double>((size_t)B * H);
+  o->dws = c.take<double>((size_t)N4 * H);
+  o->db = c.take<double>((size_t)N4);
+  o->rowdot = c.take<double>((size_t)N4);
+  return c.off;
+}
+
+struct ParF64Ws {
+  double* dg;    // [T][B][4H]
+  double* part;  // split-K partials and the column sum's chunks
+};
+
+size_t carve_par64(void* base, size_t cap, int T, int B, int D, int H, ParF64Ws* o) {
+  Carver c(base, cap);
+  const long long TB = (long long)T * B, N4 = 4ll * H;
+  o->dg = c.take<double>((size_t)TB * N4);
+  size_t np = max(part_elems(N4, D, TB), part_elems(TB, D, N4));
+  np = max(np, (size_t)col_chunks(TB) * N4);
+  o->part = c.take<double>(np);
   return c.off;
 }
 
@@ -315,7 +500,7 @@ extern "C" {
 size_t hsl_rec_fwd_f64_ws_bytes(int T, int B, int D, int H) {
   if (T < 0 || B < 0 || D < 0 || H < 0) return 0;
   RecF64Ws w;
-  return carve_rec64(nullptr, 0, T, B, H, false, &w);
+  return carve_rec64(nullptr, 0, T, B, D, H, false, &w);
 }
 
 int hsl_rec_fwd_f64(const double* x, const double* h0, const double* c0, const double* w_ih, const double* w_hh,
@@ -328,7 +513,7 @@ int hsl_rec_fwd_f64(const double* x, const double* h0, const double* c0, const d
   if (!w_hh || !a || !h_save || !c_save || (T > 0 && (!x || !w_ih || !b_ih || !gact || !tanh_c)))
     return fail(HSL_ERR_ARG, "hsl_rec_fwd_f64: null pointer");
   RecF64Ws w;
-  const size_t need = carve_rec64(ws, ws_bytes, T, B, H, false, &w);
+  const size_t need = carve_rec64(ws, ws_bytes, T, B, D, H, false, &w);
   if (!ws || ws_bytes < need) return fail(HSL_ERR_ARG, "hsl_rec_fwd_f64: workspace %zu bytes, need %zu", ws_bytes, need);
   const size_t plane = (size_t)B * H;
   HSL_CHECK(copy64(h_save, h0, (long long)plane, s));
@@ -338,9 +523,13 @@ int hsl_rec_fwd_f64(const double* x, const double* h0, const double* c0, const d
                      dim3(256), 0, s, w_hh, b_hh, a, w.ws, w.bs, H);
   HSL_HIP(hipGetLastError());
   // gih = x W_ih^T + b_ih
-  HSL_CHECK(gemm64(G64{x, w_ih, b_ih, w.big, (long long)T * B, 4ll * H, D, D, 1, 1, D, 4ll * H}, s));
+  HSL_CHECK(gemm64_split(G64{x, w_ih, b_ih, w.big, (long long)T * B, 4ll * H, D, D, 1, 1, D, 4ll * H}, w.part, s));
   for (int t = 0; t < T; ++t) {
-    hipLaunchKernelGGL(rec_step_fwd_f64, dim3(blocks_for((long long)B * H)), dim3(256), 0, s, w.big, w.ws, w.bs,
+    // sb = the S split-K partials of h_{t-1} W_s^T  [S][B][4H]
+    int S = 1;
+    HSL_CHECK(gemm64_parts(G64{h_save + (size_t)t * plane, w.ws, nullptr, w.sb, B, 4ll * H, H, H, 1, 1, H, 4ll * H},
+                           w.sb, &S, s));
+    hipLaunchKernelGGL(rec_step_fwd_f64, dim3(blocks_for((long long)B * H)), dim3(256), 0, s, w.big, w.sb, S, w.bs,
                        h_save, c_save, gact, tanh_c, t, B, H);
     HSL_HIP(hipGetLastError());
   }
@@ -350,7 +539,7 @@ int hsl_rec_fwd_f64(const double* x, const double* h0, const double* c0, const d
 size_t hsl_rec_bwd_f64_ws_bytes(int T, int B, int D, int H) {
   if (T < 0 || B < 0 || D < 0 || H < 0) return 0;
   RecF64Ws w;
-  return carve_rec64(nullptr, 0, T, B, H, true, &w);
+  return carve_rec64(nullptr, 0, T, B, D, H, true, &w);
 }
 
 int hsl_rec_bwd_f64(const double* dout, const double* dh_n, const double* dc_n, const double* x,
@@ -366,7 +555,7 @@ int hsl_rec_bwd_f64(const double* dout, const double* dh_n, const double* dc_n, 
   if (T > 0 && B > 0 && (!dout || !x || !h_save || !c_save || !gact || !tanh_c))
     return fail(HSL_ERR_ARG, "hsl_rec_bwd_f64: null pointer");
   RecF64Ws w;
-  const size_t need = carve_rec64(ws, ws_bytes, T, B, H, true, &w);
+  const size_t need = carve_rec64(ws, ws_bytes, T, B, D, H, true, &w);
   if (!ws || ws_bytes < need) return fail(HSL_ERR_ARG, "hsl_rec_bwd_f64: workspace %zu bytes, need %zu", ws_bytes, need);
   const size_t plane = (size_t)B * H;
   if (T == 0 || B == 0) {  // no steps: zero gradients, dh0 = dh_n and dc0 = dc_n
@@ -382,23 +571,25 @@ int hsl_rec_bwd_f64(const double* dout, const double* dh_n, const double* dc_n, 
   hipLaunchKernelGGL(scale_f64_kernel, dim3(blocks_for(4ll * H * H) < 4096 ? blocks_for(4ll * H * H) : 4096),
                      dim3(256), 0, s, w_hh, b_hh, a, w.ws, w.bs, H);
   HSL_HIP(hipGetLastError());
-  for (int t = T - 1; t >= 0; --t) {
-    hipLaunchKernelGGL(rec_step_bwd_f64, dim3(blocks_for((long long)plane)), dim3(256), 0, s, dout, dh_n, dc_n,
-                       c_save, gact, tanh_c, w.ws, w.big, w.dcb, t, T, B, H);
-    HSL_HIP(hipGetLastError());
-  }
-  if (dh0 || dc0) {
-    hipLaunchKernelGGL(rec_h0_grads_f64, dim3(blocks_for((long long)plane)), dim3(256), 0, s, w.big, w.ws, w.dcb,
-                       dh0, dc0, B, H);
-    HSL_HIP(hipGetLastError());
-  }
   const long long TB = (long long)T * B, N4 = 4ll * H;
+  for (int t = T - 1; t >= 0; --t) {
+    // sb = the S split-K partials of dg_{t+1} W_s  [S][B][H]
+    int S = 1;
+    if (t < T - 1)
+      HSL_CHECK(gemm64_parts(G64{w.big + (size_t)(t + 1) * B * N4, w.ws, nullptr, w.sb, B, H, N4, N4, 1, H, 1, H},
+                             w.sb, &S, s));
+    hipLaunchKernelGGL(rec_step_bwd_f64, dim3(blocks_for((long long)plane)), dim3(256), 0, s, dout, dh_n, dc_n,
+                       c_save, gact, tanh_c, w.sb, S, w.big, w.dcb, t, T, B, H);
+    HSL_HIP(hipGetLastError());
+  }
+  // dh0 = dg_0 W_s, dc0 = the carried dc
+  if (dh0) HSL_CHECK(gemm64_split(G64{w.big, w.ws, nullptr, dh0, B, H, N4, N4, 1, H, 1, H}, w.sb, s));
+  if (dc0) HSL_CHECK(copy64(dc0, w.dcb, (long long)plane, s));
   // dW_hh_s = dg^T h_prev (h_prev = h_save[0 .. T-1]), dW_ih = dg^T x, dx = dg W_ih
-  HSL_CHECK(gemm64(G64{w.big, h_save, nullptr, w.dws, N4, H, TB, 1, N4, H, 1, H}, s));
-  HSL_CHECK(gemm64(G64{w.big, x, nullptr, dw_ih, N4, D, TB, 1, N4, D, 1, D}, s));
-  if (dx) HSL_CHECK(gemm64(G64{w.big, w_ih, nullptr, dx, TB, D, N4, N4, 1, D, 1, D}, s));
-  hipLaunchKernelGGL(colsum_f64, dim3(blocks_for(N4)), dim3(256), 0, s, w.big, w.db, TB, (int)N4);
-  HSL_HIP(hipGetLastError());
+  HSL_CHECK(gemm64_split(G64{w.big, h_save, nullptr, w.dws, N4, H, TB, 1, N4, H, 1, H}, w.part, s));
+  HSL_CHECK(gemm64_split(G64{w.big, x, nullptr, dw_ih, N4, D, TB, 1, N4, D, 1, D}, w.part, s));
+  if (dx) HSL_CHECK(gemm64_split(G64{w.big, w_ih, nullptr, dx, TB, D, N4, N4, 1, D, 1, D}, w.part, s));
+  HSL_CHECK(colsum64(w.big, w.part, w.db, TB, (int)N4, s));
   hipLaunchKernelGGL(rec_final_rows_f64, dim3(blocks_for(N4)), dim3(256), 0, s, w_hh, b_hh, a, w.dws, w.db, dw_hh,
                      db_ih, db_hh, w.rowdot, H);
   HSL_HIP(hipGetLastError());
@@ -414,17 +605,17 @@ int hsl_par_fwd_f64(const double* x, const double* c0, const double* w_ih, const
   if (T == 0 || B == 0 || H == 0) return HSL_OK;
   if (!x || !w_ih || !b_ih || !gates || !out || !c_ck) return fail(HSL_ERR_ARG, "hsl_par_fwd_f64: null pointer");
   HSL_CHECK(gemm64(G64{x, w_ih, b_ih, gates, (long long)T * B, 4ll * H, D, D, 1, 1, D, 4ll * H}, s));
-  hipLaunchKernelGGL(scan_fwd_f64, dim3(blocks_for((long long)B * H)), dim3(256), 0, s, gates, c0, eps, out, c_ck, T,
-                     B, H);
+  const long long C = (long long)B * H;
+  hipLaunchKernelGGL(scan_fwd_f64, dim3((unsigned)((C + kScanThreads - 1) / kScanThreads)), dim3(kScanThreads), 0, s,
+                     gates, c0, eps, out, c_ck, T, B, H);
   HSL_HIP(hipGetLastError());
   return HSL_OK;
 }
 
 size_t hsl_par_bwd_f64_ws_bytes(int T, int B, int D, int H) {
   if (T < 0 || B < 0 || D < 0 || H < 0) return 0;
-  Carver c(nullptr, 0);
-  c.take<double>((size_t)T * B * 4 * H);
-  return c.off;
+  ParF64Ws w;
+  return carve_par64(nullptr, 0, T, B, D, H, &w);
 }
 
 int hsl_par_bwd_f64(const double* dout, const double* dh_n, const double* dc_n, const double* x, const double* c0,
@@ -435,9 +626,10 @@ int hsl_par_bwd_f64(const double* dout, const double* dh_n, const double* dc_n, 
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (H == 0) return HSL_OK;
   if (!dw_ih || !db_ih || !w_ih) return fail(HSL_ERR_ARG, "hsl_par_bwd_f64: null pointer");
-  Carver cv(ws, ws_bytes);
-  double* dg = cv.take<double>((size_t)T * B * 4 * H);
-  if (!ws || ws_bytes < cv.off) return fail(HSL_ERR_ARG, "hsl_par_bwd_f64: workspace %zu bytes, need %zu", ws_bytes, cv.off);
+  ParF64Ws w;
+  const size_t need = carve_par64(ws, ws_bytes, T, B, D, H, &w);
+  if (!ws || ws_bytes < need) return fail(HSL_ERR_ARG, "hsl_par_bwd_f64: workspace %zu bytes, need %zu", ws_bytes, need);
+  double* dg = w.dg;
   if (T == 0 || B == 0) {
     HSL_CHECK(copy64(dw_ih, nullptr, 4ll * H * D, s));
     HSL_CHECK(copy64(db_ih, nullptr, 4ll * H, s));
@@ -445,14 +637,14 @@ int hsl_par_bwd_f64(const double* dout, const double* dh_n, const double* dc_n, 
     return HSL_OK;
   }
   if (!dout || !x || !gates || !c_ck) return fail(HSL_ERR_ARG, "hsl_par_bwd_f64: null pointer");
-  hipLaunchKernelGGL(scan_bwd_f64, dim3(blocks_for((long long)B * H)), dim3(256), 0, s, gates, c0, c_ck, dout, dh_n,
-                     dc_n, eps, dg, dc0, T, B, H);
+  const long long C = (long long)B * H;
+  hipLaunchKernelGGL(scan_bwd_f64, dim3((unsigned)((C + kScanThreads - 1) / kScanThreads)), dim3(kScanThreads), 0, s,
+                     gates, c0, c_ck, dout, dh_n, dc_n, eps, dg, dc0, T, B, H);
   HSL_HIP(hipGetLastError());
   const long long TB = (long long)T * B, N4 = 4ll * H;
-  HSL_CHECK(gemm64(G64{dg, x, nullptr, dw_ih, N4, D, TB, 1, N4, D, 1, D}, s));
-  if (dx) HSL_CHECK(gemm64(G64{dg, w_ih, nullptr, dx, TB, D, N4, N4, 1, D, 1, D}, s));
-  hipLaunchKernelGGL(colsum_f64, dim3(blocks_for(N4)), dim3(256), 0, s, dg, db_ih, TB, (int)N4);
-  HSL_HIP(hipGetLastError());
+  HSL_CHECK(gemm64_split(G64{dg, x, nullptr, dw_ih, N4, D, TB, 1, N4, D, 1, D}, w.part, s));
+  if (dx) HSL_CHECK(gemm64_split(G64{dg, w_ih, nullptr, dx, TB, D, N4, N4, 1, D, 1, D}, w.part, s));
+  HSL_CHECK(colsum64(dg, w.part, db_ih, TB, (int)N4, s));
   return HSL_OK;
 }
 

@@ -29,9 +29,10 @@ constexpr int kCk = 8;  // steps per checkpoint row of c (as the fp32 scan)
 __device__ __forceinline__ double sig64(double z) { return 1.0 / (1.0 + exp(-z)); }
 
 // C[m][n] = (bias ? bias[n] : 0) + sum_k A(m,k) B(k,n), A(m,k) = A[m*sam + k*sak],
-// B(k,n) = B[k*sbk + n*sbn], C row-major with ldc.  64x64 output tiles, 256 threads of
-// 4x4 outputs each, 16-deep k-slices through LDS (loaded along whichever index is
-// contiguous in memory); every output adds its k terms in increasing order (one fma per k).
+// B(k,n) = B[k*sbk + n*sbn], C row-major with ldc.  64x64 output tiles on 4 waves (a 32x32
+// quarter each, 2x2 blocks of the fp64 matrix instruction 16x16x4), 16-deep k-slices
+// through LDS (loaded along whichever index is contiguous in memory); every output takes
+// its k terms in increasing order, four per instruction.
 // Split K: workgroup z covers k in [z*kc, min(K, (z+1)*kc)) and writes C + z*pst, so
 // each split leaves a partial product that a fixed-order sum adds afterwards.
 struct G64 {
@@ -44,20 +45,23 @@ struct G64 {
   long long pst = 0;  // distance between the splits' outputs
 };
 
+typedef double d4_t __attribute__((ext_vector_type(4)));
+
 __global__ __launch_bounds__(256) void gemm_f64_kernel(G64 g) {
   __shared__ double As[16][65];  // [k][m]
   __shared__ double Bs[16][65];  // [k][n]
-  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wm = (wv >> 1) * 32, wn = (wv & 1) * 32;  // this wave's 32x32 quarter of the tile
   const long long m0 = (long long)blockIdx.y * 64, n0 = (long long)blockIdx.x * 64;
   const long long kb0 = g.kc ? (long long)blockIdx.z * g.kc : 0;
   const long long kend = g.kc ? min(g.K, kb0 + g.kc) : g.K;
   double* C = g.C + (long long)blockIdx.z * g.pst;
   const bool a_kc = g.sak == 1, b_nc = g.sbn == 1;  // which index is contiguous
-  double acc[4][4];
+  d4_t acc[2][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
+    for (int j = 0; j < 2; ++j) acc[i][j] = d4_t{0.0, 0.0, 0.0, 0.0};
   for (long long k0 = kb0; k0 < kend; k0 += 16) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -70,30 +74,29 @@ __global__ __launch_bounds__(256) void gemm_f64_kernel(G64 g) {
       Bs[bk][bn] = (kb < kend && n < g.N) ? g.Bm[kb * g.sbk + n * g.sbn] : 0.0;
     }
     __syncthreads();
+    // v_mfma_f64_16x16x4: lane l holds A[l%16][l/16] and B[l/16][l%16] of a 16x16x4 step
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      double av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = As[k][4 * ty + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = Bs[k][4 * tx + j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fma(av[i], bv[j], acc[i][j]);
+    for (int kk = 0; kk < 4; ++kk) {
+      const int kr = 4 * kk + (lane >> 4), c = lane & 15;
+      const double a0 = As[kr][wm + c], a1 = As[kr][wm + 16 + c];
+      const double b0 = Bs[kr][wn + c], b1 = Bs[kr][wn + 16 + c];
+      acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
     }
     __syncthreads();
   }
+  // result element i of a lane: row l/16 + 4i, column l%16 of the 16x16 block
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const long long m = m0 + 4 * ty + i;
-    if (m >= g.M) continue;
+  for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const long long n = n0 + 4 * tx + j;
-      if (n < g.N) C[m * g.ldc + n] = (g.bias ? g.bias[n] : 0.0) + acc[i][j];
-    }
-  }
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const long long m = m0 + wm + 16 * bi + (lane >> 4) + 4 * i, n = n0 + wn + 16 * bj + (lane & 15);
+        if (m < g.M && n < g.N) C[m * g.ldc + n] = (g.bias ? g.bias[n] : 0.0) + acc[bi][bj][i];
+      }
 }
 
 // C[m][n] = (bias ? bias[n] : 0) + sum over s < S of part[s][m][n], in increasing s
@@ -215,8 +218,18 @@ __global__ void rec_step_fwd_f64(const double* gih, const double* zb, int S, con
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const long long n = (long long)g * H + u;
+    const double* zp = zb + (long long)b * 4 * H + n;
+    const long long zs = (long long)B * 4 * H;
     double hw = 0.0;
-    for (int z0 = 0; z0 < S; ++z0) hw += zb[((long long)z0 * B + b) * 4 * H + n];
+    int z0 = 0;
+    for (; z0 + 8 <= S; z0 += 8) {  // loads issued together, added in order
+      double v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = zp[(z0 + q) * zs];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) hw += v[q];
+    }
+    for (; z0 < S; ++z0) hw += zp[z0 * zs];
     z[g] = (gih[((long long)t * B + b) * 4 * H + n] + hw) + bs[n];
   }
   const double i = sig64(z[0]), f = sig64(z[1]), gg = sig64(z[2]), o = sig64(z[3]);
@@ -249,7 +262,15 @@ __global__ void rec_step_bwd_f64(const double* dout, const double* dh_n, const d
     dc = dc_n ? dc_n[e] : 0.0;
   } else {
     dh = 0.0;
-    for (int z0 = 0; z0 < S; ++z0) dh += dhb[z0 * plane + e];
+    int z0 = 0;
+    for (; z0 + 8 <= S; z0 += 8) {  // loads issued together, added in order
+      double v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = dhb[(z0 + q) * plane + e];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) dh += v[q];
+    }
+    for (; z0 < S; ++z0) dh += dhb[z0 * plane + e];
     dc = dcb[e];
   }
   dh = dh + dout[t * plane + e];

@@ -4,10 +4,10 @@
 // its parallel functional is dtype-generic (_parallel.py:38-74).  This path computes
 // every value in fp64 with the same data layouts and C-ABI shapes as the fp32 entry
 // points (include/hsl.h), so the autograd functions only change the entry names.  It
-// is written for exactness first (gradient checks, fp64 training): a register-blocked
-// fp64 GEMM for every product (the per-step h W_s^T and dg W_s included), per-step cell
-// kernels with one thread per (batch row, unit) and one thread per channel for the
-// scans; every sum runs in a fixed order, so results are deterministic.
+// is written for exactness first (gradient checks, fp64 training): an fp64 GEMM on the
+// fp64 matrix instruction for every product (the per-step h W_s^T and dg W_s included),
+// per-step cell kernels with one thread per (batch row, unit) and one thread per channel
+// for the scans; every sum runs in a fixed order, so results are deterministic.
 //
 //   recurrent (_torch.py:86-170): W_s = a (x) W_hh, b_s = a (x) b_hh; gih = x W_ih^T + b_ih;
 //     per step z = gih_t + b_s + h_{t-1} W_s^T, then the cell (_torch.py:27-36);
@@ -32,7 +32,7 @@ __device__ __forceinline__ double sig64(double z) { return 1.0 / (1.0 + exp(-z))
 // B(k,n) = B[k*sbk + n*sbn], C row-major with ldc.  64x64 output tiles on 4 waves (a 32x32
 // quarter each, 2x2 blocks of the fp64 matrix instruction 16x16x4), 16-deep k-slices
 // through LDS (loaded along whichever index is contiguous in memory); every output takes
-// its k terms in increasing order, four per instruction.
+// its k terms in increasing groups of four, one instruction per group.
 // Split K: workgroup z covers k in [z*kc, min(K, (z+1)*kc)) and writes C + z*pst, so
 // each split leaves a partial product that a fixed-order sum adds afterwards.
 struct G64 {

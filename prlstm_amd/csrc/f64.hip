@@ -351,30 +351,42 @@ __global__ void rec_da_f64(const double* rowdot, double* da, int H) {
   da[g] = acc;
 }
 
-// Parallel forward scan, one thread per channel (b, j), 64-thread workgroups so that the
-// channels spread over every CU: c_t = max(f,eps) c + max(i g,eps), out = o tanh(c);
-// c_ck row m = the state carried into step 8m (row 0 = max(c0, eps)), the last row
-// c_{T-1}.  Each 8-step group's gate loads are issued together before its serial chain.
+// Parallel-mode scans, one thread per (channel, time chunk).  T is cut into P chunks of L
+// steps (L a multiple of the 8-step checkpoint group), so that channels x chunks fill the
+// chip; 64-thread workgroups spread them over every CU.  Each chunk's 8-step groups issue
+// their loads together before the serial chain.  The recurrences are affine, so a chunk
+// composes to one affine map: pass 1 composes every chunk, pass 2 carries the state across
+// the chunks of a channel, pass 3 reruns each chunk from its carried state and writes.
 constexpr int kScanThreads = 64;
+constexpr long long kScanLanes = 262144;  // channels x chunks that fill the chip
 
-__global__ __launch_bounds__(kScanThreads) void scan_fwd_f64(const double* gates, const double* c0, double eps,
-                                                             double* out, double* cck, int T, int B, int H) {
-  const long long ch = blockIdx.x * (long long)kScanThreads + threadIdx.x, C = (long long)B * H;
-  if (ch >= C) return;
-  const long long b = ch / H, j = ch % H, row4 = 4ll * H;
-  double c = fmax(c0 ? c0[ch] : 0.0, eps);
-  for (int t0 = 0; t0 < T; t0 += kCk) {
-    cck[(long long)(t0 / kCk) * C + ch] = c;
-    const int n = min(kCk, T - t0);
+// Chunk length L (steps) of T: P = ceil(T / L) chunks.
+inline int scan_chunk_len(int T, long long C) {
+  const long long want = max(1ll, (kScanLanes + C - 1) / C);
+  return (int)max(8ll, ((T + want - 1) / want + 7) / 8 * 8);
+}
+
+inline int scan_chunks(int T, int L) { return T > 0 ? (T + L - 1) / L : 0; }
+
+// The forward of steps [t0, t1) of channel ch from state c: c_t = max(f,eps) c + max(i g,eps).
+// kWrite: out = o tanh(c), the checkpoint row at every group start (and the last row at
+// T-1); else only the composed map c_out = A c_in + Bc (A, Bc accumulated in place).
+template <bool kWrite>
+__device__ __forceinline__ void fwd_chunk(const double* gates, double eps, double* out, double* cck, int t0, int t1,
+                                          int T, int B, int H, long long ch, double& c, double& A) {
+  const long long C = (long long)B * H, b = ch / H, j = ch % H, row4 = 4ll * H;
+  for (int g0 = t0; g0 < t1; g0 += kCk) {
+    if (kWrite) cck[(long long)(g0 / kCk) * C + ch] = c;
+    const int n = min(kCk, t1 - g0);
     double zi[kCk], zf[kCk], zg[kCk], zo[kCk];
 #pragma unroll
     for (int k = 0; k < kCk; ++k) {
       if (k < n) {
-        const double* z = gates + ((long long)(t0 + k) * B + b) * row4 + j;
+        const double* z = gates + ((long long)(g0 + k) * B + b) * row4 + j;
         zi[k] = z[0];
         zf[k] = z[H];
         zg[k] = z[2 * H];
-        zo[k] = z[3 * H];
+        if (kWrite) zo[k] = z[3 * H];
       }
     }
 #pragma unroll
@@ -382,45 +394,83 @@ __global__ __launch_bounds__(kScanThreads) void scan_fwd_f64(const double* gates
       if (k < n) {
         const double f = fmax(sig64(zf[k]), eps), bb = fmax(sig64(zi[k]) * sig64(zg[k]), eps);
         c = fma(f, c, bb);
-        out[(long long)(t0 + k) * C + ch] = sig64(zo[k]) * tanh(c);
+        if (kWrite) {
+          out[(long long)(g0 + k) * C + ch] = sig64(zo[k]) * tanh(c);
+        } else {
+          A *= f;
+        }
       }
     }
   }
-  cck[(long long)((T + kCk - 1) / kCk) * C + ch] = c;
+  if (kWrite && t1 == T) cck[(long long)((T + kCk - 1) / kCk) * C + ch] = c;
 }
 
-// Parallel backward scan, one thread per channel: for each 8-step group from the last,
-// the group's gates and dout are loaded together, c is recomputed from the group's
-// checkpoint row, then the group's steps run in reverse: G_t = e_t + f~_{t+1} G_{t+1},
-// e_t = dout'_t o (1 - tanh^2 c_t) (+ dc_n at T-1), df~ = G c_{t-1}, db~ = G, and the
-// sigmoid / clamp chain gives dgates (the clamps pass gradient where their input is
-// >= eps); dc0 = G_0 f~_0 [c0 >= eps].
-__global__ __launch_bounds__(kScanThreads) void scan_bwd_f64(const double* gates, const double* c0,
-                                                             const double* cck, const double* dout,
-                                                             const double* dh_n, const double* dc_n, double eps,
-                                                             double* dgates, double* dc0, int T, int B, int H) {
+// Pass 1: chunk p < P-1 of every channel composes to c_out = A c_in + Bc, kept in rows p
+// (A) and P + p (Bc) of out, which pass 3 overwrites.
+__global__ __launch_bounds__(kScanThreads) void scan_fwd_compose_f64(const double* gates, double eps, double* out,
+                                                                     int T, int B, int H, int L, int P) {
+  const long long ch = blockIdx.x * (long long)kScanThreads + threadIdx.x, C = (long long)B * H;
+  const int p = blockIdx.y;
+  if (ch >= C || p >= P - 1) return;
+  double c = 0.0, A = 1.0;
+  fwd_chunk<false>(gates, eps, nullptr, nullptr, p * L, min(T, (p + 1) * L), T, B, H, ch, c, A);
+  out[(long long)p * C + ch] = A;
+  out[(long long)(P + p) * C + ch] = c;
+}
+
+// Pass 2: c entering chunk p, written to the checkpoint row of step p*L.
+__global__ __launch_bounds__(kScanThreads) void scan_fwd_carry_f64(const double* c0, double eps, const double* out,
+                                                                   double* cck, int B, int H, int L, int P) {
   const long long ch = blockIdx.x * (long long)kScanThreads + threadIdx.x, C = (long long)B * H;
   if (ch >= C) return;
-  const long long b = ch / H, j = ch % H, row4 = 4ll * H;
-  double G = 0.0, fnext = 0.0;  // G_{t+1} and f~_{t+1} (0 past T-1)
-  double first_f = 0.0;
-  const int ngroups = (T + kCk - 1) / kCk;
-  for (int m = ngroups - 1; m >= 0; --m) {
-    const int t0 = m * kCk, n = min(kCk, T - t0);
+  double c = fmax(c0 ? c0[ch] : 0.0, eps);
+  for (int p = 0; p + 1 < P; ++p) {
+    c = fma(out[(long long)p * C + ch], c, out[(long long)(P + p) * C + ch]);
+    cck[(long long)((p + 1) * L / kCk) * C + ch] = c;
+  }
+}
+
+// Pass 3 (the whole scan when P = 1): out and the checkpoint rows of chunk p.  c_ck row m
+// = the state carried into step 8m (row 0 = max(c0, eps)), the last row c_{T-1}.
+__global__ __launch_bounds__(kScanThreads) void scan_fwd_f64(const double* gates, const double* c0, double eps,
+                                                             double* out, double* cck, int T, int B, int H, int L) {
+  const long long ch = blockIdx.x * (long long)kScanThreads + threadIdx.x, C = (long long)B * H;
+  if (ch >= C) return;
+  const int p = blockIdx.y;
+  double c = p == 0 ? fmax(c0 ? c0[ch] : 0.0, eps) : cck[(long long)(p * L / kCk) * C + ch];
+  double A = 1.0;
+  fwd_chunk<true>(gates, eps, out, cck, p * L, min(T, (p + 1) * L), T, B, H, ch, c, A);
+}
+
+// The backward of steps [t0, t1) of channel ch, from the last step down.  The carried
+// value is K = f~_{t+1} G_{t+1} (G_t = e_t + K), e_t = dout'_t o (1 - tanh^2 c_t)
+// (+ dc_n at T-1) with dout' = dout (+ dh_n at T-1); c is recomputed per 8-step group
+// from its checkpoint row.  kWrite: dgates from df~ = G c_{t-1}, db~ = G and the sigmoid
+// / clamp chain (the clamps pass gradient where their input is >= eps); else only the
+// composed map K_out = Fa K_in + K (Fa accumulated in place).  Ends with K = f~_{t0} G_{t0}
+// and G = G_{t0}.
+template <bool kWrite>
+__device__ __forceinline__ void bwd_chunk(const double* gates, const double* cck, const double* dout,
+                                          const double* dh_n, const double* dc_n, double eps, double* dgates, int t0,
+                                          int t1, int T, int B, int H, long long ch, double& K, double& G,
+                                          double& Fa) {
+  const long long C = (long long)B * H, b = ch / H, j = ch % H, row4 = 4ll * H;
+  for (int m = (t1 - 1) / kCk; m >= t0 / kCk; --m) {
+    const int g0 = m * kCk, n = min(kCk, T - g0);
     double ig[kCk], fg[kCk], gg[kCk], og[kCk], dd[kCk];
 #pragma unroll
     for (int k = 0; k < kCk; ++k) {
       if (k < n) {
-        const double* z = gates + ((long long)(t0 + k) * B + b) * row4 + j;
+        const double* z = gates + ((long long)(g0 + k) * B + b) * row4 + j;
         ig[k] = z[0];
         fg[k] = z[H];
         gg[k] = z[2 * H];
         og[k] = z[3 * H];
-        dd[k] = dout[(long long)(t0 + k) * C + ch];
+        dd[k] = dout[(long long)(g0 + k) * C + ch];
       }
     }
     double cs[kCk + 1];
-    cs[0] = cck[(long long)m * C + ch];  // c_{t0-1} (max(c0, eps) for m = 0)
+    cs[0] = cck[(long long)m * C + ch];  // c_{g0-1} (max(c0, eps) for m = 0)
 #pragma unroll
     for (int k = 0; k < kCk; ++k) {
       if (k < n) {
@@ -434,30 +484,75 @@ __global__ __launch_bounds__(kScanThreads) void scan_bwd_f64(const double* gates
 #pragma unroll
     for (int k = kCk - 1; k >= 0; --k) {
       if (k < n) {
-        const int t = t0 + k;
+        const int t = g0 + k;
         const double c = cs[k + 1], cprev = cs[k], tc = tanh(c);
         double d = dd[k];
         if (t == T - 1 && dh_n) d += dh_n[ch];
         double e = d * og[k] * (1.0 - tc * tc);
         if (t == T - 1 && dc_n) e += dc_n[ch];
-        G = e + fnext * G;
-        const double bb = ig[k] * gg[k];
-        const double dbb = bb >= eps ? G : 0.0;
-        const double dfp = fg[k] >= eps ? (G * cprev) * fg[k] * (1.0 - fg[k]) : 0.0;
-        const double dbq = dbb * bb;
-        double* dq = dgates + ((long long)t * B + b) * row4 + j;
-        dq[0] = dbq * (1.0 - ig[k]);
-        dq[H] = dfp;
-        dq[2 * H] = dbq * (1.0 - gg[k]);
-        dq[3 * H] = (d * tc) * og[k] * (1.0 - og[k]);
-        fnext = fmax(fg[k], eps);
-        first_f = fnext;
+        G = e + K;
+        const double ff = fmax(fg[k], eps);
+        if (kWrite) {
+          const double bb = ig[k] * gg[k];
+          const double dbb = bb >= eps ? G : 0.0;
+          const double dfp = fg[k] >= eps ? (G * cprev) * fg[k] * (1.0 - fg[k]) : 0.0;
+          const double dbq = dbb * bb;
+          double* dq = dgates + ((long long)t * B + b) * row4 + j;
+          dq[0] = dbq * (1.0 - ig[k]);
+          dq[H] = dfp;
+          dq[2 * H] = dbq * (1.0 - gg[k]);
+          dq[3 * H] = (d * tc) * og[k] * (1.0 - og[k]);
+        } else {
+          Fa *= ff;
+        }
+        K = ff * G;
       }
     }
   }
-  if (dc0) {
+}
+
+// Backward pass 1: chunk p >= 1 composes to K_out = Fa K_in + Kz, kept in ka[p], kb[p].
+__global__ __launch_bounds__(kScanThreads) void scan_bwd_compose_f64(const double* gates, const double* cck,
+                                                                     const double* dout, const double* dh_n,
+                                                                     const double* dc_n, double eps, double* ka,
+                                                                     double* kb, int T, int B, int H, int L,
+                                                                     int P) {
+  const long long ch = blockIdx.x * (long long)kScanThreads + threadIdx.x, C = (long long)B * H;
+  const int p = blockIdx.y;
+  if (ch >= C || p < 1 || p >= P) return;
+  double K = 0.0, G = 0.0, Fa = 1.0;
+  bwd_chunk<false>(gates, cck, dout, dh_n, dc_n, eps, nullptr, p * L, min(T, (p + 1) * L), T, B, H, ch, K, G, Fa);
+  ka[(long long)p * C + ch] = Fa;
+  kb[(long long)p * C + ch] = K;
+}
+
+// Backward pass 2: K entering chunk p from above (0 for the last chunk), in kin[p].
+__global__ __launch_bounds__(kScanThreads) void scan_bwd_carry_f64(const double* ka, const double* kb, double* kin,
+                                                                   int B, int H, int P) {
+  const long long ch = blockIdx.x * (long long)kScanThreads + threadIdx.x, C = (long long)B * H;
+  if (ch >= C) return;
+  double K = 0.0;
+  for (int p = P - 1; p >= 0; --p) {
+    kin[(long long)p * C + ch] = K;
+    if (p >= 1) K = fma(ka[(long long)p * C + ch], K, kb[(long long)p * C + ch]);
+  }
+}
+
+// Backward pass 3 (the whole scan when P = 1, kin = nullptr): dgates of chunk p; chunk 0
+// also gives dc0 = G_0 f~_0 [c0 >= eps].
+__global__ __launch_bounds__(kScanThreads) void scan_bwd_f64(const double* gates, const double* c0,
+                                                             const double* cck, const double* dout,
+                                                             const double* dh_n, const double* dc_n, double eps,
+                                                             const double* kin, double* dgates, double* dc0, int T,
+                                                             int B, int H, int L) {
+  const long long ch = blockIdx.x * (long long)kScanThreads + threadIdx.x, C = (long long)B * H;
+  if (ch >= C) return;
+  const int p = blockIdx.y;
+  double K = kin ? kin[(long long)p * C + ch] : 0.0, G = 0.0, Fa = 1.0;
+  bwd_chunk<true>(gates, cck, dout, dh_n, dc_n, eps, dgates, p * L, min(T, (p + 1) * L), T, B, H, ch, K, G, Fa);
+  if (p == 0 && dc0) {
     const bool pass = (c0 ? c0[ch] : 0.0) >= eps;
-    dc0[ch] = (pass && T > 0) ? G * first_f : 0.0;
+    dc0[ch] = pass ? K : 0.0;  // K = f~_0 G_0
   }
 }
 
@@ -499,6 +594,9 @@ size_t carve_rec64(void* base, size_t cap, int T, int B, int D, int H, bool bwd,
 struct ParF64Ws {
   double* dg;    // [T][B][4H]
   double* part;  // split-K partials and the column sum's chunks
+  double* ka;    // [P][B*H] the scan chunks' composed maps and carries
+  double* kb;
+  double* kin;
 };
 
 size_t carve_par64(void* base, size_t cap, int T, int B, int D, int H, ParF64Ws* o) {
@@ -508,6 +606,11 @@ size_t carve_par64(void* base, size_t cap, int T, int B, int D, int H, ParF64Ws*
   size_t np = max(part_elems(N4, D, TB), part_elems(TB, D, N4));
   np = max(np, (size_t)col_chunks(TB) * N4);
   o->part = c.take<double>(np);
+  const long long C = (long long)B * H;
+  const size_t pc = (size_t)scan_chunks(T, scan_chunk_len(T, C)) * C;
+  o->ka = c.take<double>(pc);
+  o->kb = c.take<double>(pc);
+  o->kin = c.take<double>(pc);
   return c.off;
 }
 
@@ -627,8 +730,18 @@ int hsl_par_fwd_f64(const double* x, const double* c0, const double* w_ih, const
   if (!x || !w_ih || !b_ih || !gates || !out || !c_ck) return fail(HSL_ERR_ARG, "hsl_par_fwd_f64: null pointer");
   HSL_CHECK(gemm64(G64{x, w_ih, b_ih, gates, (long long)T * B, 4ll * H, D, D, 1, 1, D, 4ll * H}, s));
   const long long C = (long long)B * H;
-  hipLaunchKernelGGL(scan_fwd_f64, dim3((unsigned)((C + kScanThreads - 1) / kScanThreads)), dim3(kScanThreads), 0, s,
-                     gates, c0, eps, out, c_ck, T, B, H);
+  const int L = scan_chunk_len(T, C), P = scan_chunks(T, L);
+  if (P > 65535) return fail(HSL_ERR_UNSUPPORTED, "hsl_par_fwd_f64: %d scan chunks", P);
+  const unsigned gx = (unsigned)((C + kScanThreads - 1) / kScanThreads);
+  if (P > 1) {  // 2P - 1 <= T rows of out hold the chunk maps until the last pass
+    hipLaunchKernelGGL(scan_fwd_compose_f64, dim3(gx, (unsigned)(P - 1)), dim3(kScanThreads), 0, s, gates, eps, out, T,
+                       B, H, L, P);
+    HSL_HIP(hipGetLastError());
+    hipLaunchKernelGGL(scan_fwd_carry_f64, dim3(gx), dim3(kScanThreads), 0, s, c0, eps, out, c_ck, B, H, L, P);
+    HSL_HIP(hipGetLastError());
+  }
+  hipLaunchKernelGGL(scan_fwd_f64, dim3(gx, (unsigned)P), dim3(kScanThreads), 0, s, gates, c0, eps, out, c_ck, T, B, H,
+                     L);
   HSL_HIP(hipGetLastError());
   return HSL_OK;
 }
@@ -659,8 +772,18 @@ int hsl_par_bwd_f64(const double* dout, const double* dh_n, const double* dc_n, 
   }
   if (!dout || !x || !gates || !c_ck) return fail(HSL_ERR_ARG, "hsl_par_bwd_f64: null pointer");
   const long long C = (long long)B * H;
-  hipLaunchKernelGGL(scan_bwd_f64, dim3((unsigned)((C + kScanThreads - 1) / kScanThreads)), dim3(kScanThreads), 0, s,
-                     gates, c0, c_ck, dout, dh_n, dc_n, eps, dg, dc0, T, B, H);
+  const int L = scan_chunk_len(T, C), P = scan_chunks(T, L);
+  if (P > 65535) return fail(HSL_ERR_UNSUPPORTED, "hsl_par_bwd_f64: %d scan chunks", P);
+  const unsigned gx = (unsigned)((C + kScanThreads - 1) / kScanThreads);
+  if (P > 1) {
+    hipLaunchKernelGGL(scan_bwd_compose_f64, dim3(gx, (unsigned)P), dim3(kScanThreads), 0, s, gates, c_ck, dout, dh_n,
+                       dc_n, eps, w.ka, w.kb, T, B, H, L, P);
+    HSL_HIP(hipGetLastError());
+    hipLaunchKernelGGL(scan_bwd_carry_f64, dim3(gx), dim3(kScanThreads), 0, s, w.ka, w.kb, w.kin, B, H, P);
+    HSL_HIP(hipGetLastError());
+  }
+  hipLaunchKernelGGL(scan_bwd_f64, dim3(gx, (unsigned)P), dim3(kScanThreads), 0, s, gates, c0, c_ck, dout, dh_n, dc_n,
+                     eps, P > 1 ? w.kin : nullptr, dg, dc0, T, B, H, L);
   HSL_HIP(hipGetLastError());
   const long long TB = (long long)T * B, N4 = 4ll * H;
   HSL_CHECK(gemm64_split(G64{dg, x, nullptr, dw_ih, N4, D, TB, 1, N4, D, 1, D}, w.part, s));

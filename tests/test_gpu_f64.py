@@ -84,6 +84,42 @@ def test_f64_matches_oracle(dev, parallel, shape):
     _check(*shape, dev, parallel)
 
 
+def test_f64_parallel_multi_group_chunks(dev):
+    """Parallel mode with enough channels (B*H = 65536) that the scans cut T = 70 into
+    chunks of 24 steps (three checkpoint groups); the last chunk has 22 steps.
+
+    The reference here is the linear-domain fp64 recurrence (``O.linear_scan``, pinned to
+    the log-domain scan by the oracle tests) under autograd: at this size the log-domain
+    form's own fp64 rounding differs from the linear form by 1.4x the 1e-10 tolerance on
+    db_ih (a 4480-row column sum with cancellation), while two summation orders of the
+    same dgates differ by < 0.01x."""
+    T, B, D, H = 70, 64, 8, 1024
+    print(f"fp64 parallel chunks T={T} B={B} D={D} H={H}", flush=True)
+    torch.manual_seed(9)
+    m = prlstm_amd.HeadStartLSTM(D, H, parallel=True).double()
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(T, B, D, generator=g, dtype=torch.float64)
+    c0 = torch.rand(1, B, H, generator=g, dtype=torch.float64)
+    c0[0, :, :8] = 0.0  # clamped entries of c0
+    wts = tuple(torch.randn(*s, generator=g, dtype=torch.float64) for s in ((T, B, H), (B, H), (B, H)))
+    xr = x.clone().requires_grad_(True)
+    c0r = c0.clone().requires_grad_(True)
+    w_ih = m.weight_ih_l0.detach().clone().requires_grad_(True)
+    b_ih = m.bias_ih_l0.detach().clone().requires_grad_(True)
+    gi, gf, gg, go = torch.sigmoid(torch.nn.functional.linear(xr, w_ih, b_ih)).chunk(4, dim=-1)
+    c = O.linear_scan(gf, gi * gg, c0r[0])
+    out = go * torch.tanh(c)
+    ((out * wts[0]).sum() + (out[-1] * wts[1]).sum() + (c[-1] * wts[2]).sum()).backward()
+    ref = {"out": out, "h_n": out[-1:], "c_n": c[-1:], "dx": xr.grad, "dweight_ih_l0": w_ih.grad,
+           "dbias_ih_l0": b_ih.grad, "dc0": c0r.grad}
+    r_gpu = _run(m.to(dev), x, (torch.zeros(1, B, H, dtype=torch.float64), c0), wts, dev)
+    torch.cuda.synchronize()
+    for k, v in ref.items():
+        ratio = lim_ratio(r_gpu[k], v, RTOL, ATOL)
+        print(f"  {k:16s} {ratio:.3g}x of the fp64 tolerance")
+        assert ratio <= 1.0, (k, ratio)
+
+
 @pytest.mark.parametrize("parallel", [False, True])
 def test_f64_hx_and_batch_first(dev, parallel):
     _check(20, 4, 12, 36, dev, parallel, with_hx=True, batch_first=True, seed=3)

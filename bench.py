@@ -222,8 +222,9 @@ def bench_scan(args):
 
 
 # configs[0..4] of BASELINE.json (configs[1] in both modes), the two shapes of the
-# reference's published table (README.md:73-79) that no config covers, and configs[4]
-# with the module in bf16 (16-bit input projection): (name, T, B, D, H, parallel, a, dtype)
+# reference's published table (README.md:73-79) that no config covers, configs[4] with the
+# module in bf16 (16-bit input projection), and configs[2] / configs[4] with the module in
+# fp64 (the fp64 kernels): (name, T, B, D, H, parallel, a, dtype)
 MODE_CONFIGS = [
     ("configs[0]", 32, 16, 64, 128, False, 1e-4, torch.float32),
     ("configs[1]", 128, 32, 256, 256, False, 1e-4, torch.float32),
@@ -234,6 +235,8 @@ MODE_CONFIGS = [
     ("README.md:78 shape", 64, 32, 512, 1024, False, 1e-4, torch.float32),
     ("configs[4]", 4096, 16, 256, 1024, True, 0.0, torch.float32),
     ("configs[4] bf16 module", 4096, 16, 256, 1024, True, 0.0, torch.bfloat16),
+    ("configs[2] fp64 module", 256, 32, 256, 512, False, 1e-4, torch.float64),
+    ("configs[4] fp64 module", 4096, 16, 256, 1024, True, 0.0, torch.float64),
 ]
 
 

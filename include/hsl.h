@@ -248,10 +248,11 @@ int hsl_par_bwd_b16(const void* dout, const float* dh_n, const float* dc_n,
  * and its parallel functional is dtype-generic, _parallel.py:38-74).  Every argument,
  * layout and output is that of the fp32 entry point of the same name without "_f64"
  * (hsl_rec_fwd, hsl_rec_bwd, hsl_par_fwd, hsl_par_bwd), with double for float; all
- * arithmetic is fp64.  These kernels are written for exactness, not speed: one launch
- * per time step in recurrent mode, one thread per channel for the scans and a plain
- * tiled fp64 product; every sum runs in a fixed order (deterministic results).  The
- * recurrent backward's workspace always holds the [T,B,4H] dgates. */
+ * arithmetic is fp64.  Products run on the fp64 matrix instruction (split along K into
+ * partials summed in a fixed order when the output is small), recurrent mode launches a
+ * product and a cell kernel per time step, and the parallel scans run time-chunked in
+ * three passes; every sum runs in a fixed order (deterministic results).  The recurrent
+ * backward's workspace always holds the [T,B,4H] dgates. */
 size_t hsl_rec_fwd_f64_ws_bytes(int T, int B, int D, int H);
 int hsl_rec_fwd_f64(const double* x, const double* h0, const double* c0,
                     const double* w_ih, const double* w_hh, const double* b_ih,

@@ -55,6 +55,14 @@ def test_workspace_queries():
     assert lib.hsl_rec_fwd_ws_bytes(-1, 1, 1, 1) == 0
     assert lib.hsl_gemm_ws_bytes(2048, 512, 8192) > 0   # split-K for a long reduction
     assert lib.hsl_gemm_ws_bytes(8192, 2048, 256) == 0  # enough tiles: no split
+    # fp64 modules: the recurrent workspaces hold the [T,B,4H] gates / dgates in fp64, the
+    # parallel backward's its dgates; negative sizes give 0
+    T, B, D, H = 256, 32, 256, 512
+    assert lib.hsl_rec_fwd_f64_ws_bytes(T, B, D, H) >= T * B * 4 * H * 8
+    assert lib.hsl_rec_bwd_f64_ws_bytes(T, B, D, H) >= T * B * 4 * H * 8
+    assert lib.hsl_par_bwd_f64_ws_bytes(4096, 16, 256, 1024) >= 4096 * 16 * 4 * 1024 * 8
+    for f in (lib.hsl_rec_fwd_f64_ws_bytes, lib.hsl_rec_bwd_f64_ws_bytes, lib.hsl_par_bwd_f64_ws_bytes):
+        assert f(-1, 1, 1, 1) == 0
     # parallel mode keeps c every 8th step: ceil(T/8) carry-in rows, then c_n
     for T, rows in ((1, 2), (7, 2), (8, 2), (9, 3), (128, 17), (4096, 513), (0, 1), (-1, 0)):
         assert lib.hsl_scan_ck_rows(T) == rows, (T, lib.hsl_scan_ck_rows(T))
@@ -68,6 +76,14 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert rc == 1 and b"leading dimension" in lib.hsl_last_error()
     with pytest.raises(RuntimeError, match="hsl_rec_fwd failed"):
         _lib.call("hsl_rec_fwd", *([None] * 12), None, 0, 1, 1, 1, 1, None)
+    # the fp64 entry points refuse null operands before any launch
+    for name, args in (
+            ("hsl_rec_fwd_f64", [None] * 13 + [0, 4, 2, 3, 5, None]),
+            ("hsl_rec_bwd_f64", [None] * 21 + [0, 4, 2, 3, 5, None]),
+            ("hsl_par_fwd_f64", [None] * 4 + [1e-6] + [None] * 3 + [4, 2, 3, 5, None]),
+            ("hsl_par_bwd_f64", [None] * 8 + [1e-6] + [None] * 5 + [0, 4, 2, 3, 5, None])):
+        assert getattr(lib, name)(*args) == 1, name
+        assert b"null pointer" in lib.hsl_last_error(), (name, lib.hsl_last_error())
 
 
 @pytest.mark.parametrize("T,B,D,H,why", [
@@ -89,6 +105,12 @@ def test_shapes_beyond_32_bit_indexing_are_rejected(T, B, D, H, why):
         "hsl_par_fwd": lambda: lib.hsl_par_fwd(None, None, None, None, 1e-6, None, None, None, T, B, D, H, None),
         "hsl_par_bwd": lambda: lib.hsl_par_bwd(*([None] * 8), 1e-6, None, None, None, None, None, 0,
                                                T, B, D, H, None),
+        "hsl_rec_fwd_f64": lambda: lib.hsl_rec_fwd_f64(*([None] * 13), 0, T, B, D, H, None),
+        "hsl_rec_bwd_f64": lambda: lib.hsl_rec_bwd_f64(*([None] * 21), 0, T, B, D, H, None),
+        "hsl_par_fwd_f64": lambda: lib.hsl_par_fwd_f64(None, None, None, None, 1e-6, None, None, None,
+                                                       T, B, D, H, None),
+        "hsl_par_bwd_f64": lambda: lib.hsl_par_bwd_f64(*([None] * 8), 1e-6, None, None, None, None, None, 0,
+                                                       T, B, D, H, None),
     }
     if D == 8:  # the scan entry points take no D
         calls["hsl_scan_fwd"] = lambda: lib.hsl_scan_fwd(None, None, 1e-6, None, None, T, B, H, None)

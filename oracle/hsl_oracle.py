@@ -200,8 +200,8 @@ def linear_scan(f, b, c0, eps=EPS):
     fc = torch.clamp(f, min=eps)
     bc = torch.clamp(b, min=eps)
     out = []
-    for t in range(f.shape[0]):
-        c = fc[t] * c + bc[t]
+    for ft, bt in zip(fc.unbind(0), bc.unbind(0)):  # unbind: one stacked gradient in backward
+        c = ft * c + bt
         out.append(c)
     return torch.stack(out, 0)
 

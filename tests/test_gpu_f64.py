@@ -178,3 +178,38 @@ def test_f64_gradcheck(dev, parallel):
     fn = functional.headstartlstm_parallel if parallel else functional.headstartlstm_recurrent
     assert torch.autograd.gradcheck(lambda *args: fn(*args), (x, h0, c0, w_ih, w_hh, b_ih, b_hh, a),
                                     eps=1e-6, atol=1e-7, rtol=1e-5)
+
+
+def test_f64_config4_full_size(dev):
+    """configs[4] (T4096 B16 D256 H1024) as an fp64 module: the full step (16 scan chunks
+    of 256 steps, the projection and dW_ih on split K over T*B = 65536 rows) against fp64
+    autograd of the linear-domain recurrence (``O.linear_scan``) on the CPU, every element
+    of every output and gradient.  dW_ih and db_ih are sums of 65536 products, whose
+    rounding in any order is about sqrt(K) u rms(term) ~ 1e-12, hence atol 1e-9 for them;
+    the other outputs keep atol 1e-12."""
+    T, B, D, H = 4096, 16, 256, 1024
+    print(f"fp64 configs[4] T={T} B={B} D={D} H={H}", flush=True)
+    torch.manual_seed(0)
+    m = prlstm_amd.HeadStartLSTM(D, H, a_init=0.0, parallel=True).double()
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(T, B, D, generator=g, dtype=torch.float64)
+    c0 = torch.rand(1, B, H, generator=g, dtype=torch.float64)
+    wts = tuple(torch.randn(*s, generator=g, dtype=torch.float64) for s in ((T, B, H), (B, H), (B, H)))
+    xr = x.clone().requires_grad_(True)
+    c0r = c0.clone().requires_grad_(True)
+    w_ih = m.weight_ih_l0.detach().clone().requires_grad_(True)
+    b_ih = m.bias_ih_l0.detach().clone().requires_grad_(True)
+    gi, gf, gg, go = torch.sigmoid(torch.nn.functional.linear(xr, w_ih, b_ih)).chunk(4, dim=-1)
+    c = O.linear_scan(gf, gi * gg, c0r[0])
+    out = go * torch.tanh(c)
+    ((out * wts[0]).sum() + (out[-1] * wts[1]).sum() + (c[-1] * wts[2]).sum()).backward()
+    ref = {"out": out, "h_n": out[-1:], "c_n": c[-1:], "dx": xr.grad, "dweight_ih_l0": w_ih.grad,
+           "dbias_ih_l0": b_ih.grad, "dc0": c0r.grad}
+    del gi, gf, gg, go, c
+    r_gpu = _run(m.to(dev), x, (torch.zeros(1, B, H, dtype=torch.float64), c0), wts, dev)
+    torch.cuda.synchronize()
+    for k, v in ref.items():
+        atol = 1e-9 if k in ("dweight_ih_l0", "dbias_ih_l0") else ATOL
+        ratio = lim_ratio(r_gpu[k], v, RTOL, atol)
+        print(f"  {k:16s} {ratio:.3g}x of the fp64 tolerance", flush=True)
+        assert ratio <= 1.0, (k, ratio)

@@ -35,7 +35,7 @@ def _run(m, x, hx, wts, dev=None):
     return res
 
 
-def _check(T, B, D, H, dev, parallel, with_hx=False, batch_first=False, seed=0):
+def _check(T, B, D, H, dev, parallel, with_hx=False, batch_first=False, seed=0, sum_atol=ATOL):
     print(f"fp64 T={T} B={B} D={D} H={H} parallel={parallel} hx={with_hx} bf={batch_first}", flush=True)
     torch.manual_seed(seed)
     ref = O.RefHeadStartLSTM(D, H, batch_first=batch_first, parallel=parallel).double()
@@ -60,7 +60,8 @@ def _check(T, B, D, H, dev, parallel, with_hx=False, batch_first=False, seed=0):
         if v is None:  # the reference's dh0/dc0 (recurrent mode returns None for them)
             continue
         assert r_gpu[k].dtype == torch.float64, k
-        ratio = lim_ratio(r_gpu[k], v, RTOL, ATOL)
+        # parameter gradients are sums over all T*B rows: sum_atol for long ones
+        ratio = lim_ratio(r_gpu[k], v, RTOL, sum_atol if k.startswith(("dweight", "dbias", "da")) else ATOL)
         print(f"  {k:16s} {ratio:.3g}x of the fp64 tolerance")
         assert ratio <= 1.0, (k, ratio)
     if with_hx and not parallel:  # dh0/dc0 against fp64 autograd of the textbook LSTM
@@ -82,6 +83,13 @@ SHAPES = [(12, 3, 16, 24), (37, 5, 9, 70), (1, 1, 1, 1), (130, 2, 8, 40)]
 @pytest.mark.parametrize("shape", SHAPES)
 def test_f64_matches_oracle(dev, parallel, shape):
     _check(*shape, dev, parallel)
+
+
+def test_f64_config2_full_size(dev):
+    """configs[2] (T256 B32 D256 H512) as an fp64 module in recurrent mode, every element
+    against the fp64 oracle, with hx and a ~ (0.3, 0.2, 0.4, 0.1).  The parameter gradients
+    sum 8192 rows (sqrt(K) u rms(term) rounding in any order), hence atol 1e-9 for them."""
+    _check(256, 32, 256, 512, dev, False, with_hx=True, seed=21, sum_atol=1e-9)
 
 
 def test_f64_parallel_multi_group_chunks(dev):

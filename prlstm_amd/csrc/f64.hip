@@ -324,22 +324,27 @@ int colsum64(const double* dg, double* part, double* db, long long R, int N, hip
   return HSL_OK;
 }
 
-// dW_hh = a dW_hh_s, db_ih = db, db_hh = a db; rowdot[n] = W_hh[n].dW_hh_s[n] + b_hh[n] db[n]
-__global__ void rec_final_rows_f64(const double* w_hh, const double* b_hh, const double* a, const double* dws,
-                                   const double* db, double* dw_hh, double* db_ih, double* db_hh, double* rowdot,
-                                   int H) {
-  const int n = blockIdx.x * 256 + threadIdx.x;
-  if (n >= 4 * H) return;
+// dW_hh = a dW_hh_s, db_ih = db, db_hh = a db; rowdot[n] = W_hh[n].dW_hh_s[n] + b_hh[n] db[n].
+// One wave per row n: lane l adds k = l, l+64, ... in order, then the 64 lane sums are
+// added by a fixed butterfly (deterministic).
+__global__ __launch_bounds__(64) void rec_final_rows_f64(const double* w_hh, const double* b_hh, const double* a,
+                                                         const double* dws, const double* db, double* dw_hh,
+                                                         double* db_ih, double* db_hh, double* rowdot, int H) {
+  const int n = blockIdx.x, l = threadIdx.x;
   const double ag = a[n / H];
   double acc = 0.0;
-  for (int k = 0; k < H; ++k) {
+  for (int k = l; k < H; k += 64) {
     const long long e = (long long)n * H + k;
     dw_hh[e] = ag * dws[e];
     acc = fma(w_hh[e], dws[e], acc);
   }
-  rowdot[n] = acc + (b_hh ? b_hh[n] * db[n] : 0.0);
-  db_ih[n] = db[n];
-  db_hh[n] = ag * db[n];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (l == 0) {
+    rowdot[n] = acc + (b_hh ? b_hh[n] * db[n] : 0.0);
+    db_ih[n] = db[n];
+    db_hh[n] = ag * db[n];
+  }
 }
 
 // da[g] = sum of rowdot over the gate's H rows, in increasing row (one thread per gate)
@@ -714,7 +719,7 @@ int hsl_rec_bwd_f64(const double* dout, const double* dh_n, const double* dc_n, 
   HSL_CHECK(gemm64_split(G64{w.big, x, nullptr, dw_ih, N4, D, TB, 1, N4, D, 1, D}, w.part, s));
   if (dx) HSL_CHECK(gemm64_split(G64{w.big, w_ih, nullptr, dx, TB, D, N4, N4, 1, D, 1, D}, w.part, s));
   HSL_CHECK(colsum64(w.big, w.part, w.db, TB, (int)N4, s));
-  hipLaunchKernelGGL(rec_final_rows_f64, dim3(blocks_for(N4)), dim3(256), 0, s, w_hh, b_hh, a, w.dws, w.db, dw_hh,
+  hipLaunchKernelGGL(rec_final_rows_f64, dim3((unsigned)N4), dim3(64), 0, s, w_hh, b_hh, a, w.dws, w.db, dw_hh,
                      db_ih, db_hh, w.rowdot, H);
   HSL_HIP(hipGetLastError());
   hipLaunchKernelGGL(rec_da_f64, dim3(1), dim3(64), 0, s, w.rowdot, da, H);

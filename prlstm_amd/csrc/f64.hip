@@ -31,8 +31,9 @@ __device__ __forceinline__ double sig64(double z) { return 1.0 / (1.0 + exp(-z))
 // C[m][n] = (bias ? bias[n] : 0) + sum_k A(m,k) B(k,n), A(m,k) = A[m*sam + k*sak],
 // B(k,n) = B[k*sbk + n*sbn], C row-major with ldc.  64x64 output tiles on 4 waves (a 32x32
 // quarter each, 2x2 blocks of the fp64 matrix instruction 16x16x4), 16-deep k-slices
-// through LDS (loaded along whichever index is contiguous in memory); every output takes
-// its k terms in increasing groups of four, one instruction per group.
+// through LDS (loaded along whichever index is contiguous in memory, the next slice into
+// registers while the current one is multiplied); every output takes its k terms in
+// increasing groups of four, one instruction per group.
 // Split K: workgroup z covers k in [z*kc, min(K, (z+1)*kc)) and writes C + z*pst, so
 // each split leaves a partial product that a fixed-order sum adds afterwards.
 struct G64 {
@@ -62,18 +63,35 @@ __global__ __launch_bounds__(256) void gemm_f64_kernel(G64 g) {
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = d4_t{0.0, 0.0, 0.0, 0.0};
+  // this thread's 4 + 4 operand elements of a slice: LDS places and global offsets
+  int am[4], ak[4], bn[4], bk[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int e = tid + 256 * r;
+    am[r] = a_kc ? e >> 4 : e & 63;
+    ak[r] = a_kc ? e & 15 : e >> 6;
+    bn[r] = b_nc ? e & 63 : e >> 4;
+    bk[r] = b_nc ? e >> 6 : e & 15;
+  }
+  double ra[4], rb[4];  // the next slice, loaded while the current one is multiplied
+  auto load_slice = [&](long long k0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const long long m = m0 + am[r], ka = k0 + ak[r];
+      ra[r] = (m < g.M && ka < kend) ? g.A[m * g.sam + ka * g.sak] : 0.0;
+      const long long n = n0 + bn[r], kb = k0 + bk[r];
+      rb[r] = (kb < kend && n < g.N) ? g.Bm[kb * g.sbk + n * g.sbn] : 0.0;
+    }
+  };
+  if (kb0 < kend) load_slice(kb0);
   for (long long k0 = kb0; k0 < kend; k0 += 16) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int e = tid + 256 * r;
-      const int am = a_kc ? e >> 4 : e & 63, ak = a_kc ? e & 15 : e >> 6;
-      const long long m = m0 + am, ka = k0 + ak;
-      As[ak][am] = (m < g.M && ka < kend) ? g.A[m * g.sam + ka * g.sak] : 0.0;
-      const int bn = b_nc ? e & 63 : e >> 4, bk = b_nc ? e >> 6 : e & 15;
-      const long long n = n0 + bn, kb = k0 + bk;
-      Bs[bk][bn] = (kb < kend && n < g.N) ? g.Bm[kb * g.sbk + n * g.sbn] : 0.0;
+      As[ak[r]][am[r]] = ra[r];
+      Bs[bk[r]][bn[r]] = rb[r];
     }
     __syncthreads();
+    if (k0 + 16 < kend) load_slice(k0 + 16);
     // v_mfma_f64_16x16x4: lane l holds A[l%16][l/16] and B[l/16][l%16] of a 16x16x4 step
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {

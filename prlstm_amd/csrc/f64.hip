@@ -365,13 +365,15 @@ __global__ __launch_bounds__(64) void rec_final_rows_f64(const double* w_hh, con
   }
 }
 
-// da[g] = sum of rowdot over the gate's H rows, in increasing row (one thread per gate)
-__global__ void rec_da_f64(const double* rowdot, double* da, int H) {
-  const int g = threadIdx.x;
-  if (g >= 4) return;
+// da[g] = sum of rowdot over the gate's H rows: one wave per gate, lane l adds rows
+// u = l, l+64, ... in order, then a fixed butterfly adds the 64 lane sums.
+__global__ __launch_bounds__(64) void rec_da_f64(const double* rowdot, double* da, int H) {
+  const int g = blockIdx.x, l = threadIdx.x;
   double acc = 0.0;
-  for (int u = 0; u < H; ++u) acc += rowdot[(long long)g * H + u];
-  da[g] = acc;
+  for (int u = l; u < H; u += 64) acc += rowdot[(long long)g * H + u];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (l == 0) da[g] = acc;
 }
 
 // Parallel-mode scans, one thread per (channel, time chunk).  T is cut into P chunks of L
@@ -740,7 +742,7 @@ int hsl_rec_bwd_f64(const double* dout, const double* dh_n, const double* dc_n, 
   hipLaunchKernelGGL(rec_final_rows_f64, dim3((unsigned)N4), dim3(64), 0, s, w_hh, b_hh, a, w.dws, w.db, dw_hh,
                      db_ih, db_hh, w.rowdot, H);
   HSL_HIP(hipGetLastError());
-  hipLaunchKernelGGL(rec_da_f64, dim3(1), dim3(64), 0, s, w.rowdot, da, H);
+  hipLaunchKernelGGL(rec_da_f64, dim3(4), dim3(64), 0, s, w.rowdot, da, H);
   HSL_HIP(hipGetLastError());
   return HSL_OK;
 }
@@ -756,7 +758,9 @@ int hsl_par_fwd_f64(const double* x, const double* c0, const double* w_ih, const
   const int L = scan_chunk_len(T, C), P = scan_chunks(T, L);
   if (P > 65535) return fail(HSL_ERR_UNSUPPORTED, "hsl_par_fwd_f64: %d scan chunks", P);
   const unsigned gx = (unsigned)((C + kScanThreads - 1) / kScanThreads);
-  if (P > 1) {  // 2P - 1 <= T rows of out hold the chunk maps until the last pass
+  // rows [0, 2P-1) of out hold the chunk maps until the last pass (L >= 8 keeps 2P-1 <= T)
+  if (P > 1 && 2ll * P - 1 > T) return fail(HSL_ERR_UNSUPPORTED, "hsl_par_fwd_f64: %d scan chunks", P);
+  if (P > 1) {
     hipLaunchKernelGGL(scan_fwd_compose_f64, dim3(gx, (unsigned)(P - 1)), dim3(kScanThreads), 0, s, gates, eps, out, T,
                        B, H, L, P);
     HSL_HIP(hipGetLastError());

@@ -79,7 +79,8 @@ def measured_traffic(kernel):
 
 
 def make_inputs():
-    """configs[2] synthetic inputs (SURVEY 8(d) recipe): seed 0, module on CPU, then x."""
+    """configs[2] synthetic inputs: seed 0, the module built on the CPU (a = 1e-4), then
+    x ~ N(0, 1) of shape [T, B, D] drawn from the same generator."""
     from prlstm_amd import HeadStartLSTM
     torch.manual_seed(0)
     m = HeadStartLSTM(D, H, a_init=1e-4)
